@@ -1,0 +1,262 @@
+"""Benchmark of the paged-KV hot path on one MI355X.
+
+Default workload: Llama-3-8B-shaped GQA decode across all
+32 layers, batch 64, 32 query / 8 KV heads, head_dim 128, 16-token pages,
+context lengths log-uniform in [512, 8192], physical pages shuffled across
+the pool, float32 K/V/Q ~ N(0, 1).  One step = reserve one slot per sequence,
+then per layer: append the current K/V token into its page and run paged
+decode attention over the pre-step history plus that uncommitted tail.
+
+Printed JSON line: ``value`` is the whole step's algorithmic bytes (decode
+attention + append, all layers) divided by the wall time of a step.  The
+``roofline`` object is the decode attention kernel's own rate, timed with HIP
+events on the stream the kernels run on.  ``cpu_baseline`` times the CPU
+oracle (the C++ restatement of the reference's CPU paged attention) on a
+bounded sample of the same workload on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import helix_runtime_amd as hx  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+LAYERS, HQ, HKV, D, P, BATCH = 32, 32, 8, 128, 16, 64
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_bytes(lengths, hq=HQ, hkv=HKV, d=D, p=P):
+    """Algorithmic HBM bytes of one decode-attention launch (one layer):
+    sum over sequences of K+V history (each byte once per KV head), the K/V
+    tail, Q in and O out, and the block-table entries."""
+    lengths = np.asarray(lengths, np.int64)
+    return int(np.sum(2 * hkv * lengths * d * 4 + 2 * hkv * d * 4 + 2 * hq * d * 4 +
+                      ((lengths + p - 1) // p) * 4))
+
+
+def append_bytes(batch, hkv=HKV, d=D):
+    """Read source + write page, keys and values, one token per sequence."""
+    return 2 * 2 * hkv * d * 4 * batch
+
+
+def build_workload(seed, batch, layers, steps_total):
+    rng = np.random.default_rng(seed)
+    lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=batch)).astype(np.int64)
+    pages = (lengths + P - 1) // P
+    grow = (steps_total + P) // P + 1
+    n_phys = int(pages.sum() + batch * grow + 16)
+    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys)
+    log(f"pool: {n_phys} blocks x {layers} layers ({n_phys * layers * 2 * HKV * P * D * 4 / 1e9:.1f} GB)")
+    # Shuffle the free queue: allocate every block once, release in a seeded
+    # random order, so later allocations scatter each sequence over the pool.
+    tok = torch.zeros(layers, HKV, D, device="cuda:0")
+    dummies = []
+    for _ in range(n_phys):
+        s = cache.create_sequence()
+        cache.append(s, tok, tok)
+        dummies.append(s)
+    for i in rng.permutation(n_phys):
+        cache.release_sequence(dummies[int(i)])
+    # Fill the histories with N(0, 1) data in one bulk append per sequence.
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(seed)
+    src_elems = HKV * int(lengths.max()) * D
+    src_k = torch.randn(layers, src_elems + 4096, device="cuda:0", generator=gen)
+    src_v = torch.randn(layers, src_elems + 4096, device="cuda:0", generator=gen)
+    seqs = []
+    for b in range(batch):
+        s = cache.create_sequence()
+        n = int(lengths[b])
+        off = int(rng.integers(0, 1024)) * 4
+        lk = [src_k[l, off: off + HKV * n * D].view(HKV, n, D) for l in range(layers)]
+        lv = [src_v[l, off: off + HKV * n * D].view(HKV, n, D) for l in range(layers)]
+        cache.append_layer_major(s, lk, lv)
+        seqs.append(s)
+    del src_k, src_v
+    torch.cuda.empty_cache()
+    return cache, seqs, lengths
+
+
+def cpu_baseline(cache, seqs, layers_sample, threads, seed):
+    """Times the CPU oracle (C++ restatement of the reference CPU paged
+    attention, fp64 accumulation) on `layers_sample` layers x all sequences."""
+    import oracle
+
+    rng = np.random.default_rng(seed + 7)
+    batch = len(seqs)
+    tables_list = [cache.block_table(s) for s in seqs]
+    lengths = np.array([cache.length(s) for s in seqs], np.int32)
+    max_blocks = max(len(t) for t in tables_list)
+    tables = np.zeros((batch, max_blocks), np.uint32)
+    for b, t in enumerate(tables_list):
+        tables[b, : len(t)] = t
+    total_bytes, total_time, max_err = 0, 0.0, 0.0
+    for layer in range(layers_sample):
+        kp, vp = (x.cpu().numpy() for x in cache.layer_pools(layer))
+        q = rng.standard_normal((batch, HQ, D), dtype=np.float32)
+        tk = rng.standard_normal((batch, HKV, D), dtype=np.float32)
+        tv = rng.standard_normal((batch, HKV, D), dtype=np.float32)
+        t0 = time.perf_counter()
+        ref = oracle.batched_decode(q, kp, vp, tables, lengths, tk, tv, threads=threads)
+        total_time += time.perf_counter() - t0
+        total_bytes += decode_bytes(lengths)
+        # Full-size parity of the GPU kernel on the same inputs.
+        dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")  # noqa: E731
+        out = torch.empty(batch, HQ, D, device="cuda:0")
+        ws = torch.empty(hx.decode_workspace_bytes(batch, HQ, max_blocks) // 4 + 1,
+                         device="cuda:0")
+        kpool, vpool = cache.layer_pool_pointers(layer)
+        hx.paged_decode_attention(dv(q), kpool, vpool, dv(tables.astype(np.int32)), dv(lengths),
+                                  dv(tk), dv(tv), out, ws,
+                                  pool_shape=(cache.physical_blocks, HKV, P, D))
+        torch.cuda.synchronize()
+        diff = np.abs(out.cpu().numpy() - ref)
+        tol = 2e-5 + 1e-4 * np.abs(ref)
+        max_err = max(max_err, float(diff.max()))
+        if not (diff <= tol).all():
+            raise SystemExit(f"parity failure on layer {layer}: max abs err {diff.max()}")
+        del kp, vp
+    return total_bytes / total_time / 1e9, total_time, max_err
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--pages-per-split", type=int, default=0)
+    ap.add_argument("--cpu-layers", type=int, default=2)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the paged-KV "
+              "hot path shards by KV head or by sequence with no exchange; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    torch.cuda.set_device(0)
+    steps_total = args.warmup + args.steps + 2
+    t_setup = time.perf_counter()
+    cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total)
+    log(f"setup {time.perf_counter() - t_setup:.1f}s; mean context {lengths0.mean():.0f}")
+
+    batch = hx.DecodeBatch(cache, seqs, HQ, max_tokens=int(lengths0.max()) + steps_total + P,
+                           pages_per_split=args.pages_per_split)
+    split = batch.device_state()["pages_per_split"]
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(args.seed + 1)
+    L = args.layers
+    q = torch.randn(L, BATCH, HQ, D, device="cuda:0", generator=gen)
+    k = torch.randn(L, BATCH, HKV, D, device="cuda:0", generator=gen)
+    v = torch.randn(L, BATCH, HKV, D, device="cuda:0", generator=gen)
+    out = torch.empty(L, BATCH, HQ, D, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(L)]
+          for _ in range(args.steps)]
+
+    def step(events):
+        batch.prepare(stream)
+        for l in range(L):
+            if events is not None:
+                events[l][0].record(stream)
+            batch.append_layer(l, k[l], v[l], stream)
+            if events is not None:
+                events[l][1].record(stream)
+            batch.attention_layer(l, q[l], k[l], v[l], out[l], stream)
+            if events is not None:
+                events[l][2].record(stream)
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    append_ms = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(args.steps) for l in range(L)]
+    attn_ms = [ev[i][l][1].elapsed_time(ev[i][l][2]) for i in range(args.steps) for l in range(L)]
+
+    # History of timed step i is the initial length plus the tokens of the
+    # warmup and earlier timed steps.
+    per_step_decode = [decode_bytes(lengths0 + args.warmup + i) for i in range(args.steps)]
+    launch_bytes = float(np.mean(per_step_decode))
+    step_decode = launch_bytes * L
+    step_append = append_bytes(BATCH) * L
+    value = (step_decode + step_append) / (ms_per_step * 1e-3) / 1e9
+    attn_avg_ms = float(np.mean(attn_ms))
+    append_avg_ms = float(np.mean(append_ms))
+    achieved = launch_bytes / (attn_avg_ms * 1e-3) / 1e9
+    append_gbps = append_bytes(BATCH) / (append_avg_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_config3_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        gbps, secs, err = cpu_baseline(cache, seqs, args.cpu_layers, threads, args.seed)
+        cpu = {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"CPU oracle (C++ restatement of the reference CPU paged attention, "
+                         f"fp64 accumulation) on {args.cpu_layers} of {L} layers x all {BATCH} "
+                         f"sequences, {secs:.1f} s; GPU kernel matched it to max abs err "
+                         f"{err:.2e} on those layers"}
+
+    line = {
+        "metric": "paged decode attn GB/s (% of HBM peak) + append GB/s, 8B-GQA batch 64",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic N(0,1) K/V/Q, seeded; pages shuffled across the pool",
+        "config": {"workload": "config3: Llama-3-8B GQA decode, 32 layers, batch 64, "
+                               "32q/8kv heads, head_dim 128, page 16, ctx log-uniform [512, 8192]",
+                   "batch": BATCH, "layers": L, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "block_tokens": P, "mean_context": float(lengths0.mean()),
+                   "pages_per_split": split},
+        "decode_attn_gbps": round(achieved, 2),
+        "decode_attn_hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "append_gbps": round(append_gbps, 2),
+        "append_avg_us": round(append_avg_ms * 1e3, 2),
+        "decode_avg_us": round(attn_avg_ms * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    batch.close()
+    cache.close()
+
+
+if __name__ == "__main__":
+    main()

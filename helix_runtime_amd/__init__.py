@@ -1,0 +1,466 @@
+"""MI355X-native paged-KV hot path of helix-runtime.
+
+Python front end over the C ABI in ``include/helix_paged.h``.  The names and
+argument meaning follow the reference's C++ interface
+(``include/helix/kv_cache/cuda_paged.hpp``, ``include/helix/kv_cache/paged.hpp``,
+``include/helix/attention/cuda_paged.hpp``); errors surface as
+:class:`HelixError` carrying the reference's error code.  PyTorch is used
+only for device memory and streams: every computation runs in the HIP
+kernels of ``libhelix_paged.so``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+from . import _native
+from ._native import (HelixError, Sequence, INVALID_ARGUMENT, OUT_OF_RANGE, UNSUPPORTED,
+                      RESOURCE_EXHAUSTED, RUNTIME, INTERNAL, check)
+
+__all__ = [
+    "build", "load", "HelixError", "Sequence", "BlockManager", "PagedKvCache", "DecodeBatch",
+    "PagedBlockTable", "paged_attention_out", "paged_attention_with_tail_out",
+    "paged_decode_attention", "decode_workspace_bytes", "append_slots",
+    "INVALID_ARGUMENT", "OUT_OF_RANGE", "UNSUPPORTED", "RESOURCE_EXHAUSTED", "RUNTIME", "INTERNAL",
+]
+
+
+def build(jobs: int = 8) -> str:
+    """Compile libhelix_paged.so for gfx950 with the in-tree Makefile."""
+    subprocess.run(["make", "-s", "-C", _native.HERE, f"-j{jobs}", "libhelix_paged.so"],
+                   check=True)
+    return _native.LIB_PATH
+
+
+def load():
+    return _native.load()
+
+
+def _lib():
+    return _native.load()
+
+
+def _ptr(t):
+    """Device (or host) address of a tensor, or None."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _require_f32(t, name):
+    import torch
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise HelixError(INVALID_ARGUMENT, f"{name} must be a contiguous float32 tensor")
+
+
+def _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks):
+    return _native.Config(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
+
+
+# ------------------------------------------------------------------ host ----
+class BlockManager:
+    """Host page bookkeeping of the paged pool (no device memory)."""
+
+    def __init__(self, layers, kv_heads, head_dimension, block_tokens, physical_blocks):
+        h = ctypes.c_void_p()
+        cfg = _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
+        check(_lib().helix_block_manager_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self.block_tokens = block_tokens
+        self.physical_blocks = physical_blocks
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib().helix_block_manager_destroy(h)
+            self._h = None
+
+    def create_sequence(self) -> Sequence:
+        s = Sequence()
+        check(_lib().helix_block_manager_create_sequence(self._h, ctypes.byref(s)))
+        return s
+
+    def fork_sequence(self, source, prefix_tokens, allow_cow=False):
+        s, c = Sequence(), _native.CowCopy()
+        check(_lib().helix_block_manager_fork_sequence(self._h, source, prefix_tokens,
+                                                       int(allow_cow), ctypes.byref(s),
+                                                       ctypes.byref(c)))
+        return s, (c.from_block, c.to_block, c.tokens)
+
+    def append(self, seq, tokens=1):
+        slots = (ctypes.c_uint64 * tokens)()
+        check(_lib().helix_block_manager_append(self._h, seq, tokens, slots))
+        return list(slots)
+
+    def release_sequence(self, seq):
+        check(_lib().helix_block_manager_release_sequence(self._h, seq))
+
+    def contains(self, seq):
+        out = ctypes.c_int()
+        check(_lib().helix_block_manager_contains(self._h, seq, ctypes.byref(out)))
+        return bool(out.value)
+
+    def length(self, seq):
+        out = ctypes.c_size_t()
+        check(_lib().helix_block_manager_length(self._h, seq, ctypes.byref(out)))
+        return out.value
+
+    def block_table(self, seq):
+        n = ctypes.c_size_t()
+        buf = (ctypes.c_uint32 * self.physical_blocks)()
+        check(_lib().helix_block_manager_block_table(self._h, seq, buf, self.physical_blocks,
+                                                     ctypes.byref(n)))
+        return list(buf[: n.value])
+
+    def stats(self):
+        s = _native.Stats()
+        check(_lib().helix_block_manager_stats(self._h, ctypes.byref(s)))
+        return s.as_dict()
+
+    def block_info(self, block):
+        r, t = ctypes.c_size_t(), ctypes.c_size_t()
+        check(_lib().helix_block_manager_block_info(self._h, block, ctypes.byref(r),
+                                                    ctypes.byref(t)))
+        return r.value, t.value
+
+    def validate(self):
+        check(_lib().helix_block_manager_validate(self._h))
+
+    def geometry(self):
+        a, b, c = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        check(_lib().helix_block_manager_geometry(self._h, ctypes.byref(a), ctypes.byref(b),
+                                                  ctypes.byref(c)))
+        return a.value, b.value, c.value
+
+
+# ---------------------------------------------------------------- device ----
+class PagedKvCache:
+    """GPU paged KV pool (CudaPagedKvCache + the CPU cache's fork/bulk append)."""
+
+    def __init__(self, layers, kv_heads, head_dimension, block_tokens, physical_blocks,
+                 device=0):
+        h = ctypes.c_void_p()
+        cfg = _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
+        check(_lib().helix_paged_cache_create(ctypes.byref(cfg), device, ctypes.byref(h)))
+        self._h = h
+        self.layers, self.kv_heads, self.head_dimension = layers, kv_heads, head_dimension
+        self.block_tokens, self.physical_blocks, self.device = block_tokens, physical_blocks, device
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib().helix_paged_cache_destroy(h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def create_sequence(self) -> Sequence:
+        s = Sequence()
+        check(_lib().helix_paged_cache_create_sequence(self._h, ctypes.byref(s)))
+        return s
+
+    def fork_sequence(self, source, prefix_tokens, allow_cow=False, stream=None):
+        s = Sequence()
+        check(_lib().helix_paged_cache_fork_sequence(self._h, source, prefix_tokens,
+                                                     int(allow_cow), _stream(stream),
+                                                     ctypes.byref(s)))
+        return s
+
+    def append(self, seq, token_keys, token_values, stream=None):
+        """token_keys/values: device [layers, kv_heads, head_dimension]."""
+        for t, n in ((token_keys, "token keys"), (token_values, "token values")):
+            _require_f32(t, n)
+            if tuple(t.shape) != (self.layers, self.kv_heads, self.head_dimension):
+                raise HelixError(INVALID_ARGUMENT,
+                                 f"{n} shape does not match [layers, heads, dimension]")
+        check(_lib().helix_paged_cache_append(self._h, seq, _ptr(token_keys), _ptr(token_values),
+                                              _stream(stream)))
+
+    def append_layer_major(self, seq, layer_keys, layer_values, stream=None):
+        """One device [kv_heads, tokens, head_dimension] tensor per layer."""
+        if len(layer_keys) != self.layers or len(layer_values) != self.layers:
+            raise HelixError(INVALID_ARGUMENT, "requires one key/value tensor per layer")
+        tokens = layer_keys[0].shape[1]
+        for t in list(layer_keys) + list(layer_values):
+            _require_f32(t, "layer tensor")
+            if tuple(t.shape) != (self.kv_heads, tokens, self.head_dimension):
+                raise HelixError(INVALID_ARGUMENT, "layer tensor shape mismatch")
+        kp = (ctypes.c_void_p * self.layers)(*[t.data_ptr() for t in layer_keys])
+        vp = (ctypes.c_void_p * self.layers)(*[t.data_ptr() for t in layer_values])
+        check(_lib().helix_paged_cache_append_layer_major(self._h, seq, kp, vp, tokens,
+                                                          _stream(stream)))
+
+    def release_sequence(self, seq):
+        check(_lib().helix_paged_cache_release_sequence(self._h, seq))
+
+    def retrieve_layer(self, seq, layer):
+        """Allocating gather: returns device (keys, values) [kv_heads, length, dim]."""
+        import torch
+        n = self.length(seq)
+        shape = (self.kv_heads, n, self.head_dimension)
+        k = torch.empty(shape, dtype=torch.float32, device=f"cuda:{self.device}")
+        v = torch.empty(shape, dtype=torch.float32, device=f"cuda:{self.device}")
+        self.copy_layer_out(seq, layer, k, v)
+        return k, v
+
+    def copy_layer_out(self, seq, layer, keys, values, stream=None):
+        check(_lib().helix_paged_cache_copy_layer_out(self._h, seq, layer, _ptr(keys),
+                                                      _ptr(values), _stream(stream)))
+
+    def copy_layer_prefix_out(self, seq, layer, expected_length, keys, values, stream=None):
+        check(_lib().helix_paged_cache_copy_layer_prefix_out(
+            self._h, seq, layer, expected_length, _ptr(keys), _ptr(values), keys.shape[1],
+            _stream(stream)))
+
+    def contains(self, seq):
+        out = ctypes.c_int()
+        check(_lib().helix_paged_cache_contains(self._h, seq, ctypes.byref(out)))
+        return bool(out.value)
+
+    def length(self, seq):
+        out = ctypes.c_size_t()
+        check(_lib().helix_paged_cache_length(self._h, seq, ctypes.byref(out)))
+        return out.value
+
+    def block_table(self, seq):
+        n = ctypes.c_size_t()
+        buf = (ctypes.c_uint32 * self.physical_blocks)()
+        check(_lib().helix_paged_cache_block_table(self._h, seq, buf, self.physical_blocks,
+                                                   ctypes.byref(n)))
+        return list(buf[: n.value])
+
+    def stats(self):
+        s = _native.Stats()
+        check(_lib().helix_paged_cache_stats(self._h, ctypes.byref(s)))
+        return s.as_dict()
+
+    def is_healthy(self):
+        out = ctypes.c_int()
+        check(_lib().helix_paged_cache_is_healthy(self._h, ctypes.byref(out)))
+        return bool(out.value)
+
+    def geometry(self):
+        a, b, c = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        check(_lib().helix_paged_cache_geometry(self._h, ctypes.byref(a), ctypes.byref(b),
+                                                ctypes.byref(c)))
+        return a.value, b.value, c.value
+
+    def layer_pool_pointers(self, layer):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        check(_lib().helix_paged_cache_layer_pools(self._h, layer, ctypes.byref(k),
+                                                   ctypes.byref(v)))
+        return k.value, v.value
+
+    def layer_pools(self, layer):
+        """Device copies of layer `layer`'s pools [physical, kv_heads, block_tokens, dim]."""
+        import torch
+        kp, vp = self.layer_pool_pointers(layer)
+        shape = (self.physical_blocks, self.kv_heads, self.block_tokens, self.head_dimension)
+        out = []
+        for p in (kp, vp):
+            t = torch.empty(shape, dtype=torch.float32, device=f"cuda:{self.device}")
+            device_copy(t.data_ptr(), p, t.numel() * 4)
+            out.append(t)
+        return out[0], out[1]
+
+    def read_sequence(self, seq):
+        return DecodeView(self, seq)
+
+
+class DecodeView:
+    """Read lease on one sequence; holds the cache lock until released."""
+
+    def __init__(self, cache, seq):
+        h = ctypes.c_void_p()
+        check(_lib().helix_paged_cache_read_sequence(cache._h, seq, ctypes.byref(h)))
+        self._h = h
+        self._cache = cache
+
+    def release(self):
+        if self._h:
+            _lib().helix_decode_view_release(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.release()
+
+    def __del__(self):
+        self.release()
+
+    def length(self):
+        out = ctypes.c_size_t()
+        check(_lib().helix_decode_view_length(self._h, ctypes.byref(out)))
+        return out.value
+
+    def physical_blocks(self):
+        p, n = ctypes.POINTER(ctypes.c_uint32)(), ctypes.c_size_t()
+        check(_lib().helix_decode_view_physical_blocks(self._h, ctypes.byref(p), ctypes.byref(n)))
+        return [p[i] for i in range(n.value)]
+
+    def block_table(self):
+        p = ctypes.c_void_p()
+        check(_lib().helix_decode_view_block_table(self._h, ctypes.byref(p)))
+        return p.value
+
+    def layer_pool_pointers(self, layer):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        check(_lib().helix_decode_view_layer_pools(self._h, layer, ctypes.byref(k),
+                                                   ctypes.byref(v)))
+        return k.value, v.value
+
+    def poison(self):
+        _lib().helix_decode_view_poison(self._h)
+
+
+class PagedBlockTable:
+    """Validated device copy of a logical->physical page mapping."""
+
+    def __init__(self, physical_blocks, physical_block_count, device=0):
+        ids = (ctypes.c_uint32 * max(1, len(physical_blocks)))(*physical_blocks)
+        h = ctypes.c_void_p()
+        check(_lib().helix_block_table_create(ids, len(physical_blocks), physical_block_count,
+                                              device, ctypes.byref(h)))
+        self._h = h
+        self.logical_block_count = len(physical_blocks)
+        self.physical_block_count = physical_block_count
+
+    def data(self):
+        return _lib().helix_block_table_data(self._h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib().helix_block_table_destroy(h)
+            self._h = None
+
+
+# ------------------------------------------------------------- attention ----
+def paged_attention_out(query, key_blocks, value_blocks, block_table, kv_tokens,
+                        query_position_offset, output, score_workspace, stream=None):
+    """paged_scaled_dot_product_attention_out; block_table: device uint32 pointer or tensor."""
+    hq, nq, kd = query.shape
+    n, hkv, p, vd = value_blocks.shape
+    table_ptr = block_table.data_ptr() if hasattr(block_table, "data_ptr") else block_table
+    logical = 0 if kv_tokens == 0 else (kv_tokens - 1) // p + 1
+    check(_lib().helix_paged_attention_out(
+        _ptr(query), hq, nq, kd, _ptr(key_blocks), _ptr(value_blocks), n, hkv, p, vd,
+        ctypes.c_void_p(table_ptr), logical, kv_tokens, query_position_offset, _ptr(output),
+        _ptr(score_workspace), score_workspace.numel(), _stream(stream)))
+
+
+def paged_attention_with_tail_out(query, key_blocks, value_blocks, block_table, history_tokens,
+                                  tail_key, tail_value, output, score_workspace, stream=None,
+                                  logical_blocks=None):
+    hq, t, kd = query.shape
+    n, hkv, p, vd = value_blocks.shape
+    table_ptr = block_table.data_ptr() if hasattr(block_table, "data_ptr") else block_table
+    if logical_blocks is None:
+        logical_blocks = 0 if history_tokens == 0 else (history_tokens - 1) // p + 1
+    check(_lib().helix_paged_attention_with_tail_out(
+        _ptr(query), hq, t, kd, _ptr(key_blocks), _ptr(value_blocks), n, hkv, p, vd,
+        ctypes.c_void_p(table_ptr), logical_blocks, history_tokens, _ptr(tail_key),
+        _ptr(tail_value), _ptr(output), _ptr(score_workspace), score_workspace.numel(),
+        _stream(stream)))
+
+
+def decode_workspace_bytes(batch, q_heads, max_blocks, pages_per_split=0):
+    out = ctypes.c_size_t()
+    check(_lib().helix_paged_decode_workspace_bytes(batch, q_heads, max_blocks, pages_per_split,
+                                                    ctypes.byref(out)))
+    return out.value
+
+
+def paged_decode_attention(query, key_pool, value_pool, tables, lengths, tail_key, tail_value,
+                           output, workspace, pages_per_split=0, stream=None, pool_shape=None):
+    """Batched decode: query [B, Hq, 128]; pools [N, Hkv, 16, 128] tensors (or raw
+    device addresses with pool_shape); tables [B, max_blocks] int32/uint32;
+    lengths [B] int32; tail [B, Hkv, 128]; output [B, Hq, 128]."""
+    b, hq, _ = query.shape
+    if pool_shape is None:
+        pool_shape = tuple(key_pool.shape)
+        key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
+    n, hkv, _, _ = pool_shape
+    check(_lib().helix_paged_decode_attention(
+        _ptr(query), b, hq, hkv, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
+        _ptr(tables),
+        tables.shape[1], _ptr(lengths), _ptr(tail_key), _ptr(tail_value), _ptr(output),
+        _ptr(workspace), workspace.numel() * workspace.element_size(), pages_per_split,
+        _stream(stream)))
+
+
+def append_slots(keys, values, key_pool, value_pool, slots, stream=None):
+    """Write rows [count, Hkv, D] into one layer's pools at int64 slots."""
+    n, hkv, p, d = key_pool.shape
+    check(_lib().helix_paged_append_slots(_ptr(keys), _ptr(values), _ptr(key_pool),
+                                          _ptr(value_pool), n, hkv, p, d, _ptr(slots),
+                                          slots.numel(), _stream(stream)))
+
+
+class DecodeBatch:
+    """Batched decode driver over a PagedKvCache (persistent device tables)."""
+
+    def __init__(self, cache, sequences, q_heads, max_tokens, pages_per_split=0):
+        arr = (Sequence * len(sequences))(*sequences)
+        h = ctypes.c_void_p()
+        check(_lib().helix_decode_batch_create(cache._h, arr, len(sequences), q_heads, max_tokens,
+                                               pages_per_split, ctypes.byref(h)))
+        self._h = h
+        self._cache = cache
+        self.batch = len(sequences)
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib().helix_decode_batch_destroy(h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def prepare(self, stream=None):
+        check(_lib().helix_decode_batch_prepare(self._h, _stream(stream)))
+
+    def append_layer(self, layer, keys, values, stream=None):
+        check(_lib().helix_decode_batch_append_layer(self._h, layer, _ptr(keys), _ptr(values),
+                                                     _stream(stream)))
+
+    def attention_layer(self, layer, query, tail_key, tail_value, output, stream=None):
+        check(_lib().helix_decode_batch_attention_layer(self._h, layer, _ptr(query),
+                                                        _ptr(tail_key), _ptr(tail_value),
+                                                        _ptr(output), _stream(stream)))
+
+    def device_state(self):
+        t, l, s = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        mb, ps = ctypes.c_size_t(), ctypes.c_size_t()
+        check(_lib().helix_decode_batch_tables(self._h, ctypes.byref(t), ctypes.byref(l),
+                                               ctypes.byref(s), ctypes.byref(mb),
+                                               ctypes.byref(ps)))
+        return {"tables": t.value, "lengths": l.value, "slots": s.value,
+                "max_blocks": mb.value, "pages_per_split": ps.value}
+
+
+# ---------------------------------------------------------------- plumbing ----
+_hip = None
+
+
+def device_copy(dst: int, src: int, nbytes: int):
+    """hipMemcpy device-to-device (plumbing for reading raw pool memory)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.restype = ctypes.c_int
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    rc = _hip.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3)
+    if rc != 0:
+        raise HelixError(RUNTIME, f"hipMemcpy failed with {rc}")

@@ -1,0 +1,865 @@
+// extern "C" boundary: converts helix::Error (and any other exception) into a
+// status code plus a thread-local message; nothing throws across it.
+#include "../../include/helix_paged.h"
+
+#include "block_manager.hpp"
+#include "kernels.hpp"
+#include "paged_cache.hpp"
+#include "status.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+using helix::Error;
+using helix::Status;
+using helix::check;
+
+struct helix_block_manager {
+  explicit helix_block_manager(const helix::PagedConfig& c) : manager(c) {}
+  helix::BlockManager manager;
+  std::mutex mutex;
+};
+
+struct helix_paged_cache {
+  helix_paged_cache(const helix::PagedConfig& c, int device) : cache(c, device) {}
+  helix::DevicePagedCache cache;
+};
+
+struct helix_decode_view {
+  helix_decode_view(std::shared_ptr<helix::CacheState> s, std::uint64_t id, std::uint64_t cid)
+      : view(std::move(s), id, cid) {}
+  helix::DecodeView view;
+};
+
+struct helix_block_table {
+  helix::DeviceBuffer buffer;
+  std::size_t logical = 0;
+  std::size_t physical = 0;
+  int device = -1;
+};
+
+struct helix_decode_batch {
+  std::unique_ptr<helix::DecodeBatch> batch;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int guarded(F&& body) {
+  try {
+    body();
+    g_last_error.clear();
+    return HELIX_OK;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return static_cast<int>(e.status());
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return HELIX_RESOURCE_EXHAUSTED;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return HELIX_INTERNAL;
+  } catch (...) {
+    g_last_error = "unknown exception";
+    return HELIX_INTERNAL;
+  }
+}
+
+helix::PagedConfig to_config(const helix_paged_config* c) {
+  check(c != nullptr, Status::kInvalidArgument, "config must not be NULL");
+  return helix::PagedConfig{c->layers, c->kv_heads, c->head_dimension, c->block_tokens,
+                            c->physical_blocks};
+}
+
+void copy_stats(const helix::PagedStats& s, helix_paged_stats* out) {
+  check(out != nullptr, Status::kInvalidArgument, "stats output must not be NULL");
+  static_assert(sizeof(helix::PagedStats) == sizeof(helix_paged_stats), "stats layout");
+  std::memcpy(out, &s, sizeof(s));
+}
+
+void require_out(const void* p) {
+  check(p != nullptr, Status::kInvalidArgument, "output pointer must not be NULL");
+}
+
+hipStream_t as_stream(helix_stream s) { return static_cast<hipStream_t>(s); }
+
+bool overlap(const void* a, std::size_t an, const void* b, std::size_t bn) {
+  if (a == nullptr || b == nullptr || an == 0 || bn == 0) return false;
+  const auto x = reinterpret_cast<std::uintptr_t>(a);
+  const auto y = reinterpret_cast<std::uintptr_t>(b);
+  return x < y + bn && y < x + an;
+}
+
+std::size_t mul(std::size_t a, std::size_t b) {
+  check(a == 0 || b <= std::numeric_limits<std::size_t>::max() / a, Status::kOutOfRange,
+        "size computation overflows");
+  return a * b;
+}
+
+void require_manager_handle(const helix::BlockManager& m, helix_sequence s, const char* op) {
+  check(s.id != 0 && s.cache_id == m.cache_id(), Status::kInvalidArgument,
+        std::string(op) + ": sequence handle belongs to another cache or is empty");
+}
+
+// ------------------------------------------------ attention validation ----
+// validate_query_key_and_table / validate_value_blocks / validate_offset of
+// src/attention/cuda_paged.cu:211-335.
+struct AttentionShape {
+  std::size_t q_heads, queries, key_dim, physical, kv_heads, block_tokens, value_dim;
+  std::size_t logical, history, tail, keys, offset;
+};
+
+void validate_attention(const AttentionShape& s, bool allow_empty_history, const char* op) {
+  const std::string o(op);
+  check(s.physical > 0 && s.kv_heads > 0 && s.block_tokens > 0 && s.key_dim > 0,
+        Status::kInvalidArgument,
+        o + ": physical block, head, token, and key dimensions must be positive");
+  check(s.value_dim > 0, Status::kInvalidArgument, o + ": value dimension must be positive");
+  check(s.q_heads > 0 && s.q_heads % s.kv_heads == 0, Status::kInvalidArgument,
+        o + ": query heads must be a positive multiple of the key/value heads");
+  check(s.physical <= std::numeric_limits<std::uint32_t>::max(), Status::kInvalidArgument,
+        o + ": physical block capacity must fit the uint32 block-ID representation");
+  check(allow_empty_history || s.history != 0, Status::kInvalidArgument,
+        o + ": KV token count must be positive");
+  const std::size_t required = s.history == 0 ? 0 : 1 + (s.history - 1) / s.block_tokens;
+  check(s.logical == required, Status::kInvalidArgument,
+        o + ": block table length must exactly cover the logical KV token range");
+  check(s.offset <= s.keys, Status::kInvalidArgument,
+        o + ": query position offset exceeds the KV token count");
+  check(s.queries <= s.keys - s.offset, Status::kInvalidArgument,
+        o + ": query range extends beyond the KV token count");
+  check(s.value_dim <= 1024, Status::kUnsupported, o + ": value dimension above 1024");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* helix_last_error(void) { return g_last_error.c_str(); }
+
+const char* helix_status_name(int status) {
+  switch (status) {
+    case HELIX_OK: return "ok";
+    case HELIX_INVALID_ARGUMENT: return "invalid_argument";
+    case HELIX_OUT_OF_RANGE: return "out_of_range";
+    case HELIX_UNSUPPORTED: return "unsupported";
+    case HELIX_RESOURCE_EXHAUSTED: return "resource_exhausted";
+    case HELIX_RUNTIME: return "runtime";
+    case HELIX_INTERNAL: return "internal";
+    default: return "unknown";
+  }
+}
+
+// --------------------------------------------------------- block manager ----
+int helix_block_manager_create(const helix_paged_config* config, helix_block_manager** out) {
+  return guarded([&] {
+    require_out(out);
+    *out = nullptr;
+    *out = new helix_block_manager(to_config(config));
+  });
+}
+
+void helix_block_manager_destroy(helix_block_manager* m) { delete m; }
+
+int helix_block_manager_create_sequence(helix_block_manager* m, helix_sequence* out) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    require_out(out);
+    std::scoped_lock lock(m->mutex);
+    *out = helix_sequence{m->manager.create_sequence(), m->manager.cache_id()};
+  });
+}
+
+int helix_block_manager_fork_sequence(helix_block_manager* m, helix_sequence source,
+                                      size_t prefix_tokens, int allow_cow, helix_sequence* out,
+                                      helix_cow_copy* copy) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    require_out(out);
+    std::scoped_lock lock(m->mutex);
+    require_manager_handle(m->manager, source, "fork_sequence");
+    const helix::ForkPlan plan = m->manager.plan_fork(source.id, prefix_tokens, allow_cow != 0);
+    const std::uint64_t id = m->manager.commit_fork(plan);
+    *out = helix_sequence{id, m->manager.cache_id()};
+    if (copy != nullptr) {
+      *copy = helix_cow_copy{plan.cow_from, plan.cow_to,
+                             plan.copy_on_write ? plan.cow_tokens : 0};
+    }
+  });
+}
+
+int helix_block_manager_append(helix_block_manager* m, helix_sequence sequence, size_t tokens,
+                               uint64_t* slots) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    std::scoped_lock lock(m->mutex);
+    require_manager_handle(m->manager, sequence, "append");
+    const helix::AppendPlan plan = m->manager.plan_append(sequence.id, tokens);
+    if (slots != nullptr) {
+      for (std::size_t i = 0; i < tokens; ++i) {
+        slots[i] = plan.slot(i, m->manager.config().block_tokens);
+      }
+    }
+    m->manager.commit_append(plan);
+  });
+}
+
+int helix_block_manager_release_sequence(helix_block_manager* m, helix_sequence sequence) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    std::scoped_lock lock(m->mutex);
+    require_manager_handle(m->manager, sequence, "release_sequence");
+    m->manager.release(sequence.id);
+  });
+}
+
+int helix_block_manager_contains(const helix_block_manager* m, helix_sequence sequence,
+                                 int* out) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    require_out(out);
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    *out = sequence.id != 0 && sequence.cache_id == m->manager.cache_id() &&
+           m->manager.contains(sequence.id);
+  });
+}
+
+int helix_block_manager_length(const helix_block_manager* m, helix_sequence sequence,
+                               size_t* out) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    require_out(out);
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    require_manager_handle(m->manager, sequence, "length");
+    *out = m->manager.length(sequence.id);
+  });
+}
+
+int helix_block_manager_block_table(const helix_block_manager* m, helix_sequence sequence,
+                                    uint32_t* out, size_t capacity, size_t* count) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    require_out(count);
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    require_manager_handle(m->manager, sequence, "block_table");
+    const auto& blocks = m->manager.blocks(sequence.id);
+    *count = blocks.size();
+    for (std::size_t i = 0; i < blocks.size() && i < capacity; ++i) out[i] = blocks[i];
+  });
+}
+
+int helix_block_manager_stats(const helix_block_manager* m, helix_paged_stats* out) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    copy_stats(m->manager.stats(), out);
+  });
+}
+
+int helix_block_manager_block_info(const helix_block_manager* m, uint32_t block,
+                                   size_t* reference_count, size_t* token_count) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    if (reference_count != nullptr) *reference_count = m->manager.block_reference_count(block);
+    if (token_count != nullptr) *token_count = m->manager.block_token_count(block);
+  });
+}
+
+int helix_block_manager_validate(const helix_block_manager* m) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    auto* mm = const_cast<helix_block_manager*>(m);
+    std::scoped_lock lock(mm->mutex);
+    m->manager.validate();
+  });
+}
+
+int helix_block_manager_geometry(const helix_block_manager* m, size_t* bytes_per_token,
+                                 size_t* block_bytes, size_t* token_capacity) {
+  return guarded([&] {
+    check(m != nullptr, Status::kInvalidArgument, "manager must not be NULL");
+    if (bytes_per_token != nullptr) *bytes_per_token = m->manager.bytes_per_token();
+    if (block_bytes != nullptr) *block_bytes = m->manager.block_bytes();
+    if (token_capacity != nullptr) *token_capacity = m->manager.token_capacity();
+  });
+}
+
+// ----------------------------------------------------------- device cache ----
+int helix_paged_cache_create(const helix_paged_config* config, int device,
+                             helix_paged_cache** out) {
+  return guarded([&] {
+    require_out(out);
+    *out = nullptr;
+    *out = new helix_paged_cache(to_config(config), device);
+  });
+}
+
+void helix_paged_cache_destroy(helix_paged_cache* cache) { delete cache; }
+
+#define REQUIRE_CACHE() check(cache != nullptr, Status::kInvalidArgument, "cache must not be NULL")
+
+int helix_paged_cache_create_sequence(helix_paged_cache* cache, helix_sequence* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    *out = helix_sequence{cache->cache.create_sequence(), cache->cache.cache_id()};
+  });
+}
+
+int helix_paged_cache_fork_sequence(helix_paged_cache* cache, helix_sequence source,
+                                    size_t prefix_tokens, int allow_cow, helix_stream stream,
+                                    helix_sequence* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    const std::uint64_t id = cache->cache.fork_sequence(source.id, source.cache_id, prefix_tokens,
+                                                        allow_cow != 0, as_stream(stream));
+    *out = helix_sequence{id, cache->cache.cache_id()};
+  });
+}
+
+int helix_paged_cache_append(helix_paged_cache* cache, helix_sequence sequence,
+                             const float* token_keys, const float* token_values,
+                             helix_stream stream) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    cache->cache.append(sequence.id, sequence.cache_id, token_keys, token_values,
+                        as_stream(stream));
+  });
+}
+
+int helix_paged_cache_append_layer_major(helix_paged_cache* cache, helix_sequence sequence,
+                                         const float* const* layer_keys,
+                                         const float* const* layer_values, size_t tokens,
+                                         helix_stream stream) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    cache->cache.append_layer_major(sequence.id, sequence.cache_id, layer_keys, layer_values,
+                                    tokens, as_stream(stream));
+  });
+}
+
+int helix_paged_cache_release_sequence(helix_paged_cache* cache, helix_sequence sequence) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    cache->cache.release(sequence.id, sequence.cache_id);
+  });
+}
+
+int helix_paged_cache_copy_layer_out(helix_paged_cache* cache, helix_sequence sequence,
+                                     size_t layer, float* keys_out, float* values_out,
+                                     helix_stream stream) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    std::size_t length = 0;
+    {
+      auto& s = *cache->cache.state();
+      std::scoped_lock lock(s.mutex);
+      s.require_sequence(sequence.id, sequence.cache_id, "copy_layer_out");
+      length = s.manager.length(sequence.id);
+    }
+    cache->cache.copy_layer_out(sequence.id, sequence.cache_id, layer, length, keys_out,
+                                values_out, length, as_stream(stream));
+  });
+}
+
+int helix_paged_cache_copy_layer_prefix_out(helix_paged_cache* cache, helix_sequence sequence,
+                                            size_t layer, size_t expected_length,
+                                            float* keys_out, float* values_out,
+                                            size_t dest_tokens, helix_stream stream) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    cache->cache.copy_layer_out(sequence.id, sequence.cache_id, layer, expected_length, keys_out,
+                                values_out, dest_tokens, as_stream(stream));
+  });
+}
+
+int helix_paged_cache_contains(helix_paged_cache* cache, helix_sequence sequence, int* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    auto& s = *cache->cache.state();
+    std::scoped_lock lock(s.mutex);
+    *out = sequence.id != 0 && sequence.cache_id == s.manager.cache_id() &&
+           s.manager.contains(sequence.id);
+  });
+}
+
+int helix_paged_cache_length(helix_paged_cache* cache, helix_sequence sequence, size_t* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    auto& s = *cache->cache.state();
+    std::scoped_lock lock(s.mutex);
+    s.require_sequence(sequence.id, sequence.cache_id, "length");
+    *out = s.manager.length(sequence.id);
+  });
+}
+
+int helix_paged_cache_block_table(helix_paged_cache* cache, helix_sequence sequence,
+                                  uint32_t* out, size_t capacity, size_t* count) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(count);
+    auto& s = *cache->cache.state();
+    std::scoped_lock lock(s.mutex);
+    s.require_sequence(sequence.id, sequence.cache_id, "block_table");
+    const auto& blocks = s.manager.blocks(sequence.id);
+    *count = blocks.size();
+    for (std::size_t i = 0; i < blocks.size() && i < capacity; ++i) out[i] = blocks[i];
+  });
+}
+
+int helix_paged_cache_stats(helix_paged_cache* cache, helix_paged_stats* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    auto& s = *cache->cache.state();
+    std::scoped_lock lock(s.mutex);
+    copy_stats(s.manager.stats(), out);
+  });
+}
+
+int helix_paged_cache_is_healthy(helix_paged_cache* cache, int* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    auto& s = *cache->cache.state();
+    std::scoped_lock lock(s.mutex);
+    *out = !s.poisoned;
+  });
+}
+
+int helix_paged_cache_geometry(helix_paged_cache* cache, size_t* bytes_per_token,
+                               size_t* block_bytes, size_t* token_capacity) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    const auto& m = cache->cache.state()->manager;
+    if (bytes_per_token != nullptr) *bytes_per_token = m.bytes_per_token();
+    if (block_bytes != nullptr) *block_bytes = m.block_bytes();
+    if (token_capacity != nullptr) *token_capacity = m.token_capacity();
+  });
+}
+
+int helix_paged_cache_layer_pools(helix_paged_cache* cache, size_t layer, float** key_blocks,
+                                  float** value_blocks) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    const auto& s = *cache->cache.state();
+    check(layer < s.manager.config().layers, Status::kOutOfRange, "layer index is out of range");
+    if (key_blocks != nullptr) *key_blocks = s.key_pool(layer);
+    if (value_blocks != nullptr) *value_blocks = s.value_pool(layer);
+  });
+}
+
+int helix_paged_cache_read_sequence(helix_paged_cache* cache, helix_sequence sequence,
+                                    helix_decode_view** out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    *out = nullptr;
+    *out = new helix_decode_view(cache->cache.state(), sequence.id, sequence.cache_id);
+  });
+}
+
+int helix_decode_view_length(const helix_decode_view* view, size_t* out) {
+  return guarded([&] {
+    check(view != nullptr, Status::kInvalidArgument, "view must not be NULL");
+    require_out(out);
+    *out = view->view.length();
+  });
+}
+
+int helix_decode_view_physical_blocks(const helix_decode_view* view, const uint32_t** blocks,
+                                      size_t* count) {
+  return guarded([&] {
+    check(view != nullptr, Status::kInvalidArgument, "view must not be NULL");
+    require_out(blocks);
+    require_out(count);
+    const auto& b = view->view.physical_blocks();
+    *blocks = b.data();
+    *count = b.size();
+  });
+}
+
+int helix_decode_view_block_table(const helix_decode_view* view, const uint32_t** device_table) {
+  return guarded([&] {
+    check(view != nullptr, Status::kInvalidArgument, "view must not be NULL");
+    require_out(device_table);
+    *device_table = view->view.device_table();
+  });
+}
+
+int helix_decode_view_layer_pools(const helix_decode_view* view, size_t layer,
+                                  float** key_blocks, float** value_blocks) {
+  return guarded([&] {
+    check(view != nullptr, Status::kInvalidArgument, "view must not be NULL");
+    if (key_blocks != nullptr) *key_blocks = view->view.key_pool(layer);
+    if (value_blocks != nullptr) *value_blocks = view->view.value_pool(layer);
+  });
+}
+
+void helix_decode_view_poison(helix_decode_view* view) {
+  if (view != nullptr) view->view.poison();
+}
+
+void helix_decode_view_release(helix_decode_view* view) { delete view; }
+
+// ------------------------------------------------------------ block table ----
+int helix_block_table_create(const uint32_t* physical_blocks, size_t count,
+                             size_t physical_block_count, int device, helix_block_table** out) {
+  return guarded([&] {
+    require_out(out);
+    *out = nullptr;
+    check(physical_block_count != 0 &&
+              physical_block_count <= std::numeric_limits<std::uint32_t>::max(),
+          Status::kInvalidArgument,
+          "PagedBlockTable: physical block capacity must fit the uint32 block-ID representation");
+    check(device >= 0, Status::kInvalidArgument, "PagedBlockTable: device index must be non-negative");
+    check(count == 0 || physical_blocks != nullptr, Status::kInvalidArgument,
+          "PagedBlockTable: IDs must not be NULL");
+    for (std::size_t i = 0; i < count; ++i) {
+      check(physical_blocks[i] < physical_block_count, Status::kOutOfRange,
+            "PagedBlockTable: physical block ID exceeds the packed block capacity");
+    }
+    auto table = std::make_unique<helix_block_table>();
+    table->logical = count;
+    table->physical = physical_block_count;
+    table->device = device;
+    if (count != 0) {
+      table->buffer = helix::DeviceBuffer(count * sizeof(std::uint32_t), device);
+      helix::DeviceGuard guard(device);
+      helix::hip_check(hipMemcpy(table->buffer.data(), physical_blocks,
+                                 count * sizeof(std::uint32_t), hipMemcpyHostToDevice),
+                       "PagedBlockTable upload");
+    }
+    *out = table.release();
+  });
+}
+
+const uint32_t* helix_block_table_data(const helix_block_table* table) {
+  return table == nullptr ? nullptr : static_cast<const uint32_t*>(table->buffer.data());
+}
+
+size_t helix_block_table_logical_block_count(const helix_block_table* table) {
+  return table == nullptr ? 0 : table->logical;
+}
+
+void helix_block_table_destroy(helix_block_table* table) { delete table; }
+
+// -------------------------------------------- reference-shaped attention ----
+int helix_paged_score_workspace_bytes(size_t q_heads, size_t queries, size_t kv_heads,
+                                      size_t physical_blocks, size_t block_tokens,
+                                      size_t logical_blocks, size_t kv_tokens, size_t* out) {
+  return guarded([&] {
+    require_out(out);
+    AttentionShape s{q_heads, queries, 1,  physical_blocks, kv_heads, block_tokens, 1,
+                     logical_blocks, kv_tokens, 0, kv_tokens, 0};
+    validate_attention(s, false, "paged_score_workspace_bytes");
+    *out = mul(mul(mul(q_heads, queries), kv_tokens), sizeof(float));
+  });
+}
+
+int helix_paged_tail_score_workspace_bytes(size_t q_heads, size_t tail_tokens, size_t kv_heads,
+                                           size_t physical_blocks, size_t block_tokens,
+                                           size_t logical_blocks, size_t history_tokens,
+                                           size_t* out) {
+  return guarded([&] {
+    require_out(out);
+    check(tail_tokens != 0, Status::kInvalidArgument,
+          "paged_tail_score_workspace_bytes: tail token count must be positive");
+    check(history_tokens <= std::numeric_limits<std::int64_t>::max() - tail_tokens,
+          Status::kResourceExhausted,
+          "paged_tail_score_workspace_bytes: history plus tail token count overflows shape range");
+    AttentionShape s{q_heads, tail_tokens, 1, physical_blocks, kv_heads, block_tokens, 1,
+                     logical_blocks, history_tokens, tail_tokens, history_tokens + tail_tokens,
+                     history_tokens};
+    validate_attention(s, true, "paged_tail_score_workspace_bytes");
+    *out = mul(mul(mul(q_heads, tail_tokens), history_tokens + tail_tokens), sizeof(float));
+  });
+}
+
+namespace {
+
+void run_reference_attention(const AttentionShape& s, const float* query,
+                             const float* key_blocks, const float* value_blocks,
+                             const std::uint32_t* block_table, const float* tail_key,
+                             const float* tail_value, float* output, float* workspace,
+                             std::size_t workspace_elements, hipStream_t stream, const char* op) {
+  const std::string o(op);
+  const std::size_t ws = mul(mul(s.q_heads, s.queries), s.keys);
+  check(workspace_elements == ws, Status::kInvalidArgument,
+        o + ": score workspace shape does not match [heads, queries, kv tokens]");
+  if (s.queries == 0) return;
+  check(query != nullptr && output != nullptr && workspace != nullptr, Status::kInvalidArgument,
+        o + ": query, output and workspace must be non-null device pointers");
+  check(s.history == 0 || (key_blocks != nullptr && value_blocks != nullptr &&
+                           block_table != nullptr),
+        Status::kInvalidArgument, o + ": key/value blocks and block table must be non-null");
+  check(s.tail == 0 || (tail_key != nullptr && tail_value != nullptr), Status::kInvalidArgument,
+        o + ": tail key and value must be non-null");
+  const std::size_t qb = mul(ws / s.keys, s.key_dim) * sizeof(float);
+  const std::size_t ob = mul(ws / s.keys, s.value_dim) * sizeof(float);
+  const std::size_t wb = ws * sizeof(float);
+  const std::size_t page = mul(s.physical, mul(s.kv_heads, s.block_tokens));
+  const std::size_t kb = mul(page, s.key_dim) * sizeof(float);
+  const std::size_t vb = mul(page, s.value_dim) * sizeof(float);
+  const std::size_t tkb = mul(mul(s.kv_heads, s.tail), s.key_dim) * sizeof(float);
+  const std::size_t tvb = mul(mul(s.kv_heads, s.tail), s.value_dim) * sizeof(float);
+  check(!overlap(query, qb, output, ob), Status::kInvalidArgument, o + ": output must not alias query");
+  check(!overlap(key_blocks, kb, output, ob), Status::kInvalidArgument,
+        o + ": output must not alias key blocks");
+  check(!overlap(value_blocks, vb, output, ob), Status::kInvalidArgument,
+        o + ": output must not alias value blocks");
+  check(!overlap(tail_key, tkb, output, ob), Status::kInvalidArgument,
+        o + ": output must not alias tail key");
+  check(!overlap(tail_value, tvb, output, ob), Status::kInvalidArgument,
+        o + ": output must not alias tail value");
+  check(!overlap(query, qb, workspace, wb), Status::kInvalidArgument,
+        o + ": score workspace must not alias query");
+  check(!overlap(key_blocks, kb, workspace, wb), Status::kInvalidArgument,
+        o + ": score workspace must not alias key blocks");
+  check(!overlap(value_blocks, vb, workspace, wb), Status::kInvalidArgument,
+        o + ": score workspace must not alias value blocks");
+  check(!overlap(tail_key, tkb, workspace, wb), Status::kInvalidArgument,
+        o + ": score workspace must not alias tail key");
+  check(!overlap(tail_value, tvb, workspace, wb), Status::kInvalidArgument,
+        o + ": score workspace must not alias tail value");
+  check(!overlap(workspace, wb, output, ob), Status::kInvalidArgument,
+        o + ": output must not alias score workspace");
+  helix::hip::GenericArgs a{};
+  a.query = query;
+  a.key_blocks = key_blocks;
+  a.value_blocks = value_blocks;
+  a.table = block_table;
+  a.tail_key = tail_key;
+  a.tail_value = tail_value;
+  a.out = output;
+  a.workspace = workspace;
+  a.q_heads = s.q_heads;
+  a.kv_heads = s.kv_heads;
+  a.queries = s.queries;
+  a.key_dim = s.key_dim;
+  a.value_dim = s.value_dim;
+  a.block_tokens = s.block_tokens;
+  a.physical_blocks = s.physical;
+  a.history = s.history;
+  a.tail = s.tail;
+  a.offset = s.offset;
+  helix::hip_check(helix::hip::launch_generic(a, stream), (o + " launch").c_str());
+}
+
+}  // namespace
+
+int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries, size_t key_dim,
+                              const float* key_blocks, const float* value_blocks,
+                              size_t physical_blocks, size_t kv_heads, size_t block_tokens,
+                              size_t value_dim, const uint32_t* block_table,
+                              size_t logical_blocks, size_t kv_tokens,
+                              size_t query_position_offset, float* output,
+                              float* score_workspace, size_t workspace_elements,
+                              helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "paged_scaled_dot_product_attention_out";
+    AttentionShape s{q_heads, queries, key_dim, physical_blocks, kv_heads, block_tokens,
+                     value_dim, logical_blocks, kv_tokens, 0, kv_tokens, query_position_offset};
+    validate_attention(s, false, op);
+    run_reference_attention(s, query, key_blocks, value_blocks, block_table, nullptr, nullptr,
+                            output, score_workspace, workspace_elements, as_stream(stream), op);
+  });
+}
+
+int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size_t tail_tokens,
+                                        size_t key_dim, const float* key_blocks,
+                                        const float* value_blocks, size_t physical_blocks,
+                                        size_t kv_heads, size_t block_tokens, size_t value_dim,
+                                        const uint32_t* block_table, size_t logical_blocks,
+                                        size_t history_tokens, const float* tail_key,
+                                        const float* tail_value, float* output,
+                                        float* score_workspace, size_t workspace_elements,
+                                        helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "paged_scaled_dot_product_attention_with_tail_out";
+    check(tail_tokens != 0, Status::kInvalidArgument, std::string(op) +
+                                                          ": tail token count must be positive");
+    check(history_tokens <= std::numeric_limits<std::int64_t>::max() - tail_tokens,
+          Status::kResourceExhausted,
+          std::string(op) + ": history plus tail token count overflows shape range");
+    AttentionShape s{q_heads, tail_tokens, key_dim, physical_blocks, kv_heads, block_tokens,
+                     value_dim, logical_blocks, history_tokens, tail_tokens,
+                     history_tokens + tail_tokens, history_tokens};
+    validate_attention(s, true, op);
+    run_reference_attention(s, query, key_blocks, value_blocks, block_table, tail_key,
+                            tail_value, output, score_workspace, workspace_elements,
+                            as_stream(stream), op);
+  });
+}
+
+// ---------------------------------------------------------- batched decode ----
+namespace {
+
+constexpr std::size_t kDefaultPagesPerSplit = 8;
+
+std::size_t resolve_split(std::size_t pages_per_split) {
+  return pages_per_split == 0 ? kDefaultPagesPerSplit : pages_per_split;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t max_blocks,
+                                       size_t pages_per_split, size_t* out) {
+  return guarded([&] {
+    require_out(out);
+    *out = helix::hip::decode_workspace_bytes(batch, q_heads, max_blocks,
+                                              resolve_split(pages_per_split));
+  });
+}
+
+int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
+                                 size_t kv_heads, const float* key_blocks,
+                                 const float* value_blocks, size_t physical_blocks,
+                                 const uint32_t* tables, size_t max_blocks,
+                                 const int32_t* lengths, const float* tail_key,
+                                 const float* tail_value, float* output, void* workspace,
+                                 size_t workspace_bytes, size_t pages_per_split,
+                                 helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "paged_decode_attention";
+    const std::size_t split = resolve_split(pages_per_split);
+    check(kv_heads != 0 && q_heads % kv_heads == 0 &&
+              helix::hip::decode_group_supported(q_heads / kv_heads),
+          Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");
+    check(physical_blocks != 0 && physical_blocks <= std::numeric_limits<std::uint32_t>::max(),
+          Status::kInvalidArgument, std::string(op) + ": physical block count out of range");
+    check(max_blocks != 0 && max_blocks <= static_cast<std::size_t>(
+                                               std::numeric_limits<std::int32_t>::max() / 16),
+          Status::kInvalidArgument, std::string(op) + ": max_blocks out of range");
+    if (batch == 0) return;
+    check(query && key_blocks && value_blocks && tables && lengths && tail_key && tail_value &&
+              output && workspace,
+          Status::kInvalidArgument, std::string(op) + ": device pointers must be non-null");
+    check(aligned16(query) && aligned16(key_blocks) && aligned16(value_blocks) &&
+              aligned16(tail_key) && aligned16(tail_value) && aligned16(output) &&
+              aligned16(workspace),
+          Status::kInvalidArgument, std::string(op) + ": tensors must be 16-byte aligned");
+    check(workspace_bytes >= helix::hip::decode_workspace_bytes(batch, q_heads, max_blocks, split),
+          Status::kInvalidArgument, std::string(op) + ": workspace is too small");
+    const std::size_t ob = batch * q_heads * helix::hip::kDecodeHeadDim * sizeof(float);
+    check(!overlap(output, ob, query, ob) && !overlap(output, ob, workspace, workspace_bytes),
+          Status::kInvalidArgument, std::string(op) + ": output must not alias query or workspace");
+    helix::hip::DecodeArgs a{};
+    a.query = query;
+    a.key_pool = key_blocks;
+    a.value_pool = value_blocks;
+    a.tables = tables;
+    a.lengths = lengths;
+    a.tail_key = tail_key;
+    a.tail_value = tail_value;
+    a.out = output;
+    a.workspace = workspace;
+    a.batch = batch;
+    a.q_heads = q_heads;
+    a.kv_heads = kv_heads;
+    a.max_blocks = max_blocks;
+    a.physical_blocks = physical_blocks;
+    a.pages_per_split = split;
+    helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), "paged_decode_attention");
+  });
+}
+
+int helix_paged_append_slots(const float* keys, const float* values, float* key_blocks,
+                             float* value_blocks, size_t physical_blocks, size_t kv_heads,
+                             size_t block_tokens, size_t head_dim, const int64_t* slots,
+                             size_t count, helix_stream stream) {
+  return guarded([&] {
+    check(physical_blocks != 0 && kv_heads != 0 && block_tokens != 0 && head_dim != 0,
+          Status::kInvalidArgument, "append_slots: geometry must be positive");
+    if (count == 0) return;
+    check(keys && values && key_blocks && value_blocks && slots, Status::kInvalidArgument,
+          "append_slots: device pointers must be non-null");
+    helix::hip_check(
+        helix::hip::launch_append_slots(
+            keys, values, key_blocks, value_blocks,
+            helix::hip::PageGeometry{physical_blocks, kv_heads, block_tokens, head_dim}, slots,
+            count, as_stream(stream)),
+        "append_slots");
+  });
+}
+
+int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* sequences,
+                              size_t batch, size_t q_heads, size_t max_tokens,
+                              size_t pages_per_split, helix_decode_batch** out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    *out = nullptr;
+    check(batch == 0 || sequences != nullptr, Status::kInvalidArgument,
+          "decode batch sequences must not be NULL");
+    std::vector<std::uint64_t> ids(batch), cids(batch);
+    for (std::size_t i = 0; i < batch; ++i) {
+      ids[i] = sequences[i].id;
+      cids[i] = sequences[i].cache_id;
+    }
+    auto b = std::make_unique<helix_decode_batch>();
+    b->batch = std::make_unique<helix::DecodeBatch>(cache->cache.state(), ids.data(),
+                                                    cids.data(), batch, q_heads, max_tokens,
+                                                    pages_per_split);
+    *out = b.release();
+  });
+}
+
+int helix_decode_batch_prepare(helix_decode_batch* b, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->prepare(as_stream(stream));
+  });
+}
+
+int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
+                                    const float* values, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->append_layer(layer, keys, values, as_stream(stream));
+  });
+}
+
+int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
+                                       const float* tail_key, const float* tail_value,
+                                       float* output, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->attention_layer(layer, query, tail_key, tail_value, output, as_stream(stream));
+  });
+}
+
+int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tables,
+                              const int32_t** lengths, const int64_t** slots,
+                              size_t* max_blocks, size_t* pages_per_split) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    if (tables != nullptr) *tables = b->batch->tables();
+    if (lengths != nullptr) *lengths = b->batch->lengths();
+    if (slots != nullptr) *slots = b->batch->slots();
+    if (max_blocks != nullptr) *max_blocks = b->batch->max_blocks();
+    if (pages_per_split != nullptr) *pages_per_split = b->batch->pages_per_split();
+  });
+}
+
+void helix_decode_batch_destroy(helix_decode_batch* b) { delete b; }
+
+}  // extern "C"

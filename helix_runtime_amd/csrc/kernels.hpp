@@ -1,0 +1,139 @@
+// Device kernels of the paged-KV hot path (gfx950) and their host launchers.
+//
+// Every launcher takes plain device pointers and sizes, launches on the given
+// stream and returns the hipError_t of the launch.  Shapes are validated by
+// the callers (paged_cache.cpp / c_api.cpp) before anything is launched.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace helix::hip {
+
+// Pool geometry of one layer: [physical_blocks, kv_heads, block_tokens, dim].
+struct PageGeometry {
+  std::size_t physical_blocks;
+  std::size_t kv_heads;
+  std::size_t block_tokens;
+  std::size_t head_dim;
+};
+
+// One token for every layer.  src [layers, kv_heads, head_dim]; the token
+// lands at (block, offset) of every layer pool.  Layer l's key pool starts at
+// key_base + l * layer_stride (elements), values likewise.
+hipError_t launch_append_token(const float* keys, const float* values, float* key_base,
+                               float* value_base, std::size_t layer_stride, std::size_t layers,
+                               const PageGeometry& g, std::uint32_t block, std::size_t offset,
+                               hipStream_t stream);
+
+// Bulk layer-major append of `tokens` tokens.  layer_keys/layer_values are
+// device arrays of `layers` device pointers, each [kv_heads, tokens, dim].
+// blocks[i] is the physical block of logical block first_block + i.
+// `vectorized` selects 128-bit accesses (every layer pointer 16-byte aligned
+// and head_dim % 4 == 0, checked by the caller on the host copies).
+hipError_t launch_append_bulk(const float* const* layer_keys, const float* const* layer_values,
+                              float* key_base, float* value_base, std::size_t layer_stride,
+                              std::size_t layers, const PageGeometry& g,
+                              const std::uint32_t* blocks, std::size_t first_block,
+                              std::size_t old_length, std::size_t tokens, hipStream_t stream,
+                              bool vectorized);
+
+// Batched append into one layer: src [count, kv_heads, dim]; slots[i] is the
+// flat slot block * block_tokens + offset of row i (negative rows skipped).
+hipError_t launch_append_slots(const float* keys, const float* values, float* key_pool,
+                               float* value_pool, const PageGeometry& g, const std::int64_t* slots,
+                               std::size_t count, hipStream_t stream);
+
+// Gather one layer of one sequence into [kv_heads, dest_tokens, dim].
+hipError_t launch_gather(const float* key_pool, const float* value_pool, const PageGeometry& g,
+                         const std::uint32_t* blocks, std::size_t length, float* keys_out,
+                         float* values_out, std::size_t dest_tokens, hipStream_t stream);
+
+// Copy the first `tokens` token rows of block `from` into block `to` for
+// every layer and head (copy-on-write of a partial shared page).
+hipError_t launch_page_copy(float* key_base, float* value_base, std::size_t layer_stride,
+                            std::size_t layers, const PageGeometry& g, std::uint32_t from,
+                            std::uint32_t to, std::size_t tokens, hipStream_t stream);
+
+// Scatter (row, column, value) triples into a [rows, cols] uint32 table.
+hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
+                                const std::uint32_t* updates, std::size_t count,
+                                hipStream_t stream);
+
+// ------------------------------------------------------------- decode ----
+// Batched one-token decode with an uncommitted tail (split-K over pages).
+//   query      [batch, q_heads, 128]
+//   tables     [batch, max_blocks] physical block IDs
+//   lengths    [batch] committed history tokens per sequence
+//   tail_key / tail_value [batch, kv_heads, 128]
+//   out        [batch, q_heads, 128]
+//   workspace  decode_workspace_bytes(batch, q_heads, max_blocks) bytes
+struct DecodeArgs {
+  const float* query;
+  const float* key_pool;
+  const float* value_pool;
+  const std::uint32_t* tables;
+  const std::int32_t* lengths;
+  const float* tail_key;
+  const float* tail_value;
+  float* out;
+  void* workspace;
+  std::size_t batch;
+  std::size_t q_heads;
+  std::size_t kv_heads;
+  std::size_t max_blocks;
+  std::size_t physical_blocks;
+  std::size_t pages_per_split;
+};
+
+constexpr std::size_t kDecodeHeadDim = 128;
+constexpr std::size_t kDecodeBlockTokens = 16;
+
+std::size_t decode_max_splits(std::size_t max_blocks, std::size_t pages_per_split);
+std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t max_blocks,
+                                   std::size_t pages_per_split);
+bool decode_group_supported(std::size_t group);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
+
+// ------------------------------------------------------------ generic ----
+// Reference-shaped paged attention for any geometry (one query row per
+// workgroup).  Materialises probabilities into workspace [q_heads, queries,
+// history + tail] exactly like the reference's score workspace contract.
+struct GenericArgs {
+  const float* query;        // [q_heads, queries, key_dim]
+  const float* key_blocks;   // [physical, kv_heads, block_tokens, key_dim]
+  const float* value_blocks; // [physical, kv_heads, block_tokens, value_dim]
+  const std::uint32_t* table;
+  const float* tail_key;     // [kv_heads, tail, key_dim] or null
+  const float* tail_value;   // [kv_heads, tail, value_dim] or null
+  float* out;                // [q_heads, queries, value_dim]
+  float* workspace;          // [q_heads, queries, history + tail]
+  std::size_t q_heads, kv_heads, queries, key_dim, value_dim;
+  std::size_t block_tokens, physical_blocks;
+  std::size_t history, tail, offset;
+};
+
+hipError_t launch_generic(const GenericArgs& a, hipStream_t stream);
+
+// ------------------------------------------------------- chunked prefill ----
+// Causal attention of a `tokens`-row chunk per sequence over its paged
+// history plus the chunk itself (MFMA f32 path, head_dim 128, page 16).
+//   query [batch, q_heads, tokens, 128]; chunk_key/value [batch, kv_heads, tokens, 128]
+//   tables [batch, max_blocks]; lengths [batch] history tokens; out like query.
+struct PrefillArgs {
+  const float* query;
+  const float* key_pool;
+  const float* value_pool;
+  const std::uint32_t* tables;
+  const std::int32_t* lengths;
+  const float* chunk_key;
+  const float* chunk_value;
+  float* out;
+  std::size_t batch, q_heads, kv_heads, tokens, max_blocks, physical_blocks;
+};
+
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
+
+}  // namespace helix::hip

@@ -1,0 +1,189 @@
+// GPU-resident paged KV cache for one device (the MI355X counterpart of the
+// reference's CudaPagedKvCache, include/helix/kv_cache/cuda_paged.hpp:44-120)
+// with the CPU cache's sharing features (aligned fork with reference-counted
+// pages, src/kv_cache/paged.cpp:535-620) and a copy-on-write extension.
+//
+// HBM layout: one allocation holds every layer's key and value pool,
+// [layers][K|V][physical_blocks][kv_heads][block_tokens][head_dim] fp32, so
+// layer l's key pool is the reference's per-layer [N, H, P, D] tensor at
+// element offset (2l) * layer_elements and its value pool follows it.
+#pragma once
+
+#include "block_manager.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+namespace helix {
+
+// Owning device allocation.
+class DeviceBuffer {
+public:
+  DeviceBuffer() = default;
+  DeviceBuffer(std::size_t bytes, int device);
+  ~DeviceBuffer();
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  DeviceBuffer(DeviceBuffer&& o) noexcept;
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+  [[nodiscard]] void* data() const noexcept { return ptr_; }
+  [[nodiscard]] std::size_t size() const noexcept { return bytes_; }
+
+private:
+  void* ptr_ = nullptr;
+  std::size_t bytes_ = 0;
+};
+
+// Owning pinned host allocation (hipHostMalloc).
+class PinnedBuffer {
+public:
+  PinnedBuffer() = default;
+  explicit PinnedBuffer(std::size_t bytes);
+  ~PinnedBuffer();
+  PinnedBuffer(const PinnedBuffer&) = delete;
+  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+  PinnedBuffer(PinnedBuffer&& o) noexcept;
+  PinnedBuffer& operator=(PinnedBuffer&& o) noexcept;
+  [[nodiscard]] void* data() const noexcept { return ptr_; }
+
+private:
+  void* ptr_ = nullptr;
+};
+
+// Sets the device for the scope and restores the previous one.
+class DeviceGuard {
+public:
+  explicit DeviceGuard(int device);
+  ~DeviceGuard();
+
+private:
+  int previous_ = -1;
+};
+
+void hip_check(hipError_t e, const char* what);
+
+struct CacheState {
+  CacheState(const PagedConfig& config, int device);
+
+  BlockManager manager;
+  int device;
+  DeviceBuffer slab;
+  std::size_t layer_elements = 0;  // physical_blocks * kv_heads * block_tokens * head_dim
+  std::mutex mutex;
+  bool poisoned = false;
+  DeviceBuffer staging;            // transient upload area (grown on demand)
+
+  [[nodiscard]] float* key_pool(std::size_t layer) const {
+    return static_cast<float*>(slab.data()) + (2 * layer) * layer_elements;
+  }
+  [[nodiscard]] float* value_pool(std::size_t layer) const {
+    return static_cast<float*>(slab.data()) + (2 * layer + 1) * layer_elements;
+  }
+  [[nodiscard]] std::size_t layer_stride() const noexcept { return 2 * layer_elements; }
+  [[nodiscard]] bool overlaps_pool(const void* p, std::size_t bytes) const;
+  void require_healthy(const char* op) const;
+  void require_sequence(std::uint64_t id, std::uint64_t cache_id, const char* op) const;
+  void* staging_bytes(std::size_t bytes);
+};
+
+// Every operation takes the cache mutex for its whole duration.  Device work
+// is enqueued on the caller's stream and synchronised before metadata is
+// committed, as CudaPagedKvCache::append does (src/kv_cache/cuda_paged.cpp:
+// 557-611); a failed synchronisation poisons the cache.
+class DevicePagedCache {
+public:
+  DevicePagedCache(const PagedConfig& config, int device);
+
+  [[nodiscard]] const std::shared_ptr<CacheState>& state() const noexcept { return state_; }
+  [[nodiscard]] std::uint64_t cache_id() const noexcept { return state_->manager.cache_id(); }
+
+  std::uint64_t create_sequence();
+  std::uint64_t fork_sequence(std::uint64_t sequence, std::uint64_t cache_id, std::size_t prefix,
+                              bool allow_copy_on_write, hipStream_t stream);
+  void append(std::uint64_t sequence, std::uint64_t cache_id, const float* keys,
+              const float* values, hipStream_t stream);
+  void append_layer_major(std::uint64_t sequence, std::uint64_t cache_id,
+                          const float* const* layer_keys, const float* const* layer_values,
+                          std::size_t tokens, hipStream_t stream);
+  void release(std::uint64_t sequence, std::uint64_t cache_id);
+  // Gathers exactly `expected_length` tokens (or the current length when
+  // expected_length is SIZE_MAX) of one layer into [kv_heads, dest_tokens,
+  // head_dim] device buffers and synchronises the stream.
+  void copy_layer_out(std::uint64_t sequence, std::uint64_t cache_id, std::size_t layer,
+                      std::size_t expected_length, float* keys_out, float* values_out,
+                      std::size_t dest_tokens, hipStream_t stream);
+
+private:
+  std::shared_ptr<CacheState> state_;
+};
+
+// A read lease: holds the cache mutex and a device copy of one sequence's
+// block table (CudaPagedKvCache::DecodeView, cuda_paged.hpp:52-89).
+class DecodeView {
+public:
+  DecodeView(std::shared_ptr<CacheState> state, std::uint64_t sequence, std::uint64_t cache_id);
+  [[nodiscard]] std::size_t length() const;
+  [[nodiscard]] const std::vector<std::uint32_t>& physical_blocks() const;
+  [[nodiscard]] const std::uint32_t* device_table() const;
+  [[nodiscard]] float* key_pool(std::size_t layer) const;
+  [[nodiscard]] float* value_pool(std::size_t layer) const;
+  void poison() noexcept;
+
+private:
+  void require_valid(const char* op) const;
+  std::shared_ptr<CacheState> state_;
+  std::unique_lock<std::mutex> lock_;
+  std::size_t length_ = 0;
+  std::vector<std::uint32_t> blocks_;
+  DeviceBuffer table_;
+  bool valid_ = false;
+};
+
+// Batched decode driver: persistent device block tables [batch, max_blocks]
+// and history lengths for a fixed set of sequences, updated incrementally
+// each step (one pinned upload + one tiny kernel), plus the split-K
+// workspace.  prepare() reserves and commits one token slot per sequence;
+// append_layer() must then write that slot for every layer before the next
+// prepare().  Sequences of a live batch must not be released.
+class DecodeBatch {
+public:
+  DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t* sequences,
+              const std::uint64_t* cache_ids, std::size_t batch, std::size_t q_heads,
+              std::size_t max_tokens, std::size_t pages_per_split);
+  ~DecodeBatch();
+
+  void prepare(hipStream_t stream);
+  void append_layer(std::size_t layer, const float* keys, const float* values,
+                    hipStream_t stream) const;
+  void attention_layer(std::size_t layer, const float* query, const float* tail_key,
+                       const float* tail_value, float* out, hipStream_t stream) const;
+
+  [[nodiscard]] const std::uint32_t* tables() const;
+  [[nodiscard]] const std::int32_t* lengths() const;
+  [[nodiscard]] const std::int64_t* slots() const;
+  [[nodiscard]] std::size_t max_blocks() const noexcept { return max_blocks_; }
+  [[nodiscard]] std::size_t pages_per_split() const noexcept { return pages_per_split_; }
+  [[nodiscard]] std::size_t batch() const noexcept { return sequences_.size(); }
+
+private:
+  std::shared_ptr<CacheState> state_;
+  std::vector<std::uint64_t> sequences_;
+  std::size_t q_heads_;
+  std::size_t max_blocks_;
+  std::size_t pages_per_split_;
+  DeviceBuffer tables_;
+  DeviceBuffer step_;       // lengths [B] int32 | slots [B] int64 | updates
+  DeviceBuffer workspace_;
+  PinnedBuffer pinned_[2];
+  hipEvent_t uploaded_[2] = {nullptr, nullptr};
+  int next_pinned_ = 0;
+  std::size_t step_bytes_ = 0;
+  bool prepared_ = false;
+};
+
+}  // namespace helix

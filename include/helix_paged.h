@@ -1,0 +1,286 @@
+/*
+ * helix_paged.h -- C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Drop-in boundary for the reference's paged cache and paged attention
+ * (parthpandya5/helix-runtime).  Every entry point takes plain pointers and
+ * sizes; device pointers refer to HIP device memory of the cache's device;
+ * `stream` is a hipStream_t (NULL selects the null stream).  No exception
+ * crosses this boundary: every function returns a helix_status and stores a
+ * message retrievable with helix_last_error() on the calling thread.
+ *
+ * Citations are "reference file:line" of the interface each entry replaces.
+ */
+#ifndef HELIX_PAGED_H
+#define HELIX_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* helix::ErrorCode (include/helix/core/error.hpp:10-17) shifted by one so
+ * that zero means success. */
+typedef enum helix_status {
+  HELIX_OK = 0,
+  HELIX_INVALID_ARGUMENT = 1,
+  HELIX_OUT_OF_RANGE = 2,
+  HELIX_UNSUPPORTED = 3,
+  HELIX_RESOURCE_EXHAUSTED = 4,
+  HELIX_RUNTIME = 5,
+  HELIX_INTERNAL = 6
+} helix_status;
+
+typedef void* helix_stream; /* hipStream_t */
+
+/* PagedKvCacheConfig (include/helix/kv_cache/paged.hpp:60-66). */
+typedef struct helix_paged_config {
+  size_t layers;
+  size_t kv_heads;
+  size_t head_dimension;
+  size_t block_tokens;
+  size_t physical_blocks;
+} helix_paged_config;
+
+/* PagedKvCacheStats (include/helix/kv_cache/paged.hpp:68-107), 64-bit. */
+typedef struct helix_paged_stats {
+  uint64_t bytes_reserved, bytes_used, bytes_free, peak_bytes_used;
+  uint64_t total_blocks, used_blocks, free_blocks, active_sequence_count;
+  uint64_t active_tokens, resident_tokens, allocated_token_slots;
+  uint64_t block_reference_count, shared_blocks;
+  uint64_t sequence_create_count, sequence_fork_count, append_count, release_count;
+  uint64_t block_allocation_count, block_reuse_count;
+} helix_paged_stats;
+
+/* PagedSequenceHandle / CudaPagedSequenceHandle
+ * (include/helix/kv_cache/paged.hpp:34-58, cuda_paged.hpp:18-42). id 0 is
+ * the empty handle. */
+typedef struct helix_sequence {
+  uint64_t id;
+  uint64_t cache_id;
+} helix_sequence;
+
+/* Copy-on-write page copy a fork implies (extension; no reference
+ * counterpart, docs/KV_CACHE.md:247): tokens == 0 when none. */
+typedef struct helix_cow_copy {
+  uint32_t from_block;
+  uint32_t to_block;
+  size_t tokens;
+} helix_cow_copy;
+
+typedef struct helix_block_manager helix_block_manager;
+typedef struct helix_paged_cache helix_paged_cache;
+typedef struct helix_decode_view helix_decode_view;
+typedef struct helix_block_table helix_block_table;
+typedef struct helix_decode_batch helix_decode_batch;
+
+/* ----------------------------------------------------------- errors ---- */
+/* Message of the last failed call on this thread ("" after success). */
+const char* helix_last_error(void);
+/* helix::error_code_name (include/helix/core/error.hpp:19). */
+const char* helix_status_name(int status);
+
+/* ---------------------------------------------- host page bookkeeping ---- */
+/* The metadata half of PagedKvCache (src/kv_cache/paged.cpp), usable without
+ * a device: FIFO allocation, block tables, reference counts, statistics. */
+int helix_block_manager_create(const helix_paged_config* config, helix_block_manager** out);
+void helix_block_manager_destroy(helix_block_manager* manager);
+/* PagedKvCache::create_sequence (paged.cpp:509-533). */
+int helix_block_manager_create_sequence(helix_block_manager* m, helix_sequence* out);
+/* PagedKvCache::fork_sequence (paged.cpp:535-620); allow_cow != 0 accepts a
+ * non-aligned prefix and reports the page copy the caller must perform. */
+int helix_block_manager_fork_sequence(helix_block_manager* m, helix_sequence source,
+                                      size_t prefix_tokens, int allow_cow, helix_sequence* out,
+                                      helix_cow_copy* copy);
+/* Appends `tokens` tokens (paged.cpp:622-719, 721-871); writes each token's
+ * physical slot block * block_tokens + offset into slots (may be NULL). */
+int helix_block_manager_append(helix_block_manager* m, helix_sequence sequence, size_t tokens,
+                               uint64_t* slots);
+/* PagedKvCache::release_sequence (paged.cpp:952-1001). */
+int helix_block_manager_release_sequence(helix_block_manager* m, helix_sequence sequence);
+int helix_block_manager_contains(const helix_block_manager* m, helix_sequence sequence, int* out);
+int helix_block_manager_length(const helix_block_manager* m, helix_sequence sequence,
+                               size_t* out);
+/* PagedKvCache::block_table (paged.cpp:1014-1023): writes min(count,
+ * capacity) IDs and the full count. */
+int helix_block_manager_block_table(const helix_block_manager* m, helix_sequence sequence,
+                                    uint32_t* out, size_t capacity, size_t* count);
+int helix_block_manager_stats(const helix_block_manager* m, helix_paged_stats* out);
+int helix_block_manager_block_info(const helix_block_manager* m, uint32_t block,
+                                   size_t* reference_count, size_t* token_count);
+/* Re-derives every invariant (paged.cpp:282-393); HELIX_INTERNAL on failure. */
+int helix_block_manager_validate(const helix_block_manager* m);
+/* bytes_per_token / block_bytes / token_capacity (paged.cpp:1035-1045). */
+int helix_block_manager_geometry(const helix_block_manager* m, size_t* bytes_per_token,
+                                 size_t* block_bytes, size_t* token_capacity);
+
+/* ------------------------------------------------------ device cache ---- */
+/* CudaPagedKvCache (include/helix/kv_cache/cuda_paged.hpp:91-116, src/kv_cache/
+ * cuda_paged.cpp:454-697) plus the CPU cache's fork and bulk append. */
+int helix_paged_cache_create(const helix_paged_config* config, int device,
+                             helix_paged_cache** out);
+void helix_paged_cache_destroy(helix_paged_cache* cache);
+int helix_paged_cache_create_sequence(helix_paged_cache* cache, helix_sequence* out);
+/* PagedKvCache::fork_sequence (paged.cpp:535-620); allow_cow != 0 copies a
+ * partial last page on the device (extension). */
+int helix_paged_cache_fork_sequence(helix_paged_cache* cache, helix_sequence source,
+                                    size_t prefix_tokens, int allow_cow, helix_stream stream,
+                                    helix_sequence* out);
+/* CudaPagedKvCache::append (cuda_paged.cpp:491-611): token_keys/values are
+ * device [layers, kv_heads, head_dim]; one kernel, then a stream sync, then
+ * the metadata commit. */
+int helix_paged_cache_append(helix_paged_cache* cache, helix_sequence sequence,
+                             const float* token_keys, const float* token_values,
+                             helix_stream stream);
+/* PagedKvCache::append_layer_major (paged.cpp:721-871): host arrays of
+ * `layers` device pointers, each [kv_heads, tokens, head_dim]. */
+int helix_paged_cache_append_layer_major(helix_paged_cache* cache, helix_sequence sequence,
+                                         const float* const* layer_keys,
+                                         const float* const* layer_values, size_t tokens,
+                                         helix_stream stream);
+/* CudaPagedKvCache::release_sequence (cuda_paged.cpp:613-643). */
+int helix_paged_cache_release_sequence(helix_paged_cache* cache, helix_sequence sequence);
+/* PagedKvCache::copy_layer_out (paged.cpp:887-893): device outputs
+ * [kv_heads, length, head_dim]; synchronises the stream. */
+int helix_paged_cache_copy_layer_out(helix_paged_cache* cache, helix_sequence sequence,
+                                     size_t layer, float* keys_out, float* values_out,
+                                     helix_stream stream);
+/* PagedKvCache::copy_layer_prefix_out (paged.cpp:895-950): outputs
+ * [kv_heads, dest_tokens, head_dim], trailing rows untouched. */
+int helix_paged_cache_copy_layer_prefix_out(helix_paged_cache* cache, helix_sequence sequence,
+                                            size_t layer, size_t expected_length,
+                                            float* keys_out, float* values_out,
+                                            size_t dest_tokens, helix_stream stream);
+int helix_paged_cache_contains(helix_paged_cache* cache, helix_sequence sequence, int* out);
+int helix_paged_cache_length(helix_paged_cache* cache, helix_sequence sequence, size_t* out);
+int helix_paged_cache_block_table(helix_paged_cache* cache, helix_sequence sequence,
+                                  uint32_t* out, size_t capacity, size_t* count);
+int helix_paged_cache_stats(helix_paged_cache* cache, helix_paged_stats* out);
+/* CudaPagedKvCache::is_healthy (cuda_paged.cpp:656-659). */
+int helix_paged_cache_is_healthy(helix_paged_cache* cache, int* out);
+int helix_paged_cache_geometry(helix_paged_cache* cache, size_t* bytes_per_token,
+                               size_t* block_bytes, size_t* token_capacity);
+/* Device pools of one layer, each [physical_blocks, kv_heads, block_tokens,
+ * head_dim] (DecodeView::layer_key_blocks / layer_value_blocks). */
+int helix_paged_cache_layer_pools(helix_paged_cache* cache, size_t layer, float** key_blocks,
+                                  float** value_blocks);
+
+/* CudaPagedKvCache::read_sequence / DecodeView (cuda_paged.cpp:377-452,
+ * 645-654).  The view holds the cache mutex until released, from the same
+ * thread; append and release block meanwhile. */
+int helix_paged_cache_read_sequence(helix_paged_cache* cache, helix_sequence sequence,
+                                    helix_decode_view** out);
+int helix_decode_view_length(const helix_decode_view* view, size_t* out);
+int helix_decode_view_physical_blocks(const helix_decode_view* view, const uint32_t** blocks,
+                                      size_t* count);
+/* Device copy of the block table (NULL for an empty sequence). */
+int helix_decode_view_block_table(const helix_decode_view* view, const uint32_t** device_table);
+int helix_decode_view_layer_pools(const helix_decode_view* view, size_t layer,
+                                  float** key_blocks, float** value_blocks);
+/* DecodeView::poison_after_consumer_failure (cuda_paged.cpp:441-452). */
+void helix_decode_view_poison(helix_decode_view* view);
+void helix_decode_view_release(helix_decode_view* view);
+
+/* PagedBlockTable (include/helix/kv_cache/cuda_block_table.hpp:134-169,
+ * src/kv_cache/cuda_block_table.cpp:22-47): validates every ID against
+ * physical_block_count, then uploads synchronously.  Empty tables own no
+ * device memory and report a NULL data pointer. */
+int helix_block_table_create(const uint32_t* physical_blocks, size_t count,
+                             size_t physical_block_count, int device, helix_block_table** out);
+const uint32_t* helix_block_table_data(const helix_block_table* table);
+size_t helix_block_table_logical_block_count(const helix_block_table* table);
+void helix_block_table_destroy(helix_block_table* table);
+
+/* ------------------------------------------- reference-shaped attention ---- */
+/* Shapes (the reference's attention::cuda contract, include/helix/attention/
+ * cuda_paged.hpp:186-240):
+ *   query        [q_heads, queries, key_dim]
+ *   key_blocks   [physical_blocks, kv_heads, block_tokens, key_dim]
+ *   value_blocks [physical_blocks, kv_heads, block_tokens, value_dim]
+ *   block_table  logical_blocks device uint32 IDs
+ *   workspace    [q_heads, queries, kv_tokens] -- receives probabilities
+ *   output       [q_heads, queries, value_dim]
+ * q_heads must be a multiple of kv_heads (the reference requires equality;
+ * grouped-query attention is an extension). */
+
+/* paged_score_workspace_bytes (cuda_paged.cu:381-394): validates the
+ * history-only geometry and returns q_heads * queries * kv_tokens * 4. */
+int helix_paged_score_workspace_bytes(size_t q_heads, size_t queries, size_t kv_heads,
+                                      size_t physical_blocks, size_t block_tokens,
+                                      size_t logical_blocks, size_t kv_tokens, size_t* out);
+/* paged_tail_score_workspace_bytes (cuda_paged.cu:396-418). */
+int helix_paged_tail_score_workspace_bytes(size_t q_heads, size_t tail_tokens, size_t kv_heads,
+                                           size_t physical_blocks, size_t block_tokens,
+                                           size_t logical_blocks, size_t history_tokens,
+                                           size_t* out);
+/* paged_scaled_dot_product_attention_out (cuda_paged.cu:420-481). */
+int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries, size_t key_dim,
+                              const float* key_blocks, const float* value_blocks,
+                              size_t physical_blocks, size_t kv_heads, size_t block_tokens,
+                              size_t value_dim, const uint32_t* block_table,
+                              size_t logical_blocks, size_t kv_tokens,
+                              size_t query_position_offset, float* output,
+                              float* score_workspace, size_t workspace_elements,
+                              helix_stream stream);
+/* paged_scaled_dot_product_attention_with_tail_out (cuda_paged.cu:483-548):
+ * tail_key [kv_heads, tail_tokens, key_dim], tail_value [kv_heads,
+ * tail_tokens, value_dim]; query row q sees the history and tail rows 0..q. */
+int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size_t tail_tokens,
+                                        size_t key_dim, const float* key_blocks,
+                                        const float* value_blocks, size_t physical_blocks,
+                                        size_t kv_heads, size_t block_tokens, size_t value_dim,
+                                        const uint32_t* block_table, size_t logical_blocks,
+                                        size_t history_tokens, const float* tail_key,
+                                        const float* tail_value, float* output,
+                                        float* score_workspace, size_t workspace_elements,
+                                        helix_stream stream);
+
+/* -------------------------------------------- batched decode (extension) ---- */
+/* One-token decode for `batch` sequences at once (the reference runs one
+ * sequence per call, docs/ATTENTION.md:317), head_dim 128, 16-token pages,
+ * q_heads / kv_heads in {1, 2, 4, 8}:
+ *   query [batch, q_heads, 128]; tables [batch, max_blocks] uint32;
+ *   lengths [batch] int32 history tokens; tail_key/value [batch, kv_heads, 128];
+ *   output [batch, q_heads, 128].
+ * pages_per_split == 0 selects the default split size. */
+int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t max_blocks,
+                                       size_t pages_per_split, size_t* out);
+int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
+                                 size_t kv_heads, const float* key_blocks,
+                                 const float* value_blocks, size_t physical_blocks,
+                                 const uint32_t* tables, size_t max_blocks,
+                                 const int32_t* lengths, const float* tail_key,
+                                 const float* tail_value, float* output, void* workspace,
+                                 size_t workspace_bytes, size_t pages_per_split,
+                                 helix_stream stream);
+/* Writes rows [count, kv_heads, head_dim] of keys/values into one layer's
+ * pools at slots[i] = block * block_tokens + offset (negative: skipped). */
+int helix_paged_append_slots(const float* keys, const float* values, float* key_blocks,
+                             float* value_blocks, size_t physical_blocks, size_t kv_heads,
+                             size_t block_tokens, size_t head_dim, const int64_t* slots,
+                             size_t count, helix_stream stream);
+
+/* A decode driver over a cache: persistent device block tables for a fixed
+ * set of sequences.  prepare() reserves one slot per sequence (allocating
+ * pages), append_layer() writes it, attention_layer() attends over the
+ * history before the step plus the tail. */
+int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* sequences,
+                              size_t batch, size_t q_heads, size_t max_tokens,
+                              size_t pages_per_split, helix_decode_batch** out);
+int helix_decode_batch_prepare(helix_decode_batch* b, helix_stream stream);
+int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
+                                    const float* values, helix_stream stream);
+int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
+                                       const float* tail_key, const float* tail_value,
+                                       float* output, helix_stream stream);
+int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tables,
+                              const int32_t** lengths, const int64_t** slots,
+                              size_t* max_blocks, size_t* pages_per_split);
+void helix_decode_batch_destroy(helix_decode_batch* b);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELIX_PAGED_H */

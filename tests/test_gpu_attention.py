@@ -1,0 +1,316 @@
+"""GPU paged attention against the CPU oracle.
+
+Tolerance: the north-star bound, max-abs 2e-5 plus rel 1e-4, for outputs of
+the batched decode kernel; the reference's own GPU-test bound 2e-5 + D * 1e-6
+on outputs and 2e-6 on probabilities for the reference-shaped entry points
+(tests/cuda_attention_test.cpp:227,270,441-443)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import helix_runtime_amd as hx
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-5, 1e-4
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to("cuda:0")
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def reversed_table(logical, physical):
+    return np.array([physical - 1 - i for i in range(logical)], np.uint32)
+
+
+def run_tail(q, kp, vp, table, hist, tk, tv):
+    hq, t, _ = q.shape
+    dv = vp.shape[-1]
+    out = torch.empty(hq, t, dv, device="cuda:0")
+    ws = torch.empty(hq, t, hist + t, device="cuda:0")
+    tab = dev(table.astype(np.int32)) if len(table) else torch.zeros(1, dtype=torch.int32,
+                                                                      device="cuda:0")
+    hx.paged_attention_with_tail_out(dev(q), dev(kp), dev(vp), tab if len(table) else 0, hist,
+                                     dev(tk), dev(tv), out, ws)
+    torch.cuda.synchronize()
+    return host(out), host(ws)
+
+
+def run_history(q, kp, vp, table, kv_tokens, offset):
+    hq, nq, _ = q.shape
+    dv = vp.shape[-1]
+    out = torch.empty(hq, nq, dv, device="cuda:0")
+    ws = torch.empty(hq, nq, kv_tokens, device="cuda:0")
+    hx.paged_attention_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), kv_tokens,
+                           offset, out, ws)
+    torch.cuda.synchronize()
+    return host(out), host(ws)
+
+
+# ------------------------------------------------ reference-shaped API ----
+def test_known_reordered_blocks_ignore_poisoned_padding(device):
+    # tests/cuda_attention_test.cpp:196-228
+    table = np.array([2, 0], np.uint32)
+    q = np.array([[[1, 0], [0, 1]]], np.float32)
+    k = np.array([[[1, 0], [0, 1], [1, 1]]], np.float32)
+    v = np.array([[[10, 1, -1], [20, 2, -2], [30, 3, -3]]], np.float32)
+    kp = oracle.pack_logical_blocks(k, table, 3, 2, 10000.0)
+    vp = oracle.pack_logical_blocks(v, table, 3, 2, -10000.0)
+    out, ws = run_history(q, kp, vp, table, 3, 1)
+    exp_out, exp_ws = oracle.sdpa(q, k, v, 1)
+    np.testing.assert_allclose(out, exp_out, atol=2e-5, rtol=0)
+    np.testing.assert_allclose(ws, exp_ws, atol=2e-6, rtol=0)
+
+
+@pytest.mark.parametrize("h,nq,nk,d,dv,p", [(1, 1, 3, 1, 2, 2), (2, 3, 5, 5, 7, 2),
+                                             (3, 7, 11, 37, 41, 4)])
+def test_history_odd_shapes(device, h, nq, nk, d, dv, p):
+    # tests/cuda_attention_test.cpp:230-273 (seeds 8101-8103, padding +-77)
+    logical = (nk - 1) // p + 1
+    phys = logical + 2
+    table = reversed_table(logical, phys)
+    q = oracle.random_uniform((h, nq, d), 8101)
+    k = oracle.random_uniform((h, nk, d), 8102)
+    v = oracle.random_uniform((h, nk, dv), 8103)
+    kp = oracle.pack_logical_blocks(k, table, phys, p, 77.0)
+    vp = oracle.pack_logical_blocks(v, table, phys, p, -77.0)
+    out, ws = run_history(q, kp, vp, table, nk, nk - nq)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, nk, query_position_offset=nk - nq)
+    np.testing.assert_allclose(out, exp_out, atol=2e-5 + d * 1e-6, rtol=0)
+    np.testing.assert_allclose(ws, exp_ws, atol=2e-6, rtol=0)
+
+
+@pytest.mark.parametrize("h,hist,tail,d,dv,p", [(1, 0, 1, 1, 2, 2), (2, 3, 1, 5, 7, 2),
+                                                 (3, 5, 3, 37, 41, 4)])
+def test_tail_odd_shapes(device, h, hist, tail, d, dv, p):
+    # tests/cuda_attention_test.cpp:376-449 (seeds 8201-8205, padding +-10000)
+    logical = 0 if hist == 0 else (hist - 1) // p + 1
+    phys = logical + 2
+    table = reversed_table(logical, phys)
+    q = oracle.random_uniform((h, tail, d), 8201)
+    hk = oracle.random_uniform((h, hist, d), 8202)
+    hv = oracle.random_uniform((h, hist, dv), 8203)
+    tk = oracle.random_uniform((h, tail, d), 8204)
+    tv = oracle.random_uniform((h, tail, dv), 8205)
+    kp = oracle.pack_logical_blocks(hk, table, phys, p, 1e4)
+    vp = oracle.pack_logical_blocks(hv, table, phys, p, -1e4)
+    out, ws = run_tail(q, kp, vp, table, hist, tk, tv)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    np.testing.assert_allclose(out, exp_out, atol=2e-5 + d * 1e-6, rtol=0)
+    np.testing.assert_allclose(ws, exp_ws, atol=2e-6, rtol=0)
+
+
+def test_tail_causal_mask_does_not_read_future_nan(device):
+    # tests/cuda_attention_test.cpp:533-554
+    nan = np.nan
+    q = np.zeros((1, 2, 1), np.float32)
+    kp = np.zeros((1, 1, 2, 1), np.float32)
+    tk = np.array([[[0.0], [nan]]], np.float32)
+    tv = np.array([[[3.0], [nan]]], np.float32)
+    out, ws = run_tail(q, kp, kp, np.zeros(0, np.uint32), 0, tk, tv)
+    assert out.ravel()[0] == 3.0 and np.isnan(out.ravel()[1])
+    assert ws.ravel()[0] == 1.0 and ws.ravel()[1] == 0.0
+
+
+def test_gqa_generic_matches_oracle(device):
+    hq, hkv, d, p, hist, t = 8, 2, 24, 4, 19, 3
+    logical = (hist - 1) // p + 1
+    table = np.random.default_rng(3).permutation(logical + 3)[:logical].astype(np.uint32)
+    kp = oracle.random_normal((logical + 3, hkv, p, d), 1)
+    vp = oracle.random_normal((logical + 3, hkv, p, d), 2)
+    q = oracle.random_normal((hq, t, d), 3)
+    tk = oracle.random_normal((hkv, t, d), 4)
+    tv = oracle.random_normal((hkv, t, d), 5)
+    out, ws = run_tail(q, kp, vp, table, hist, tk, tv)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=2e-6, rtol=0)
+
+
+def test_reference_contract_errors(device):
+    # tests/cuda_attention_test.cpp:290-374 (the checks that survive the
+    # pointer-and-size boundary)
+    q = torch.zeros(1, 2, 2, device=device)
+    kb = torch.zeros(3, 1, 2, 2, device=device)
+    vb = torch.zeros(3, 1, 2, 2, device=device)
+    out = torch.zeros(1, 2, 2, device=device)
+    ws = torch.zeros(1, 2, 3, device=device)
+    table = dev(np.array([2, 0], np.int32))
+    lib = hx.load()
+    base = dict(query=q, key_blocks=kb, value_blocks=vb, block_table=table)
+
+    def call(kv_tokens=3, offset=1, output=out, workspace=ws, logical=2, key_blocks=kb,
+             value_blocks=vb, query=q):
+        return lib.helix_paged_attention_out(
+            query.data_ptr(), query.shape[0], query.shape[1], query.shape[2],
+            key_blocks.data_ptr(), value_blocks.data_ptr(), key_blocks.shape[0],
+            key_blocks.shape[1], key_blocks.shape[2], value_blocks.shape[3], table.data_ptr(),
+            logical, kv_tokens, offset, output.data_ptr(), workspace.data_ptr(),
+            workspace.numel(), None)
+
+    assert call() == 0
+    assert call(logical=1) == hx.INVALID_ARGUMENT          # short table
+    assert call(kv_tokens=0, offset=0, logical=0) == hx.INVALID_ARGUMENT
+    assert call(offset=2) == hx.INVALID_ARGUMENT          # query range past the keys
+    assert call(output=q) == hx.INVALID_ARGUMENT          # output aliases query
+    ws5 = torch.zeros(1, 2, 3, device=device)
+    assert call(output=ws5, workspace=ws5) == hx.INVALID_ARGUMENT
+    assert call(workspace=torch.zeros(1, 2, 2, device=device)) == hx.INVALID_ARGUMENT
+    torch.cuda.synchronize()
+    bad = hx.PagedBlockTable([2, 0], 3)
+    assert bad.logical_block_count == 2
+    with pytest.raises(hx.HelixError) as e:
+        hx.PagedBlockTable([3], 3)
+    assert e.value.status == hx.OUT_OF_RANGE
+    with pytest.raises(hx.HelixError):
+        hx.PagedBlockTable([], 0)
+    empty = hx.PagedBlockTable([], 3)
+    assert empty.data() is None
+
+
+def test_zero_queries_launch_nothing(device):
+    # tests/cuda_attention_test.cpp:275-288
+    q = torch.zeros(2, 0, 5, device=device)
+    kb = torch.zeros(4, 2, 3, 5, device=device)
+    vb = torch.zeros(4, 2, 3, 7, device=device)
+    out = torch.zeros(2, 0, 7, device=device)
+    ws = torch.zeros(2, 0, 7, device=device)
+    table = dev(np.array([3, 1, 0], np.int32))
+    hx.paged_attention_out(q, kb, vb, table, 7, 7, out, ws)
+    n = ctypes_size()
+    assert hx.load().helix_paged_score_workspace_bytes(2, 0, 2, 4, 3, 3, 7, n) == 0
+    assert n._obj.value == 0
+
+
+def ctypes_size():
+    import ctypes
+    return ctypes.byref(ctypes.c_size_t())
+
+
+# -------------------------------------------------------- batched decode ----
+def make_decode_problem(seed, batch, hq, hkv, lengths, spare=1.25, d=128, p=16):
+    rng = np.random.default_rng(seed)
+    pages = [(int(n) + p - 1) // p for n in lengths]
+    need = sum(pages)
+    n_phys = max(1, int(math.ceil(need * spare)))
+    perm = rng.permutation(n_phys).astype(np.uint32)
+    max_blocks = max(1, max(pages))
+    tables = np.zeros((batch, max_blocks), np.uint32)
+    off = 0
+    for b in range(batch):
+        tables[b, : pages[b]] = perm[off: off + pages[b]]
+        off += pages[b]
+    kp = rng.standard_normal((n_phys, hkv, p, d), dtype=np.float32)
+    vp = rng.standard_normal((n_phys, hkv, p, d), dtype=np.float32)
+    q = rng.standard_normal((batch, hq, d), dtype=np.float32)
+    tk = rng.standard_normal((batch, hkv, d), dtype=np.float32)
+    tv = rng.standard_normal((batch, hkv, d), dtype=np.float32)
+    return q, kp, vp, tables, np.asarray(lengths, np.int32), tk, tv
+
+
+def run_decode(q, kp, vp, tables, lengths, tk, tv, pages_per_split=0):
+    b, hq, d = q.shape
+    out = torch.empty(b, hq, d, device="cuda:0")
+    nbytes = hx.decode_workspace_bytes(b, hq, tables.shape[1], pages_per_split)
+    ws = torch.empty(max(1, nbytes // 4), device="cuda:0")
+    hx.paged_decode_attention(dev(q), dev(kp), dev(vp), dev(tables.astype(np.int32)),
+                              dev(lengths), dev(tk), dev(tv), out, ws, pages_per_split)
+    torch.cuda.synchronize()
+    return host(out)
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (32, 8), (64, 8)])
+def test_decode_groups_match_oracle(device, hq, hkv):
+    lengths = [0, 1, 15, 16, 17, 100, 255, 256, 1000]
+    prob = make_decode_problem(7, len(lengths), hq, hkv, lengths)
+    out = run_decode(*prob)
+    ref = oracle.batched_decode(*prob, threads=8)
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 8, 64])
+def test_decode_split_sizes_agree(device, split):
+    lengths = [5, 33, 160, 481, 1500, 2049]
+    prob = make_decode_problem(11, len(lengths), 32, 8, lengths)
+    out = run_decode(*prob, pages_per_split=split)
+    ref = oracle.batched_decode(*prob, threads=8)
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_config2_llama2_mha_decode(device):
+    # B8, 32/32 heads, D128, P16, ctx ~U[128, 2048], pool 1.25x.
+    rng = np.random.default_rng(2)
+    lengths = rng.integers(128, 2049, size=8)
+    prob = make_decode_problem(2, 8, 32, 32, lengths)
+    out = run_decode(*prob)
+    ref = oracle.batched_decode(*prob, threads=8)
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_config3_shape_sampled_decode(device):
+    # BASELINE config 3 shape (32/8 heads, ctx log-uniform [512, 8192]) on 8 sequences.
+    rng = np.random.default_rng(3)
+    lengths = np.exp(rng.uniform(np.log(512), np.log(8192), size=8)).astype(np.int64)
+    prob = make_decode_problem(3, 8, 32, 8, lengths)
+    out = run_decode(*prob)
+    ref = oracle.batched_decode(*prob, threads=8)
+    np.testing.assert_allclose(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_decode_is_deterministic(device):
+    prob = make_decode_problem(5, 4, 32, 8, [700, 3000, 64, 1])
+    a = run_decode(*prob)
+    b = run_decode(*prob)
+    assert np.array_equal(a, b)
+
+
+def test_decode_special_values_follow_reference_softmax(device):
+    # src/kernels/cpu/reference.cpp:264-316 -- +inf scores share the mass,
+    # NaN scores poison the row, out-of-range pages give NaN.
+    q, kp, vp, tables, lengths, tk, tv = make_decode_problem(9, 4, 4, 4, [40, 40, 40, 40])
+    q[:] = 1.0
+    kp = kp.copy()
+    # sequence 0 head 0: two +inf keys (tokens 3 and 20)
+    for tok in (3, 20):
+        kp[tables[0, tok // 16], 0, tok % 16, 0] = np.inf
+        kp[tables[0, tok // 16], 0, tok % 16, 1:] = 0.0
+    # sequence 1 head 1: a NaN key at token 30
+    kp[tables[1, 30 // 16], 1, 30 % 16, 5] = np.nan
+    # sequence 2: a corrupt page ID
+    tables = tables.copy()
+    tables[2, 1] = 10_000
+    out = run_decode(q, kp, vp, tables, lengths, tk, tv)
+    tables_ok = tables.copy()
+    tables_ok[2, 1] = tables[3, 0]
+    ref = oracle.batched_decode(q, kp, vp, tables_ok, lengths, tk, tv)
+    expected0 = 0.5 * (vp[tables[0, 0], 0, 3] + vp[tables[0, 1], 0, 4])
+    np.testing.assert_allclose(out[0, 0], expected0, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ref[0, 0], expected0, atol=ATOL, rtol=RTOL)
+    assert np.isnan(out[1, 1]).all() and np.isnan(ref[1, 1]).all()
+    assert np.isnan(out[2]).all()
+    np.testing.assert_allclose(out[3], ref[3], atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(out[1, [0, 2, 3]], ref[1, [0, 2, 3]], atol=ATOL, rtol=RTOL)
+
+
+def test_decode_rejects_bad_arguments(device):
+    q, kp, vp, tables, lengths, tk, tv = make_decode_problem(1, 2, 12, 4, [10, 20])
+    with pytest.raises(hx.HelixError) as e:
+        run_decode(q, kp, vp, tables, lengths, tk, tv)  # group of 3
+    assert e.value.status == hx.UNSUPPORTED
+    q, kp, vp, tables, lengths, tk, tv = make_decode_problem(1, 2, 8, 4, [10, 20])
+    out = torch.empty(2, 8, 128, device=device)
+    small = torch.empty(1, device=device)
+    with pytest.raises(hx.HelixError):
+        hx.paged_decode_attention(dev(q), dev(kp), dev(vp), dev(tables.astype(np.int32)),
+                                  dev(lengths), dev(tk), dev(tv), out, small, 1)

@@ -1,0 +1,103 @@
+"""The batched decode driver end to end: per step prepare (slot reservation
+and incremental device tables), per layer append of the current token and
+attention over the pre-step history plus the tail.  Outputs are checked
+against the oracle per step and layer; the pages written by the appends are
+checked bit-exactly against the oracle pool afterwards."""
+
+import numpy as np
+import pytest
+import torch
+
+import helix_runtime_amd as hx
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-5, 1e-4
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("hq", [8, 32])
+def test_decode_batch_steps_match_oracle(device, hq):
+    L, H, D, P = 2, 8, 128, 16
+    rng = np.random.default_rng(hq)
+    lengths = [1, 15, 16, 31, 47, 200]
+    N = sum((n + 8) // P + 2 for n in lengths) + 8
+    cache = hx.PagedKvCache(L, H, D, P, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for n in lengths:
+        s, so = cache.create_sequence(), pool.create_sequence()
+        k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        cache.append_layer_major(s, [dev(k[l]) for l in range(L)], [dev(v[l]) for l in range(L)])
+        pool.append_layer_major(so, k, v)
+        seqs.append((s, so))
+    # a bystander sequence keeps allocating between steps (FIFO interleaving)
+    other, other_o = cache.create_sequence(), pool.create_sequence()
+    B = len(seqs)
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], hq, max_tokens=256)
+    for step in range(3):
+        tok = np.zeros((1, L, H, 1, D), np.float32)
+        cache.append_layer_major(other, [dev(tok[0, l]) for l in range(L)],
+                                 [dev(tok[0, l]) for l in range(L)])
+        pool.append_layer_major(other_o, tok[0], tok[0])
+        batch.prepare()
+        hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+        max_blocks = batch.device_state()["max_blocks"]
+        tables = np.zeros((B, max_blocks), np.uint32)
+        keys = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        values = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        for layer in range(L):
+            q = rng.standard_normal((B, hq, D), dtype=np.float32)
+            out = torch.empty(B, hq, D, device=device)
+            batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+            batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            torch.cuda.synchronize()
+            kp, vp = pool.layer_pages(layer)
+            for b, (_, so) in enumerate(seqs):
+                t = pool.block_table(so)
+                tables[b, : len(t)] = t
+            ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
+                                        threads=8)
+            np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+        for b, (_, so) in enumerate(seqs):
+            pool.append(so, keys[:, b], values[:, b])
+        assert cache.stats() == pool.stats()
+    for s, so in seqs:
+        assert cache.block_table(s) == pool.block_table(so).tolist()
+        for layer in range(L):
+            gk, gv = cache.retrieve_layer(s, layer)
+            ok, ov = pool.copy_layer(so, layer)
+            np.testing.assert_array_equal(host(gk), ok)
+            np.testing.assert_array_equal(host(gv), ov)
+    batch.close()
+
+
+def test_decode_batch_validates(device):
+    cache = hx.PagedKvCache(1, 2, 128, 16, 8)
+    s = cache.create_sequence()
+    with pytest.raises(hx.HelixError) as e:
+        hx.DecodeBatch(cache, [s], 6, max_tokens=64)
+    assert e.value.status == hx.UNSUPPORTED
+    with pytest.raises(hx.HelixError):
+        hx.DecodeBatch(cache, [s, s], 4, max_tokens=64)
+    odd = hx.PagedKvCache(1, 2, 64, 16, 8)
+    with pytest.raises(hx.HelixError) as e:
+        hx.DecodeBatch(odd, [odd.create_sequence()], 4, max_tokens=64)
+    assert e.value.status == hx.UNSUPPORTED
+    b = hx.DecodeBatch(cache, [s], 4, max_tokens=17)
+    x = torch.zeros(1, 2, 128, device=device)
+    with pytest.raises(hx.HelixError):
+        b.append_layer(0, x, x)  # before prepare
+    b.prepare()
+    with pytest.raises(hx.HelixError):
+        b.append_layer(1, x, x)  # layer out of range
+    b.close()
