@@ -134,6 +134,24 @@ def cpu_baseline(cache, seqs, layers_sample, threads, seed):
     return total_bytes / total_time / 1e9, total_time, max_err
 
 
+def copy_probe(nbytes=1 << 30, reps=10):
+    """Streaming copy of a known size: reads nbytes and writes nbytes per launch."""
+    src = torch.randn(nbytes // 4, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes,
+                      "avg_ms": round(ms, 4), "gbps_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,6 +163,8 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (HBM probe / counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -154,6 +174,9 @@ def main():
         sys.exit(2)
 
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        copy_probe()
+        return
     steps_total = args.warmup + args.steps + 2
     t_setup = time.perf_counter()
     cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total)

@@ -285,7 +285,7 @@ class DecodeView:
         self._cache = cache
 
     def release(self):
-        if self._h:
+        if getattr(self, "_h", None):
             _lib().helix_decode_view_release(self._h)
             self._h = None
 
