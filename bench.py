@@ -18,6 +18,7 @@ bounded sample of the same workload on this host's cores.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -54,7 +55,7 @@ def append_bytes(batch, hkv=HKV, d=D):
     return 2 * 2 * hkv * d * 4 * batch
 
 
-def build_workload(seed, batch, layers, steps_total):
+def build_workload(seed, batch, layers, steps_total, shuffle=True):
     rng = np.random.default_rng(seed)
     lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=batch)).astype(np.int64)
     pages = (lengths + P - 1) // P
@@ -66,11 +67,11 @@ def build_workload(seed, batch, layers, steps_total):
     # random order, so later allocations scatter each sequence over the pool.
     tok = torch.zeros(layers, HKV, D, device="cuda:0")
     dummies = []
-    for _ in range(n_phys):
+    for _ in range(n_phys if shuffle else 0):
         s = cache.create_sequence()
         cache.append(s, tok, tok)
         dummies.append(s)
-    for i in rng.permutation(n_phys):
+    for i in rng.permutation(len(dummies)):
         cache.release_sequence(dummies[int(i)])
     # Fill the histories with N(0, 1) data in one bulk append per sequence.
     gen = torch.Generator(device="cuda:0")
@@ -118,8 +119,7 @@ def cpu_baseline(cache, seqs, layers_sample, threads, seed):
         # Full-size parity of the GPU kernel on the same inputs.
         dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")  # noqa: E731
         out = torch.empty(batch, HQ, D, device="cuda:0")
-        ws = torch.empty(hx.decode_workspace_bytes(batch, HQ, max_blocks) // 4 + 1,
-                         device="cuda:0")
+        ws = hx.decode_workspace(batch, HQ, HKV, max_blocks)
         kpool, vpool = cache.layer_pool_pointers(layer)
         hx.paged_decode_attention(dv(q), kpool, vpool, dv(tables.astype(np.int32)), dv(lengths),
                                   dv(tk), dv(tv), out, ws,
@@ -147,9 +147,31 @@ def copy_probe(nbytes=1 << 30, reps=10):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
+    big = torch.randn(4 * nbytes // 4, device="cuda:0")
+    del src, dst
+    props = torch.cuda.get_device_properties(0)
+    best = (0.0, 0, 0.0)
+    for per_cu in (2, 4, 8, 16, 32):
+        blocks = props.multi_processor_count * per_cu
+        sink = torch.empty(blocks * 256, device="cuda:0")
+        args = (ctypes.c_void_p(big.data_ptr()), big.numel(), ctypes.c_void_p(sink.data_ptr()),
+                blocks, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        hx.check(hx.load().helix_probe_stream_read(*args))
+        e0.record()
+        for _ in range(reps):
+            hx.check(hx.load().helix_probe_stream_read(*args))
+        e1.record()
+        torch.cuda.synchronize()
+        ms_r = e0.elapsed_time(e1) / reps
+        gbps = 4 * nbytes / ms_r / 1e6
+        log(f"stream-read probe: {blocks} workgroups: {gbps:.0f} GB/s")
+        if gbps > best[0]:
+            best = (gbps, blocks, ms_r)
+    ms_read = best[2]
     print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes,
-                      "avg_ms": round(ms, 4), "gbps_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}),
-          flush=True)
+                      "avg_ms": round(ms, 4), "gbps_read_plus_write": round(2 * nbytes / ms / 1e6, 1),
+                      "read_probe_bytes": 4 * nbytes, "read_probe_ms": round(ms_read, 4),
+                      "read_probe_gbps": round(4 * nbytes / ms_read / 1e6, 1)}), flush=True)
 
 
 def main():
@@ -159,10 +181,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--layers", type=int, default=LAYERS)
-    ap.add_argument("--pages-per-split", type=int, default=0)
+    ap.add_argument("--pages-per-split", type=int, default=0,
+                    help="decode split size in pages (0: library default)")
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-shuffle", action="store_true",
+                    help="allocate pages in pool order instead of scattering them")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM probe / counter calibration)")
     args = ap.parse_args()
@@ -179,7 +204,8 @@ def main():
         return
     steps_total = args.warmup + args.steps + 2
     t_setup = time.perf_counter()
-    cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total)
+    cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total,
+                                             shuffle=not args.no_shuffle)
     log(f"setup {time.perf_counter() - t_setup:.1f}s; mean context {lengths0.mean():.0f}")
 
     batch = hx.DecodeBatch(cache, seqs, HQ, max_tokens=int(lengths0.max()) + steps_total + P,

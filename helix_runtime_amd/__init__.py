@@ -22,7 +22,7 @@ from ._native import (HelixError, Sequence, INVALID_ARGUMENT, OUT_OF_RANGE, UNSU
 __all__ = [
     "build", "load", "HelixError", "Sequence", "BlockManager", "PagedKvCache", "DecodeBatch",
     "PagedBlockTable", "paged_attention_out", "paged_attention_with_tail_out",
-    "paged_decode_attention", "decode_workspace_bytes", "append_slots",
+    "paged_decode_attention", "decode_workspace_bytes", "decode_workspace", "append_slots",
     "INVALID_ARGUMENT", "OUT_OF_RANGE", "UNSUPPORTED", "RESOURCE_EXHAUSTED", "RUNTIME", "INTERNAL",
 ]
 
@@ -374,11 +374,21 @@ def paged_attention_with_tail_out(query, key_blocks, value_blocks, block_table, 
         _stream(stream)))
 
 
-def decode_workspace_bytes(batch, q_heads, max_blocks, pages_per_split=0):
+def decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks, pages_per_split=0):
     out = ctypes.c_size_t()
-    check(_lib().helix_paged_decode_workspace_bytes(batch, q_heads, max_blocks, pages_per_split,
-                                                    ctypes.byref(out)))
+    check(_lib().helix_paged_decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks,
+                                                    pages_per_split, ctypes.byref(out)))
     return out.value
+
+
+def decode_workspace(batch, q_heads, kv_heads, max_blocks, pages_per_split=0, device="cuda:0",
+                     stream=None):
+    """Allocate and zero a decode workspace (torch uint8 tensor)."""
+    import torch
+    n = decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks, pages_per_split)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+    check(_lib().helix_paged_decode_workspace_init(_ptr(ws), ws.numel(), _stream(stream)))
+    return ws
 
 
 def paged_decode_attention(query, key_pool, value_pool, tables, lengths, tail_key, tail_value,

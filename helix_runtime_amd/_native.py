@@ -118,7 +118,8 @@ SIGNATURES = {
     "helix_paged_attention_with_tail_out": (
         c_int, [vp, c_size, c_size, c_size, vp, vp, c_size, c_size, c_size, c_size, vp, c_size,
                 c_size, vp, vp, vp, vp, c_size, vp]),
-    "helix_paged_decode_workspace_bytes": (c_int, [c_size, c_size, c_size, c_size, P(c_size)]),
+    "helix_paged_decode_workspace_bytes": (c_int, [c_size] * 5 + [P(c_size)]),
+    "helix_paged_decode_workspace_init": (c_int, [vp, c_size, vp]),
     "helix_paged_decode_attention": (
         c_int, [vp, c_size, c_size, c_size, vp, vp, c_size, vp, c_size, vp, vp, vp, vp, vp,
                 c_size, c_size, vp]),
@@ -130,6 +131,7 @@ SIGNATURES = {
     "helix_decode_batch_attention_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_tables": (c_int, [vp, P(vp), P(vp), P(vp), P(c_size), P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
+    "helix_probe_stream_read": (c_int, [vp, c_size, vp, ctypes.c_uint, vp]),
 }
 
 _lib = None

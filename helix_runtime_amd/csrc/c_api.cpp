@@ -711,22 +711,33 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
 // ---------------------------------------------------------- batched decode ----
 namespace {
 
-constexpr std::size_t kDefaultPagesPerSplit = 8;
-
 std::size_t resolve_split(std::size_t pages_per_split) {
-  return pages_per_split == 0 ? kDefaultPagesPerSplit : pages_per_split;
+  return pages_per_split == 0 ? helix::hip::kDefaultPagesPerSplit : pages_per_split;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
-int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t max_blocks,
-                                       size_t pages_per_split, size_t* out) {
+int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t kv_heads,
+                                       size_t max_blocks, size_t pages_per_split, size_t* out) {
   return guarded([&] {
     require_out(out);
-    *out = helix::hip::decode_workspace_bytes(batch, q_heads, max_blocks,
+    check(kv_heads != 0 && q_heads % kv_heads == 0, Status::kInvalidArgument,
+          "paged_decode_workspace_bytes: q_heads must be a multiple of kv_heads");
+    *out = helix::hip::decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks,
                                               resolve_split(pages_per_split));
+  });
+}
+
+int helix_paged_decode_workspace_init(void* workspace, size_t workspace_bytes,
+                                      helix_stream stream) {
+  return guarded([&] {
+    check(workspace != nullptr || workspace_bytes == 0, Status::kInvalidArgument,
+          "paged_decode_workspace_init: workspace must not be NULL");
+    helix::hip_check(helix::hip::launch_decode_workspace_init(workspace, workspace_bytes,
+                                                             as_stream(stream)),
+                     "paged_decode_workspace_init");
   });
 }
 
@@ -740,7 +751,6 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_decode_attention";
-    const std::size_t split = resolve_split(pages_per_split);
     check(kv_heads != 0 && q_heads % kv_heads == 0 &&
               helix::hip::decode_group_supported(q_heads / kv_heads),
           Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");
@@ -749,7 +759,15 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
     check(max_blocks != 0 && max_blocks <= static_cast<std::size_t>(
                                                std::numeric_limits<std::int32_t>::max() / 16),
           Status::kInvalidArgument, std::string(op) + ": max_blocks out of range");
+    check(batch <= static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max()) /
+                       (kv_heads * (max_blocks + 1)),
+          Status::kInvalidArgument, std::string(op) + ": batch too large");
     if (batch == 0) return;
+    const std::size_t split = resolve_split(pages_per_split);
+    check(kv_heads * batch * helix::hip::decode_max_splits(max_blocks, split) <= (1u << 30),
+          Status::kInvalidArgument, std::string(op) + ": too many work items");
+    check(helix::hip::decode_max_splits(max_blocks, split) <= helix::hip::kMaxDecodeSplits,
+          Status::kUnsupported, std::string(op) + ": max_blocks / pages_per_split above 4096");
     check(query && key_blocks && value_blocks && tables && lengths && tail_key && tail_value &&
               output && workspace,
           Status::kInvalidArgument, std::string(op) + ": device pointers must be non-null");
@@ -757,7 +775,8 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
               aligned16(tail_key) && aligned16(tail_value) && aligned16(output) &&
               aligned16(workspace),
           Status::kInvalidArgument, std::string(op) + ": tensors must be 16-byte aligned");
-    check(workspace_bytes >= helix::hip::decode_workspace_bytes(batch, q_heads, max_blocks, split),
+    check(workspace_bytes >=
+              helix::hip::decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks, split),
           Status::kInvalidArgument, std::string(op) + ": workspace is too small");
     const std::size_t ob = batch * q_heads * helix::hip::kDecodeHeadDim * sizeof(float);
     check(!overlap(output, ob, query, ob) && !overlap(output, ob, workspace, workspace_bytes),
@@ -778,6 +797,7 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
     a.max_blocks = max_blocks;
     a.physical_blocks = physical_blocks;
     a.pages_per_split = split;
+    a.items = 0;
     helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), "paged_decode_attention");
   });
 }

@@ -268,8 +268,9 @@ struct DecodeKernelArgs {
   const float* tail_key;
   const float* tail_value;
   float* out;
-  float* part_o;   // [batch, q_heads, max_splits, 128]
-  float* part_ml;  // [batch, q_heads, max_splits, 2]
+  float* part_o;        // [batch * kv_heads * max_splits, G, 128]
+  float* part_ml;       // [batch * kv_heads * max_splits, G, 2]
+  int batch;
   int q_heads;
   int kv_heads;
   int max_blocks;
@@ -279,9 +280,41 @@ struct DecodeKernelArgs {
   float qscale;
 };
 
-// Split-K decode.  One wavefront per (sequence, kv head, split of pages);
-// the G = q_heads / kv_heads query heads that share the kv head are held in
-// registers, so every K/V byte is read from HBM once per kv head.
+__device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
+  return (hist < 0 || hist > max_blocks * 16) ? -1 : hist;
+}
+
+// Page splits of one (sequence, kv head) unit; an invalid length (-1)
+// attends to the tail only.
+__device__ __forceinline__ int unit_splits(int hist, int pages_per_split) {
+  const int pages = hist < 0 ? 0 : (hist + 15) / 16;
+  const int s = (pages + pages_per_split - 1) / pages_per_split;
+  return s < 1 ? 1 : s;
+}
+
+// Wave-wide inclusive prefix sum.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Split-K decode.  Work items are page splits of the (sequence, kv head)
+// units: every full split of every unit first (sequence major), then the
+// last split of each unit, which also attends to the uncommitted tail token.
+// One wavefront runs one item and the hardware dispatcher hands out items as
+// wavefronts retire, so faster waves take more items and the short last
+// splits fill the end of the launch.  A unit with one split is finished in
+// place; otherwise every split leaves a partial (m, l, o) for
+// decode_merge_kernel.  (Merging inside this kernel would need a device-scope
+// release per split, which on a multi-XCD part writes back the L2 and costs
+// far more than the separate launch.)
+//
+// The G = q_heads / kv_heads query heads of the unit stay in registers, so
+// each K/V byte is read from HBM once per kv head.
 //
 // Lane layout: lane = 32 * parity + j.  A 128-bit load at float4 index
 // i * 64 + lane of a page covers token 2i + parity, dims 4j..4j+3, so each
@@ -296,7 +329,8 @@ struct DecodeKernelArgs {
 // scores take all the mass uniformly (exp2_ratio treats inf == inf as 1 and
 // resets finite history), and a row whose maximum stays -inf is NaN.  A page
 // ID >= physical_blocks yields NaN, like the reference kernels
-// (src/attention/cuda_paged.cu:58-61), and is never dereferenced.
+// (src/attention/cuda_paged.cu:58-61), and is never dereferenced; so does a
+// history length the table row cannot cover.
 template <int G>
 __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
   constexpr int D = 128;
@@ -311,35 +345,65 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
   const int lane = threadIdx.x;
   const int parity = lane >> 5;
   const int j = lane & 31;
-  const int split = blockIdx.x;
-  const int item = blockIdx.y;
-  const int b = item / a.kv_heads;
-  const int kvh = item % a.kv_heads;
+  const int item = blockIdx.x;
+  const int CP = a.pages_per_split;
 
-  int hist = a.lengths[b];
-  bool bad_page = false;
-  if (hist < 0 || hist > a.max_blocks * P) {
-    // A length the table cannot cover: attend to the tail only and return
-    // NaN rather than reading past the table row.
-    hist = 0;
-    bad_page = true;
+  // ---- locate (sequence b, kv head, split) of this item ----------------
+  long long fulls = 0;  // full (non-last) split items over all sequences
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int bb = c0 + lane;
+    int w = 0;
+    if (bb < a.batch) w = (unit_splits(clamp_length(a.lengths[bb], a.max_blocks), CP) - 1) * a.kv_heads;
+    fulls += __shfl(wave_incl_scan(w, lane), 63, 64);
   }
-  const int hist_pages = (hist + P - 1) / P;
-  int splits = (hist_pages + a.pages_per_split - 1) / a.pages_per_split;
-  if (splits < 1) splits = 1;
-  if (split >= splits) return;
-  const int pg0 = split * a.pages_per_split;
-  const int pg1 = min(hist_pages, pg0 + a.pages_per_split);
-  const bool last = split == splits - 1;
+  int b = 0, kvh = 0, split = 0;
+  if (item < fulls) {
+    long long base = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int bb = c0 + lane;
+      int w = 0;
+      if (bb < a.batch) {
+        w = (unit_splits(clamp_length(a.lengths[bb], a.max_blocks), CP) - 1) * a.kv_heads;
+      }
+      const int incl = wave_incl_scan(w, lane);
+      const long long lo = base + incl - w;
+      const unsigned long long hit = __ballot(bb < a.batch && lo <= item && item < base + incl);
+      if (hit != 0) {
+        const int src = __ffsll(static_cast<long long>(hit)) - 1;
+        b = c0 + src;
+        const long long r = item - __shfl(lo, src, 64);
+        const int per = unit_splits(clamp_length(a.lengths[b], a.max_blocks), CP) - 1;
+        kvh = static_cast<int>(r / per);
+        split = static_cast<int>(r % per);
+        break;
+      }
+      base += __shfl(incl, 63, 64);
+    }
+  } else {
+    const long long r = item - fulls;
+    if (r >= static_cast<long long>(a.batch) * a.kv_heads) return;
+    b = static_cast<int>(r / a.kv_heads);
+    kvh = static_cast<int>(r % a.kv_heads);
+    split = unit_splits(clamp_length(a.lengths[b], a.max_blocks), CP) - 1;
+  }
 
+  const int hist = clamp_length(a.lengths[b], a.max_blocks);
+  const int hist_ok = hist < 0 ? 0 : hist;
+  const int pages = (hist_ok + P - 1) / P;
+  const int splits = unit_splits(hist, CP);
+  const bool last = split == splits - 1;
+  const int pg0 = split * CP;
+  const int pg1 = min(pages, pg0 + CP);
+  const std::uint32_t* table = a.tables + static_cast<std::size_t>(b) * a.max_blocks;
   const std::size_t qrow0 = static_cast<std::size_t>(b) * a.q_heads + kvh * G;
+  const std::size_t page_elems = static_cast<std::size_t>(P) * D;
+
   float4 q[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float4 v = reinterpret_cast<const float4*>(a.query + (qrow0 + h) * D)[j];
     q[h] = make_float4(v.x * a.qscale, v.y * a.qscale, v.z * a.qscale, v.w * a.qscale);
   }
-
   float acc[G][4];
 #pragma unroll
   for (int h = 0; h < G; ++h) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
@@ -349,31 +413,25 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
     m[r] = -INFINITY;
     l[r] = 0.0f;
   }
-
-  const std::uint32_t* table = a.tables + static_cast<std::size_t>(b) * a.max_blocks;
-  const std::size_t page_elems = static_cast<std::size_t>(P) * D;
-
-  auto page_ptr = [&](const float* pool, std::uint32_t phys) {
-    return pool + (static_cast<std::size_t>(phys) * a.kv_heads + kvh) * page_elems;
-  };
+  bool bad_page = hist < 0;
 
   // One page (or the tail as a 1-token page) through score, softmax and P.V.
   auto process = [&](const float4 (&k)[8], float4 (&v)[8], int valid) {
-    float x[NV];
+    float xs[NV];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        x[i * G + h] = q[h].x * k[i].x + q[h].y * k[i].y + q[h].z * k[i].z + q[h].w * k[i].w;
+        xs[i * G + h] = q[h].x * k[i].x + q[h].y * k[i].y + q[h].z * k[i].z + q[h].w * k[i].w;
       }
     }
-    reduce_scores<G>(x, j);
+    reduce_scores<G>(xs, j);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int vi = (j >> DUPB) * R + r;
       const int tok = 2 * (vi / G) + parity;
       const bool ok = tok < valid;
-      const float s = ok ? x[r] : -INFINITY;
+      const float s = ok ? xs[r] : -INFINITY;
       const float mn = fmaxf(m[r], token_max(s));
       const float alpha = exp2_ratio(m[r], mn);
       const float p = ok ? exp2_ratio(s, mn) : 0.0f;
@@ -422,41 +480,37 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
     }
   };
 
-  auto load_page = [&](int pg, float4 (&k)[8], float4 (&v)[8]) -> bool {
-    const std::uint32_t phys = table[pg];
-    if (phys >= a.physical_blocks) return false;
-    const float4* kp = reinterpret_cast<const float4*>(page_ptr(a.key_pool, phys));
-    const float4* vp = reinterpret_cast<const float4*>(page_ptr(a.value_pool, phys));
+  // Loads are issued unconditionally (page index clamped by the caller, an
+  // out-of-range page ID redirected to page 0 and flagged), so the compiler
+  // can count outstanding loads exactly and never drains the queue early.
+  auto load_page = [&](int pg, float4 (&k)[8], float4 (&v)[8]) {
+    std::uint32_t phys = table[pg];
+    if (phys >= a.physical_blocks) {
+      bad_page = true;
+      phys = 0;
+    }
+    const std::size_t off = (static_cast<std::size_t>(phys) * a.kv_heads + kvh) * page_elems;
+    const float4* kp = reinterpret_cast<const float4*>(a.key_pool + off);
+    const float4* vp = reinterpret_cast<const float4*>(a.value_pool + off);
 #pragma unroll
     for (int i = 0; i < 8; ++i) k[i] = kp[i * 64 + lane];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = vp[i * 64 + lane];
-    return true;
   };
 
+  // History pages [pg0, pg1) through a two-buffer ping-pong pipeline: while
+  // one page is reduced the loads of the next two are in flight.
   if (pg0 < pg1) {
-    float4 kc[8], vc[8];
-    bool okc = load_page(pg0, kc, vc);
-    for (int pg = pg0; pg < pg1; ++pg) {
-      float4 kn[8], vn[8];
-      bool okn = true;
-      if (pg + 1 < pg1) okn = load_page(pg + 1, kn, vn);
-      if (okc) {
-        process(kc, vc, min(P, hist - pg * P));
-      } else {
-        bad_page = true;
-      }
-      if (pg + 1 < pg1) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          kc[i] = kn[i];
-          vc[i] = vn[i];
-        }
-        okc = okn;
-      }
+    float4 ka[8], va[8], kb[8], vb[8];
+    load_page(pg0, ka, va);
+    load_page(min(pg0 + 1, pg1 - 1), kb, vb);
+    for (int pg = pg0; pg < pg1; pg += 2) {
+      process(ka, va, min(P, hist_ok - pg * P));
+      load_page(min(pg + 2, pg1 - 1), ka, va);
+      if (pg + 1 < pg1) process(kb, vb, min(P, hist_ok - (pg + 1) * P));
+      load_page(min(pg + 3, pg1 - 1), kb, vb);
     }
   }
-
   if (last) {
     // The uncommitted current token: lanes of half 0 hold its 128 dims.
     float4 kt[8], vt[8];
@@ -488,69 +542,112 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
     }
   }
   __syncthreads();
-  if (parity != 0) return;
 
-  const std::size_t out_row0 = qrow0;
   if (splits == 1) {
+    if (parity == 0) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float mh = s_head[1][h];
-      const float lh = s_head[2][h];
-      float4 o;
-      if (mh == -INFINITY) {
-        o = make_float4(NAN, NAN, NAN, NAN);
-      } else {
-        const float inv = 1.0f / lh;
-        o = make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+      for (int h = 0; h < G; ++h) {
+        const float mh = s_head[1][h];
+        const float lh = s_head[2][h];
+        float4 o;
+        if (mh == -INFINITY) {
+          o = make_float4(NAN, NAN, NAN, NAN);
+        } else {
+          const float inv = 1.0f / lh;
+          o = make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+        }
+        reinterpret_cast<float4*>(a.out + (qrow0 + h) * D)[j] = o;
       }
-      reinterpret_cast<float4*>(a.out + (out_row0 + h) * D)[j] = o;
     }
     return;
   }
+
+  const std::size_t slot = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * a.max_splits + split;
+  if (parity == 0) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const std::size_t pidx = (out_row0 + h) * a.max_splits + split;
-    reinterpret_cast<float4*>(a.part_o + pidx * D)[j] =
-        make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-    if (j == 0) {
-      a.part_ml[2 * pidx] = s_head[1][h];
-      a.part_ml[2 * pidx + 1] = s_head[2][h];
+    for (int h = 0; h < G; ++h) {
+      reinterpret_cast<float4*>(a.part_o + (slot * G + h) * D)[j] =
+          make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    }
+    if (j < G) {
+      a.part_ml[(slot * G + j) * 2] = s_head[1][j];
+      a.part_ml[(slot * G + j) * 2 + 1] = s_head[2][j];
     }
   }
 }
 
-// Merges the per-split (m, l, o) of every (sequence, q head) row that used
-// more than one split: O = sum_c o_c * 2^(m_c - M) / sum_c l_c * 2^(m_c - M).
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeKernelArgs a) {
+// Merges the split partials of every unit with more than one split:
+// O_h = sum_s o_sh 2^(m_sh - M_h) / sum_s l_sh 2^(m_sh - M_h).  One
+// workgroup per (sequence, kv head); the per-split weights are formed once
+// in LDS, then every thread sums its outputs over the splits with
+// independent loads in flight.
+template <int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeKernelArgs a) {
   constexpr int D = 128;
-  constexpr int P = 16;
-  const int row = blockIdx.x;  // b * q_heads + h
-  const int b = row / a.q_heads;
-  int hist = a.lengths[b];
-  if (hist < 0 || hist > a.max_blocks * P) hist = 0;
-  const int hist_pages = (hist + P - 1) / P;
-  const int splits = (hist_pages + a.pages_per_split - 1) / a.pages_per_split;
+  extern __shared__ float s_w[];  // [G][max_splits] weights, then [G] 1/den
+  const int unit = blockIdx.x;
+  const int b = unit / a.kv_heads;
+  const int hist = clamp_length(a.lengths[b], a.max_blocks);
+  const int splits = unit_splits(hist, a.pages_per_split);
   if (splits <= 1) return;
-  const std::size_t base = static_cast<std::size_t>(row) * a.max_splits;
-  float mx = -INFINITY;
-  for (int c = 0; c < splits; ++c) mx = fmaxf(mx, a.part_ml[2 * (base + c)]);
-  float den = 0.0f;
-  float2 num = make_float2(0.f, 0.f);
-  for (int c = 0; c < splits; ++c) {
-    const float w = exp2_ratio(a.part_ml[2 * (base + c)], mx);
-    den += w * a.part_ml[2 * (base + c) + 1];
-    const float2 o = reinterpret_cast<const float2*>(a.part_o + (base + c) * D)[threadIdx.x];
-    num.x += w * o.x;
-    num.y += w * o.y;
+  float* s_inv = s_w + G * a.max_splits;
+  __shared__ float s_max[G];
+  const std::size_t slot0 = static_cast<std::size_t>(unit) * a.max_splits;
+  const int tid = threadIdx.x;
+  // Per head: the largest split maximum (one wave per head, G <= 8 heads
+  // over four waves).
+  for (int h = tid / 64; h < G; h += 4) {
+    float mx = -INFINITY;
+    for (int s = tid % 64; s < splits; s += 64) mx = fmaxf(mx, a.part_ml[((slot0 + s) * G + h) * 2]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (tid % 64 == 0) s_max[h] = mx;
   }
-  float2 res;
-  if (mx == -INFINITY) {
-    res = make_float2(NAN, NAN);
-  } else {
-    const float inv = 1.0f / den;
-    res = make_float2(num.x * inv, num.y * inv);
+  __syncthreads();
+  for (int t = tid; t < G * splits; t += 256) {
+    const int h = t / splits;
+    const int s = t % splits;
+    s_w[h * a.max_splits + s] = exp2_ratio(a.part_ml[((slot0 + s) * G + h) * 2], s_max[h]);
   }
-  reinterpret_cast<float2*>(a.out + static_cast<std::size_t>(row) * D)[threadIdx.x] = res;
+  __syncthreads();
+  for (int h = tid / 64; h < G; h += 4) {
+    float den = 0.0f;
+    for (int s = tid % 64; s < splits; s += 64) {
+      den += s_w[h * a.max_splits + s] * a.part_ml[((slot0 + s) * G + h) * 2 + 1];
+    }
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    if (tid % 64 == 0) s_inv[h] = s_max[h] == -INFINITY ? NAN : 1.0f / den;
+  }
+  __syncthreads();
+  const std::size_t qrow0 = static_cast<std::size_t>(b) * a.q_heads +
+                            static_cast<std::size_t>(unit % a.kv_heads) * G;
+  for (int t = tid; t < G * (D / 4); t += 256) {
+    const int h = t / (D / 4);
+    const int d4 = t % (D / 4);
+    const float* w = s_w + h * a.max_splits;
+    float4 n0 = make_float4(0.f, 0.f, 0.f, 0.f), n1 = n0;
+    int s = 0;
+    for (; s + 1 < splits; s += 2) {
+      const float4 o0 = reinterpret_cast<const float4*>(a.part_o + ((slot0 + s) * G + h) * D)[d4];
+      const float4 o1 =
+          reinterpret_cast<const float4*>(a.part_o + ((slot0 + s + 1) * G + h) * D)[d4];
+      n0.x += w[s] * o0.x; n0.y += w[s] * o0.y; n0.z += w[s] * o0.z; n0.w += w[s] * o0.w;
+      n1.x += w[s + 1] * o1.x; n1.y += w[s + 1] * o1.y;
+      n1.z += w[s + 1] * o1.z; n1.w += w[s + 1] * o1.w;
+    }
+    if (s < splits) {
+      const float4 o0 = reinterpret_cast<const float4*>(a.part_o + ((slot0 + s) * G + h) * D)[d4];
+      n0.x += w[s] * o0.x; n0.y += w[s] * o0.y; n0.z += w[s] * o0.z; n0.w += w[s] * o0.w;
+    }
+    const float inv = s_inv[h];
+    reinterpret_cast<float4*>(a.out + (qrow0 + h) * D)[d4] =
+        make_float4((n0.x + n1.x) * inv, (n0.y + n1.y) * inv, (n0.z + n1.z) * inv,
+                    (n0.w + n1.w) * inv);
+  }
+}
+
+__global__ void zero_words_kernel(unsigned* p, std::size_t n) {
+  const std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+  if (i < n) p[i] = 0u;
 }
 
 // ------------------------------------------------------------ generic ----
@@ -793,24 +890,68 @@ hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
   return hipGetLastError();
 }
 
+namespace {
+
+std::size_t align256(std::size_t n) { return (n + 255) & ~std::size_t{255}; }
+
+struct WorkspaceLayout {
+  std::size_t part_o, part_ml, total;
+};
+
+WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
+                           std::size_t max_splits) {
+  const std::size_t group = q_heads / kv_heads;
+  const std::size_t slots = batch * kv_heads * max_splits;
+  WorkspaceLayout l{};
+  l.part_o = 0;
+  l.part_ml = align256(slots * group * kDecodeHeadDim * sizeof(float));
+  l.total = l.part_ml + align256(slots * group * 2 * sizeof(float));
+  return l;
+}
+
+}  // namespace
+
 std::size_t decode_max_splits(std::size_t max_blocks, std::size_t pages_per_split) {
   const std::size_t s = (max_blocks + pages_per_split - 1) / pages_per_split;
   return s == 0 ? 1 : s;
 }
 
-std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t max_blocks,
-                                   std::size_t pages_per_split) {
-  const std::size_t splits = decode_max_splits(max_blocks, pages_per_split);
-  return batch * q_heads * splits * (kDecodeHeadDim + 2) * sizeof(float);
+std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
+                                   std::size_t max_blocks, std::size_t pages_per_split) {
+  if (kv_heads == 0 || q_heads % kv_heads != 0 || pages_per_split == 0) return 0;
+  return layout_for(batch, q_heads, kv_heads, decode_max_splits(max_blocks, pages_per_split)).total;
+}
+
+hipError_t launch_decode_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream) {
+  const std::size_t words = bytes / sizeof(unsigned);
+  if (words == 0) return hipSuccess;
+  zero_words_kernel<<<grid_for(words, kThreads), kThreads, 0, stream>>>(
+      static_cast<unsigned*>(workspace), words);
+  return hipGetLastError();
 }
 
 bool decode_group_supported(std::size_t group) {
   return group == 1 || group == 2 || group == 4 || group == 8;
 }
 
+std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::size_t kv_heads,
+                         std::size_t max_blocks, std::size_t pages_per_split) {
+  std::size_t items = 0;
+  for (std::size_t b = 0; b < batch; ++b) {
+    const std::int64_t h = lengths[b];
+    const std::size_t pages =
+        (h < 0 || h > static_cast<std::int64_t>(max_blocks * 16)) ? 0 : (h + 15) / 16;
+    const std::size_t s = (pages + pages_per_split - 1) / pages_per_split;
+    items += kv_heads * (s < 1 ? 1 : s);
+  }
+  return items;
+}
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if (a.batch == 0) return hipSuccess;
-  const std::size_t splits = decode_max_splits(a.max_blocks, a.pages_per_split);
+  const std::size_t max_splits = decode_max_splits(a.max_blocks, a.pages_per_split);
+  const WorkspaceLayout lay = layout_for(a.batch, a.q_heads, a.kv_heads, max_splits);
+  auto* ws = static_cast<unsigned char*>(a.workspace);
   DecodeKernelArgs k{};
   k.query = a.query;
   k.key_pool = a.key_pool;
@@ -820,17 +961,22 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.tail_key = a.tail_key;
   k.tail_value = a.tail_value;
   k.out = a.out;
-  k.part_o = static_cast<float*>(a.workspace);
-  k.part_ml = k.part_o + a.batch * a.q_heads * splits * kDecodeHeadDim;
+  k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+  k.batch = static_cast<int>(a.batch);
   k.q_heads = static_cast<int>(a.q_heads);
   k.kv_heads = static_cast<int>(a.kv_heads);
   k.max_blocks = static_cast<int>(a.max_blocks);
-  k.max_splits = static_cast<int>(splits);
+  k.max_splits = static_cast<int>(max_splits);
   k.pages_per_split = static_cast<int>(a.pages_per_split);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
-  dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a.batch * a.kv_heads));
-  switch (a.q_heads / a.kv_heads) {
+  // Items beyond the real work (when the caller passes no exact count)
+  // return at once.
+  const std::size_t items = a.items != 0 ? a.items : a.batch * a.kv_heads * max_splits;
+  const dim3 grid(static_cast<unsigned>(items));
+  const std::size_t group = a.q_heads / a.kv_heads;
+  switch (group) {
     case 1: decode_split_kernel<1><<<grid, 64, 0, stream>>>(k); break;
     case 2: decode_split_kernel<2><<<grid, 64, 0, stream>>>(k); break;
     case 4: decode_split_kernel<4><<<grid, 64, 0, stream>>>(k); break;
@@ -838,12 +984,17 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (splits > 1) {
-    decode_combine_kernel<<<static_cast<unsigned>(a.batch * a.q_heads), 64, 0, stream>>>(k);
-    e = hipGetLastError();
+  if (e != hipSuccess || max_splits == 1) return e;
+  const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
+  const std::size_t lds = (group * max_splits + group) * sizeof(float);
+  switch (group) {
+    case 1: decode_merge_kernel<1><<<mgrid, 256, lds, stream>>>(k); break;
+    case 2: decode_merge_kernel<2><<<mgrid, 256, lds, stream>>>(k); break;
+    case 4: decode_merge_kernel<4><<<mgrid, 256, lds, stream>>>(k); break;
+    case 8: decode_merge_kernel<8><<<mgrid, 256, lds, stream>>>(k); break;
+    default: return hipErrorInvalidValue;
   }
-  return e;
+  return hipGetLastError();
 }
 
 hipError_t launch_generic(const GenericArgs& a, hipStream_t stream) {

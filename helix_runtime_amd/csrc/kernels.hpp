@@ -63,13 +63,15 @@ hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
                                 hipStream_t stream);
 
 // ------------------------------------------------------------- decode ----
-// Batched one-token decode with an uncommitted tail (split-K over pages).
+// Batched one-token decode with an uncommitted tail (split-K over pages with
+// an in-kernel merge).
 //   query      [batch, q_heads, 128]
 //   tables     [batch, max_blocks] physical block IDs
 //   lengths    [batch] committed history tokens per sequence
 //   tail_key / tail_value [batch, kv_heads, 128]
 //   out        [batch, q_heads, 128]
-//   workspace  decode_workspace_bytes(batch, q_heads, max_blocks) bytes
+//   workspace  decode_workspace_bytes(...) bytes of split partials
+//   items      exact work-item count (decode_items) or 0 for the upper bound
 struct DecodeArgs {
   const float* query;
   const float* key_pool;
@@ -86,14 +88,22 @@ struct DecodeArgs {
   std::size_t max_blocks;
   std::size_t physical_blocks;
   std::size_t pages_per_split;
+  std::size_t items;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;
 constexpr std::size_t kDecodeBlockTokens = 16;
+constexpr std::size_t kDefaultPagesPerSplit = 16;
+// Largest split count per sequence the merge kernel's LDS holds.
+constexpr std::size_t kMaxDecodeSplits = 4096;
 
 std::size_t decode_max_splits(std::size_t max_blocks, std::size_t pages_per_split);
-std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t max_blocks,
-                                   std::size_t pages_per_split);
+std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
+                                   std::size_t max_blocks, std::size_t pages_per_split);
+// Work items of one launch for host-known lengths.
+std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::size_t kv_heads,
+                         std::size_t max_blocks, std::size_t pages_per_split);
+hipError_t launch_decode_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream);
 bool decode_group_supported(std::size_t group);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
 

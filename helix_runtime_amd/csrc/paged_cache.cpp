@@ -377,18 +377,11 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
           "decode batch max_tokens leaves no room for the next token");
     total_pages += s.manager.blocks(sequences[i]).size();
   }
-  if (pages_per_split == 0) {
-    // Enough split work items to cover the chip several times over while
-    // keeping the combine traffic small.
-    const std::size_t mean = std::max<std::size_t>(1, total_pages / batch);
-    const std::size_t items_target = 8192;
-    pages_per_split = 64;
-    while (pages_per_split > 4 &&
-           batch * c.kv_heads * ((mean + pages_per_split - 1) / pages_per_split) < items_target) {
-      pages_per_split /= 2;
-    }
-  }
-  pages_per_split_ = pages_per_split;
+  static_cast<void>(total_pages);
+  pages_per_split_ = pages_per_split != 0 ? pages_per_split : hip::kDefaultPagesPerSplit;
+  check(hip::decode_max_splits(max_blocks_, pages_per_split_) <= hip::kMaxDecodeSplits,
+        Status::kUnsupported, "decode batch: max_tokens / pages_per_split above 4096 splits");
+  host_lengths_.assign(batch, 0);
 
   DeviceGuard guard(s.device);
   std::vector<std::uint32_t> host(batch * max_blocks_, 0);
@@ -403,7 +396,11 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
                 3 * batch * sizeof(std::uint32_t);
   step_ = DeviceBuffer(step_bytes_, s.device);
   workspace_ = DeviceBuffer(
-      hip::decode_workspace_bytes(batch, q_heads, max_blocks_, pages_per_split_), s.device);
+      hip::decode_workspace_bytes(batch, q_heads, c.kv_heads, max_blocks_, pages_per_split_),
+      s.device);
+  hip_check(hip::launch_decode_workspace_init(workspace_.data(), workspace_.size(), nullptr),
+            "decode batch workspace init");
+  hip_check(hipDeviceSynchronize(), "decode batch workspace init");
   for (int i = 0; i < 2; ++i) {
     pinned_[i] = PinnedBuffer(step_bytes_);
     hip_check(hipEventCreateWithFlags(&uploaded_[i], hipEventDisableTiming), "hipEventCreate");
@@ -460,6 +457,7 @@ void DecodeBatch::prepare(hipStream_t stream) {
     const AppendPlan plan = s.manager.plan_append(sequences_[i], 1);
     s.manager.commit_append(plan);
     lengths[i] = static_cast<std::int32_t>(plan.old_length);
+    host_lengths_[i] = lengths[i];
     slots[i] = static_cast<std::int64_t>(plan.slot(0, c.block_tokens));
     if (plan.new_blocks != 0) {
       updates[3 * n_updates] = static_cast<std::uint32_t>(i);
@@ -472,6 +470,7 @@ void DecodeBatch::prepare(hipStream_t stream) {
   hip_check(hipMemcpyAsync(step_.data(), host, step_bytes_, hipMemcpyHostToDevice, stream),
             "decode batch step upload");
   hip_check(hipEventRecord(uploaded_[which], stream), "decode batch event");
+  items_ = hip::decode_items(host_lengths_.data(), B, c.kv_heads, max_blocks_, pages_per_split_);
   // The updates follow the slots in the device copy of the step buffer.
   const auto* dev_updates = reinterpret_cast<const std::uint32_t*>(this->slots() + B);
   hip_check(hip::launch_table_updates(static_cast<std::uint32_t*>(tables_.data()), max_blocks_,
@@ -519,6 +518,7 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.max_blocks = max_blocks_;
   a.physical_blocks = c.physical_blocks;
   a.pages_per_split = pages_per_split_;
+  a.items = items_;
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
 }

@@ -176,6 +176,8 @@ private:
   std::size_t q_heads_;
   std::size_t max_blocks_;
   std::size_t pages_per_split_;
+  std::size_t items_ = 0;      // work items of the prepared step
+  std::vector<std::int32_t> host_lengths_;
   DeviceBuffer tables_;
   DeviceBuffer step_;       // lengths [B] int32 | slots [B] int64 | updates
   DeviceBuffer workspace_;

@@ -243,9 +243,15 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
  *   query [batch, q_heads, 128]; tables [batch, max_blocks] uint32;
  *   lengths [batch] int32 history tokens; tail_key/value [batch, kv_heads, 128];
  *   output [batch, q_heads, 128].
- * pages_per_split == 0 selects the default split size. */
-int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t max_blocks,
-                                       size_t pages_per_split, size_t* out);
+ * Each sequence's history is cut into splits of `pages_per_split` pages (0
+ * selects 16; at most 4096 splits per sequence), one wavefront per split;
+ * the workspace holds the split partials (calls that overlap on one
+ * workspace race).  helix_paged_decode_workspace_init zero-fills a workspace
+ * (optional: every call writes the partials it reads). */
+int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t kv_heads,
+                                       size_t max_blocks, size_t pages_per_split, size_t* out);
+int helix_paged_decode_workspace_init(void* workspace, size_t workspace_bytes,
+                                      helix_stream stream);
 int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
                                  size_t kv_heads, const float* key_blocks,
                                  const float* value_blocks, size_t physical_blocks,
@@ -278,6 +284,14 @@ int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tabl
                               const int32_t** lengths, const int64_t** slots,
                               size_t* max_blocks, size_t* pages_per_split);
 void helix_decode_batch_destroy(helix_decode_batch* b);
+
+/* ------------------------------------------------------- measurement ---- */
+/* Streaming-read probe (no reference counterpart): reads n_floats floats
+ * with 128-bit loads using `blocks` workgroups of 256 threads and writes one
+ * float per thread into out (blocks * 256 floats).  bench.py uses it to
+ * measure the attainable HBM read bandwidth. */
+int helix_probe_stream_read(const float* data, size_t n_floats, float* out, unsigned blocks,
+                            helix_stream stream);
 
 #ifdef __cplusplus
 }
