@@ -387,7 +387,10 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeKernelArgs a) {
     split = unit_splits(clamp_length(a.lengths[b], a.max_blocks), CP) - 1;
   }
 
-  const int hist = clamp_length(a.lengths[b], a.max_blocks);
+  b = __builtin_amdgcn_readfirstlane(b);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  split = __builtin_amdgcn_readfirstlane(split);
+  const int hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[b], a.max_blocks));
   const int hist_ok = hist < 0 ? 0 : hist;
   const int pages = (hist_ok + P - 1) / P;
   const int splits = unit_splits(hist, CP);
