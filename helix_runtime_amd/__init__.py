@@ -417,6 +417,32 @@ def append_slots(keys, values, key_pool, value_pool, slots, stream=None):
                                           slots.numel(), _stream(stream)))
 
 
+def paged_prefill_attention(query, key_pool, value_pool, tables, lengths, chunk_key,
+                            chunk_value, output, stream=None, pool_shape=None):
+    """Batched chunked prefill (MFMA): query [B, Hq, T, 128]; pools [N, Hkv, 16,
+    128] tensors (or raw device addresses with pool_shape); tables [B,
+    max_blocks] int32/uint32; lengths [B] int32 history tokens; chunk_key /
+    chunk_value [B, Hkv, T, 128]; output [B, Hq, T, 128]."""
+    b, hq, t, _ = query.shape
+    if pool_shape is None:
+        pool_shape = tuple(key_pool.shape)
+        key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
+    n, hkv, _, _ = pool_shape
+    check(_lib().helix_paged_prefill_attention(
+        _ptr(query), b, hq, hkv, t, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
+        _ptr(tables), tables.shape[1], _ptr(lengths), _ptr(chunk_key), _ptr(chunk_value),
+        _ptr(output), _stream(stream)))
+
+
+def append_chunk(keys, values, key_pool, value_pool, slots, stream=None):
+    """Write rows [B, Hkv, T, D] into one layer's pools at int64 slots [B, T]."""
+    n, hkv, p, d = key_pool.shape
+    b, t = slots.shape
+    check(_lib().helix_paged_append_chunk(_ptr(keys), _ptr(values), _ptr(key_pool),
+                                          _ptr(value_pool), n, hkv, p, d, _ptr(slots), b, t,
+                                          _stream(stream)))
+
+
 class DecodeBatch:
     """Batched decode driver over a PagedKvCache (persistent device tables)."""
 
@@ -440,6 +466,15 @@ class DecodeBatch:
 
     def prepare(self, stream=None):
         check(_lib().helix_decode_batch_prepare(self._h, _stream(stream)))
+
+    def prepare_chunk(self, tokens, stream=None):
+        """Reserve `tokens` slots per sequence (chunked prefill step)."""
+        check(_lib().helix_decode_batch_prepare_chunk(self._h, tokens, _stream(stream)))
+
+    def prefill_layer(self, layer, query, chunk_key, chunk_value, output, stream=None):
+        check(_lib().helix_decode_batch_prefill_layer(self._h, layer, _ptr(query),
+                                                      _ptr(chunk_key), _ptr(chunk_value),
+                                                      _ptr(output), _stream(stream)))
 
     def append_layer(self, layer, keys, values, stream=None):
         check(_lib().helix_decode_batch_append_layer(self._h, layer, _ptr(keys), _ptr(values),

@@ -125,6 +125,13 @@ SIGNATURES = {
                 c_size, c_size, vp]),
     "helix_paged_append_slots": (
         c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, vp]),
+    "helix_paged_prefill_attention": (
+        c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, vp, c_size, vp, vp, vp, vp,
+                vp]),
+    "helix_paged_append_chunk": (
+        c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, c_size, vp]),
+    "helix_decode_batch_prepare_chunk": (c_int, [vp, c_size, vp]),
+    "helix_decode_batch_prefill_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_create": (c_int, [vp, P(Sequence), c_size, c_size, c_size, c_size, P(vp)]),
     "helix_decode_batch_prepare": (c_int, [vp, vp]),
     "helix_decode_batch_append_layer": (c_int, [vp, c_size, vp, vp, vp]),

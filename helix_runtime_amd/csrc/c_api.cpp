@@ -821,6 +821,76 @@ int helix_paged_append_slots(const float* keys, const float* values, float* key_
   });
 }
 
+int helix_paged_append_chunk(const float* keys, const float* values, float* key_blocks,
+                             float* value_blocks, size_t physical_blocks, size_t kv_heads,
+                             size_t block_tokens, size_t head_dim, const int64_t* slots,
+                             size_t batch, size_t tokens, helix_stream stream) {
+  return guarded([&] {
+    check(physical_blocks != 0 && kv_heads != 0 && block_tokens != 0 && head_dim != 0,
+          Status::kInvalidArgument, "append_chunk: geometry must be positive");
+    if (batch == 0 || tokens == 0) return;
+    check(keys && values && key_blocks && value_blocks && slots, Status::kInvalidArgument,
+          "append_chunk: device pointers must be non-null");
+    helix::hip_check(
+        helix::hip::launch_append_slots(
+            keys, values, key_blocks, value_blocks,
+            helix::hip::PageGeometry{physical_blocks, kv_heads, block_tokens, head_dim}, slots,
+            batch, as_stream(stream), tokens),
+        "append_chunk");
+  });
+}
+
+int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_heads,
+                                  size_t kv_heads, size_t tokens, const float* key_blocks,
+                                  const float* value_blocks, size_t physical_blocks,
+                                  const uint32_t* tables, size_t max_blocks,
+                                  const int32_t* lengths, const float* chunk_key,
+                                  const float* chunk_value, float* output, helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "paged_prefill_attention";
+    check(kv_heads != 0 && q_heads % kv_heads == 0 &&
+              helix::hip::prefill_group_supported(q_heads / kv_heads),
+          Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");
+    check(physical_blocks != 0 && physical_blocks <= std::numeric_limits<std::uint32_t>::max(),
+          Status::kInvalidArgument, std::string(op) + ": physical block count out of range");
+    check(max_blocks != 0 && max_blocks <= static_cast<std::size_t>(
+                                               std::numeric_limits<std::int32_t>::max() / 32),
+          Status::kInvalidArgument, std::string(op) + ": max_blocks out of range");
+    check(tokens <= static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max() / 2),
+          Status::kInvalidArgument, std::string(op) + ": chunk too long");
+    check(batch <= 65535 && kv_heads <= 65535, Status::kInvalidArgument,
+          std::string(op) + ": batch and kv_heads must fit a grid dimension");
+    if (batch == 0 || tokens == 0) return;
+    check(query && key_blocks && value_blocks && tables && lengths && chunk_key && chunk_value &&
+              output,
+          Status::kInvalidArgument, std::string(op) + ": device pointers must be non-null");
+    check(aligned16(query) && aligned16(key_blocks) && aligned16(value_blocks) &&
+              aligned16(chunk_key) && aligned16(chunk_value) && aligned16(output),
+          Status::kInvalidArgument, std::string(op) + ": tensors must be 16-byte aligned");
+    const std::size_t ob = batch * q_heads * tokens * helix::hip::kDecodeHeadDim * sizeof(float);
+    const std::size_t cb = batch * kv_heads * tokens * helix::hip::kDecodeHeadDim * sizeof(float);
+    check(!overlap(output, ob, query, ob) && !overlap(output, ob, chunk_key, cb) &&
+              !overlap(output, ob, chunk_value, cb),
+          Status::kInvalidArgument, std::string(op) + ": output must not alias query or chunk");
+    helix::hip::PrefillArgs a{};
+    a.query = query;
+    a.key_pool = key_blocks;
+    a.value_pool = value_blocks;
+    a.tables = tables;
+    a.lengths = lengths;
+    a.chunk_key = chunk_key;
+    a.chunk_value = chunk_value;
+    a.out = output;
+    a.batch = batch;
+    a.q_heads = q_heads;
+    a.kv_heads = kv_heads;
+    a.tokens = tokens;
+    a.max_blocks = max_blocks;
+    a.physical_blocks = physical_blocks;
+    helix::hip_check(helix::hip::launch_prefill(a, as_stream(stream)), op);
+  });
+}
+
 int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* sequences,
                               size_t batch, size_t q_heads, size_t max_tokens,
                               size_t pages_per_split, helix_decode_batch** out) {
@@ -850,6 +920,13 @@ int helix_decode_batch_prepare(helix_decode_batch* b, helix_stream stream) {
   });
 }
 
+int helix_decode_batch_prepare_chunk(helix_decode_batch* b, size_t tokens, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->prepare(as_stream(stream), tokens);
+  });
+}
+
 int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
                                     const float* values, helix_stream stream) {
   return guarded([&] {
@@ -864,6 +941,15 @@ int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, cons
   return guarded([&] {
     check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
     b->batch->attention_layer(layer, query, tail_key, tail_value, output, as_stream(stream));
+  });
+}
+
+int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const float* query,
+                                     const float* chunk_key, const float* chunk_value,
+                                     float* output, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->prefill_layer(layer, query, chunk_key, chunk_value, output, as_stream(stream));
   });
 }
 

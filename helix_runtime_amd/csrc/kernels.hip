@@ -104,26 +104,30 @@ __global__ void append_bulk_kernel(LayerPointers src, float* key_base, float* va
   }
 }
 
-// Batched per-layer append through a slot mapping (decode step: one new
-// token per sequence).
+// Batched per-layer append through a slot mapping.  Source rows are
+// [batch, heads, tokens, dim] (tokens = 1 for a decode step, the chunk
+// length for chunked prefill); token t of sequence b goes to physical slot
+// slots[b * tokens + t] = block * block_tokens + offset (negative: skipped).
 template <typename V>
 __global__ void append_slots_kernel(const float* __restrict__ keys,
                                     const float* __restrict__ values, float* key_pool,
                                     float* value_pool, std::size_t heads, std::size_t block_tokens,
                                     std::size_t dim, const std::int64_t* __restrict__ slots,
-                                    std::size_t count) {
+                                    std::size_t count, std::size_t tokens) {
   constexpr int W = vec_width<V>();
   const std::size_t dv = dim / W;
-  const std::size_t total = count * heads * dv;
+  const std::size_t total = count * heads * tokens * dv;
   const float* src = blockIdx.y == 0 ? keys : values;
   float* pool = blockIdx.y == 0 ? key_pool : value_pool;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t c = e % dv;
-    const std::size_t rh = e / dv;
-    const std::size_t h = rh % heads;
-    const std::size_t row = rh / heads;
-    const std::int64_t slot = slots[row];
+    const std::size_t ht = e / dv;
+    const std::size_t t = ht % tokens;
+    const std::size_t bh = ht / tokens;
+    const std::size_t h = bh % heads;
+    const std::size_t b = bh / heads;
+    const std::int64_t slot = slots[b * tokens + t];
     if (slot < 0) continue;
     const std::size_t block = static_cast<std::size_t>(slot) / block_tokens;
     const std::size_t off = static_cast<std::size_t>(slot) % block_tokens;
@@ -831,17 +835,19 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
 
 hipError_t launch_append_slots(const float* keys, const float* values, float* key_pool,
                                float* value_pool, const PageGeometry& g, const std::int64_t* slots,
-                               std::size_t count, hipStream_t stream) {
-  if (count == 0) return hipSuccess;
+                               std::size_t count, hipStream_t stream, std::size_t tokens) {
+  if (count == 0 || tokens == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
-  const std::size_t work = count * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
+  const std::size_t work = count * tokens * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
   dim3 grid(grid_for(work, kThreads), 2);
   if (vec) {
     append_slots_kernel<float4><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count);
+        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count,
+        tokens);
   } else {
     append_slots_kernel<float><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count);
+        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count,
+        tokens);
   }
   return hipGetLastError();
 }

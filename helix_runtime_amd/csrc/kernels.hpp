@@ -44,7 +44,7 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
 // flat slot block * block_tokens + offset of row i (negative rows skipped).
 hipError_t launch_append_slots(const float* keys, const float* values, float* key_pool,
                                float* value_pool, const PageGeometry& g, const std::int64_t* slots,
-                               std::size_t count, hipStream_t stream);
+                               std::size_t count, hipStream_t stream, std::size_t tokens = 1);
 
 // Gather one layer of one sequence into [kv_heads, dest_tokens, dim].
 hipError_t launch_gather(const float* key_pool, const float* value_pool, const PageGeometry& g,
@@ -128,10 +128,11 @@ struct GenericArgs {
 hipError_t launch_generic(const GenericArgs& a, hipStream_t stream);
 
 // ------------------------------------------------------- chunked prefill ----
-// Causal attention of a `tokens`-row chunk per sequence over its paged
-// history plus the chunk itself (MFMA f32 path, head_dim 128, page 16).
-//   query [batch, q_heads, tokens, 128]; chunk_key/value [batch, kv_heads, tokens, 128]
-//   tables [batch, max_blocks]; lengths [batch] history tokens; out like query.
+// Batched chunked-prefill attention (MFMA): every sequence b attends with
+// `tokens` query rows to its paged history (lengths[b] tokens through row b
+// of tables) plus its chunk, causally inside the chunk.  Shapes: query and
+// out [batch, q_heads, tokens, 128]; chunk_key/value [batch, kv_heads,
+// tokens, 128]; pools [physical_blocks, kv_heads, 16, 128].
 struct PrefillArgs {
   const float* query;
   const float* key_pool;
@@ -144,6 +145,7 @@ struct PrefillArgs {
   std::size_t batch, q_heads, kv_heads, tokens, max_blocks, physical_blocks;
 };
 
+bool prefill_group_supported(std::size_t group);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace helix::hip

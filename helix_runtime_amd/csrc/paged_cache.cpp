@@ -392,9 +392,6 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
   tables_ = DeviceBuffer(host.size() * sizeof(std::uint32_t), s.device);
   hip_check(hipMemcpy(tables_.data(), host.data(), tables_.size(), hipMemcpyHostToDevice),
             "decode batch table upload");
-  step_bytes_ = align8(batch * sizeof(std::int32_t)) + batch * sizeof(std::int64_t) +
-                3 * batch * sizeof(std::uint32_t);
-  step_ = DeviceBuffer(step_bytes_, s.device);
   workspace_ = DeviceBuffer(
       hip::decode_workspace_bytes(batch, q_heads, c.kv_heads, max_blocks_, pages_per_split_),
       s.device);
@@ -402,9 +399,9 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
             "decode batch workspace init");
   hip_check(hipDeviceSynchronize(), "decode batch workspace init");
   for (int i = 0; i < 2; ++i) {
-    pinned_[i] = PinnedBuffer(step_bytes_);
     hip_check(hipEventCreateWithFlags(&uploaded_[i], hipEventDisableTiming), "hipEventCreate");
   }
+  reserve_step(1);
 }
 
 DecodeBatch::~DecodeBatch() {
@@ -427,23 +424,48 @@ const std::int64_t* DecodeBatch::slots() const {
                                                align8(batch() * sizeof(std::int32_t)));
 }
 
-void DecodeBatch::prepare(hipStream_t stream) {
+// Step buffers for `tokens` slots per sequence: lengths [B] int32, slots
+// [B, tokens] int64 and up to B * (tokens / block_tokens + 1) table updates
+// of 3 words, in one device buffer and two pinned staging copies.
+void DecodeBatch::reserve_step(std::size_t tokens) {
+  if (tokens <= step_capacity_) return;
+  const PagedConfig& c = state_->manager.config();
+  const std::size_t B = batch();
+  const std::size_t max_updates = B * (tokens / c.block_tokens + 1);
+  const std::size_t bytes = align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
+                            3 * max_updates * sizeof(std::uint32_t);
+  for (hipEvent_t e : uploaded_) hip_check(hipEventSynchronize(e), "decode batch staging wait");
+  DeviceGuard guard(state_->device);
+  // The device buffer may still be read by queued kernels of earlier steps.
+  hip_check(hipDeviceSynchronize(), "decode batch step resize");
+  step_ = DeviceBuffer(bytes, state_->device);
+  for (auto& pinned : pinned_) pinned = PinnedBuffer(bytes);
+  step_bytes_ = bytes;
+  step_capacity_ = tokens;
+}
+
+void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   CacheState& s = *state_;
   std::scoped_lock lock(s.mutex);
   s.require_healthy("decode batch prepare");
   const PagedConfig& c = s.manager.config();
   const std::size_t B = batch();
+  check(tokens != 0, Status::kInvalidArgument, "decode batch prepare needs at least one token");
+  check(tokens <= max_blocks_ * c.block_tokens, Status::kOutOfRange,
+        "decode batch prepare: more tokens than the batch's max_tokens");
   std::size_t new_blocks = 0;
   for (std::size_t i = 0; i < B; ++i) {
     check(s.manager.contains(sequences_[i]), Status::kInvalidArgument,
           "decode batch sequence was released");
     const std::size_t len = s.manager.length(sequences_[i]);
-    check(len + 1 <= max_blocks_ * c.block_tokens, Status::kOutOfRange,
+    check(len + tokens <= max_blocks_ * c.block_tokens, Status::kOutOfRange,
           "decode batch sequence reached the batch's max_tokens");
-    new_blocks += len % c.block_tokens == 0 ? 1 : 0;
+    new_blocks += (len + tokens + c.block_tokens - 1) / c.block_tokens -
+                  (len + c.block_tokens - 1) / c.block_tokens;
   }
   check(new_blocks <= s.manager.free_block_count(), Status::kResourceExhausted,
-        "decode batch prepare: the pool has too few free blocks for the next token");
+        "decode batch prepare: the pool has too few free blocks for the step");
+  reserve_step(tokens);
 
   const int which = next_pinned_;
   next_pinned_ ^= 1;
@@ -451,31 +473,38 @@ void DecodeBatch::prepare(hipStream_t stream) {
   auto* host = static_cast<unsigned char*>(pinned_[which].data());
   auto* lengths = reinterpret_cast<std::int32_t*>(host);
   auto* slots = reinterpret_cast<std::int64_t*>(host + align8(B * sizeof(std::int32_t)));
-  auto* updates = reinterpret_cast<std::uint32_t*>(slots + B);  // host staging
+  auto* updates = reinterpret_cast<std::uint32_t*>(slots + B * tokens);  // host staging
   std::size_t n_updates = 0;
   for (std::size_t i = 0; i < B; ++i) {
-    const AppendPlan plan = s.manager.plan_append(sequences_[i], 1);
+    const AppendPlan plan = s.manager.plan_append(sequences_[i], tokens);
     s.manager.commit_append(plan);
     lengths[i] = static_cast<std::int32_t>(plan.old_length);
     host_lengths_[i] = lengths[i];
-    slots[i] = static_cast<std::int64_t>(plan.slot(0, c.block_tokens));
-    if (plan.new_blocks != 0) {
+    for (std::size_t t = 0; t < tokens; ++t) {
+      slots[i * tokens + t] = static_cast<std::int64_t>(plan.slot(t, c.block_tokens));
+    }
+    // Newly allocated blocks are the last new_blocks entries of plan.blocks.
+    const std::size_t first_new = plan.blocks.size() - plan.new_blocks;
+    for (std::size_t k = first_new; k < plan.blocks.size(); ++k) {
       updates[3 * n_updates] = static_cast<std::uint32_t>(i);
-      updates[3 * n_updates + 1] = static_cast<std::uint32_t>(plan.first_block);
-      updates[3 * n_updates + 2] = plan.blocks.back();
+      updates[3 * n_updates + 1] = static_cast<std::uint32_t>(plan.first_block + k);
+      updates[3 * n_updates + 2] = plan.blocks[k];
       ++n_updates;
     }
   }
   DeviceGuard guard(s.device);
-  hip_check(hipMemcpyAsync(step_.data(), host, step_bytes_, hipMemcpyHostToDevice, stream),
+  const std::size_t used = align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
+                           3 * n_updates * sizeof(std::uint32_t);
+  hip_check(hipMemcpyAsync(step_.data(), host, used, hipMemcpyHostToDevice, stream),
             "decode batch step upload");
   hip_check(hipEventRecord(uploaded_[which], stream), "decode batch event");
   items_ = hip::decode_items(host_lengths_.data(), B, c.kv_heads, max_blocks_, pages_per_split_);
   // The updates follow the slots in the device copy of the step buffer.
-  const auto* dev_updates = reinterpret_cast<const std::uint32_t*>(this->slots() + B);
+  const auto* dev_updates = reinterpret_cast<const std::uint32_t*>(this->slots() + B * tokens);
   hip_check(hip::launch_table_updates(static_cast<std::uint32_t*>(tables_.data()), max_blocks_,
                                       dev_updates, n_updates, stream),
             "decode batch table update");
+  step_tokens_ = tokens;
   prepared_ = true;
 }
 
@@ -491,7 +520,7 @@ void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float
                                      state_->value_pool(layer),
                                      hip::PageGeometry{c.physical_blocks, c.kv_heads,
                                                        c.block_tokens, c.head_dimension},
-                                     slots(), batch(), stream),
+                                     slots(), batch(), stream, step_tokens_),
             "decode batch append launch");
 }
 
@@ -499,6 +528,8 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
                                   const float* tail_value, float* out, hipStream_t stream) const {
   const PagedConfig& c = state_->manager.config();
   check(prepared_, Status::kInvalidArgument, "decode batch attention before prepare");
+  check(step_tokens_ == 1, Status::kInvalidArgument,
+        "decode batch attention needs a one-token step (use prefill for chunks)");
   check(layer < c.layers, Status::kOutOfRange, "decode batch layer is out of range");
   check(query != nullptr && tail_key != nullptr && tail_value != nullptr && out != nullptr,
         Status::kInvalidArgument, "decode batch attention needs query, tail and output");
@@ -521,6 +552,32 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.items = items_;
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
+}
+
+void DecodeBatch::prefill_layer(std::size_t layer, const float* query, const float* chunk_key,
+                                const float* chunk_value, float* out, hipStream_t stream) const {
+  const PagedConfig& c = state_->manager.config();
+  check(prepared_, Status::kInvalidArgument, "decode batch prefill before prepare");
+  check(layer < c.layers, Status::kOutOfRange, "decode batch layer is out of range");
+  check(query != nullptr && chunk_key != nullptr && chunk_value != nullptr && out != nullptr,
+        Status::kInvalidArgument, "decode batch prefill needs query, chunk and output");
+  hip::PrefillArgs a{};
+  a.query = query;
+  a.key_pool = state_->key_pool(layer);
+  a.value_pool = state_->value_pool(layer);
+  a.tables = tables();
+  a.lengths = lengths();
+  a.chunk_key = chunk_key;
+  a.chunk_value = chunk_value;
+  a.out = out;
+  a.batch = batch();
+  a.q_heads = q_heads_;
+  a.kv_heads = c.kv_heads;
+  a.tokens = step_tokens_;
+  a.max_blocks = max_blocks_;
+  a.physical_blocks = c.physical_blocks;
+  DeviceGuard guard(state_->device);
+  hip_check(hip::launch_prefill(a, stream), "decode batch prefill launch");
 }
 
 }  // namespace helix

@@ -144,12 +144,15 @@ private:
   bool valid_ = false;
 };
 
-// Batched decode driver: persistent device block tables [batch, max_blocks]
+// Batched step driver: persistent device block tables [batch, max_blocks]
 // and history lengths for a fixed set of sequences, updated incrementally
 // each step (one pinned upload + one tiny kernel), plus the split-K
-// workspace.  prepare() reserves and commits one token slot per sequence;
-// append_layer() must then write that slot for every layer before the next
-// prepare().  Sequences of a live batch must not be released.
+// workspace.  prepare(tokens) reserves and commits `tokens` slots per
+// sequence (1 for a decode step, the chunk length for chunked prefill);
+// append_layer() must then write those slots for every layer before the
+// next prepare().  attention_layer() is the one-token decode,
+// prefill_layer() the chunk attention.  Sequences of a live batch must not
+// be released.
 class DecodeBatch {
 public:
   DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t* sequences,
@@ -157,11 +160,13 @@ public:
               std::size_t max_tokens, std::size_t pages_per_split);
   ~DecodeBatch();
 
-  void prepare(hipStream_t stream);
+  void prepare(hipStream_t stream, std::size_t tokens = 1);
   void append_layer(std::size_t layer, const float* keys, const float* values,
                     hipStream_t stream) const;
   void attention_layer(std::size_t layer, const float* query, const float* tail_key,
                        const float* tail_value, float* out, hipStream_t stream) const;
+  void prefill_layer(std::size_t layer, const float* query, const float* chunk_key,
+                     const float* chunk_value, float* out, hipStream_t stream) const;
 
   [[nodiscard]] const std::uint32_t* tables() const;
   [[nodiscard]] const std::int32_t* lengths() const;
@@ -169,6 +174,7 @@ public:
   [[nodiscard]] std::size_t max_blocks() const noexcept { return max_blocks_; }
   [[nodiscard]] std::size_t pages_per_split() const noexcept { return pages_per_split_; }
   [[nodiscard]] std::size_t batch() const noexcept { return sequences_.size(); }
+  [[nodiscard]] std::size_t step_tokens() const noexcept { return step_tokens_; }
 
 private:
   std::shared_ptr<CacheState> state_;
@@ -179,13 +185,17 @@ private:
   std::size_t items_ = 0;      // work items of the prepared step
   std::vector<std::int32_t> host_lengths_;
   DeviceBuffer tables_;
-  DeviceBuffer step_;       // lengths [B] int32 | slots [B] int64 | updates
+  DeviceBuffer step_;       // lengths [B] int32 | slots [B, tokens] int64 | updates
   DeviceBuffer workspace_;
   PinnedBuffer pinned_[2];
   hipEvent_t uploaded_[2] = {nullptr, nullptr};
   int next_pinned_ = 0;
   std::size_t step_bytes_ = 0;
+  std::size_t step_capacity_ = 0;  // tokens per sequence the step buffers hold
+  std::size_t step_tokens_ = 0;    // tokens of the prepared step
   bool prepared_ = false;
+
+  void reserve_step(std::size_t tokens);
 };
 
 }  // namespace helix

@@ -1,8 +1,357 @@
-// Chunked-prefill attention (MFMA path); filled in by the prefill kernel.
+// Chunked-prefill attention on the CDNA4 matrix cores (fp32 MFMA).
+//
+// The reference runs prefill through the same paged attention as decode,
+// with T query rows and a T-token uncommitted tail
+// (src/attention/paged_reference.cpp:173-384, cuda_paged.cu:483-548): query
+// row q sees every history token and tail tokens 0..q.  For T = 512 that is
+// dense work, so it is computed as a flash-attention style tiled product on
+// v_mfma_f32_16x16x4_f32 with fp32 operands and fp32 accumulation.
+//
+// Work decomposition.  A workgroup (4 wavefronts) owns one (sequence, kv
+// head) and 128 query rows: the G = q_heads / kv_heads query heads of that
+// kv head times 128 / G consecutive chunk positions, so every K/V byte
+// staged in LDS feeds all G heads.  Each wavefront holds 32 of those rows
+// (two 16-row tiles) and keeps its Q rows in registers.  Keys stream through
+// a double-buffered LDS stage 32 at a time: history pages through the block
+// table, then the chunk rows.
+//
+// Layout trick.  Scores are computed transposed, S^T = K Q^T, so the MFMA
+// result leaves each lane holding 4 keys of one query row; the row's max and
+// sum then need only two cross-lane steps, and the transposed product
+// O^T = V^T P^T takes those probabilities as its B operand unchanged and
+// accumulates O with the same row per lane, so the online-softmax rescale is
+// lane local.  The reduction dimension of each MFMA is visited in a permuted
+// order (the same for both operands), which lets every operand fetch be one
+// 128-bit LDS read.
+//
+// Special values follow src/kernels/cpu/reference.cpp:264-316 as in the
+// decode kernel.  A masked (future) chunk value row must not reach the rows
+// that do not see it: 0 * inf would be NaN where the reference skips the
+// key.  Staging flags non-finite value rows that some row of the workgroup
+// masks, and such a block takes an exact per-key path for P.V.
 #include "kernels.hpp"
 
-namespace helix::hip {
+#include <hip/hip_runtime.h>
 
-hipError_t launch_prefill(const PrefillArgs&, hipStream_t) { return hipErrorNotSupported; }
+#include <cmath>
+#include <cstdint>
+
+namespace helix::hip {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int D = 128;
+constexpr int P = 16;
+constexpr int kRows = 128;      // query rows per workgroup
+constexpr int kKeys = 16;       // keys per LDS stage (one page)
+constexpr int kKStride = D + 4; // padded K row: 8 consecutive rows hit distinct banks
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PrefillKernelArgs {
+  const float* query;
+  const float* key_pool;
+  const float* value_pool;
+  const std::uint32_t* tables;
+  const std::int32_t* lengths;
+  const float* chunk_key;
+  const float* chunk_value;
+  float* out;
+  int q_heads;
+  int kv_heads;
+  int tokens;
+  int max_blocks;
+  int pos_blocks;
+  std::uint32_t physical_blocks;
+  float qscale;
+};
+
+__device__ __forceinline__ float exp2_ratio(float a, float b) {
+  return a == b ? 1.0f : exp2f(a - b);
+}
+
+__device__ __forceinline__ float comp(const float4& v, int c) {
+  return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ bool finite4(const float4& v) {
+  return isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
+}
+
+template <int G>
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
+  constexpr int PW = kRows / G;  // chunk positions per workgroup
+  __shared__ __align__(16) float s_k[2][kKeys * kKStride];
+  __shared__ __align__(16) float s_v[2][kKeys * D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;  // MFMA column: query row of the tile / dim group
+  const int grp = lane >> 4;  // MFMA k group
+  // Later position blocks see more keys: dispatch them first.
+  const int pb = a.pos_blocks - 1 - static_cast<int>(blockIdx.x);
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int T = a.tokens;
+  const int pos0 = pb * PW;
+
+  int hist = a.lengths[b];
+  bool bad = hist < 0 || hist > a.max_blocks * P;
+  if (bad) hist = 0;
+  const int key_end = hist + min(T, pos0 + PW);
+  const std::uint32_t* table = a.tables + static_cast<std::size_t>(b) * a.max_blocks;
+  const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
+
+  // Rows of this lane: tile t holds workgroup row wave * 32 + t * 16 + col.
+  int qpos[2];
+  std::size_t qrow[2];
+  float4 q[2][8];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = wave * 32 + t * 16 + col;
+    const int head = kvh * G + r / PW;
+    qpos[t] = pos0 + r % PW;
+    qrow[t] = ((static_cast<std::size_t>(b) * a.q_heads + head) * T + qpos[t]) * D;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (qpos[t] < T) v = *reinterpret_cast<const float4*>(a.query + qrow[t] + 16 * c + 4 * grp);
+      q[t][c] = make_float4(v.x * a.qscale, v.y * a.qscale, v.z * a.qscale, v.w * a.qscale);
+    }
+  }
+
+  v4f o[2][2][4];  // [tile][dim half][component]: O^T tiles
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[t][h][c] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY};
+  float l[2] = {0.f, 0.f};
+
+  // Staging: thread tid moves float4 column tid % 32 of key rows
+  // tid / 32 and tid / 32 + 8 of a 16-key block, for K and V.
+  const int srow = tid >> 5;
+  const int scol = tid & 31;
+  float4 stk[2], stv[2];
+  bool st_nonfinite = false;
+  auto stage_load = [&](int blk) {
+    st_nonfinite = false;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int key = blk * kKeys + srow + 8 * r;
+      const float* kp = nullptr;
+      const float* vp = nullptr;
+      if (key < hist) {
+        std::uint32_t page = table[key / P];
+        if (page >= a.physical_blocks) {
+          bad = true;
+        } else {
+          const std::size_t off =
+              ((static_cast<std::size_t>(page) * a.kv_heads + kvh) * P + key % P) * D + scol * 4;
+          kp = a.key_pool + off;
+          vp = a.value_pool + off;
+        }
+      } else if (key < key_end) {
+        const std::size_t off = (chunk_row0 + (key - hist)) * D + scol * 4;
+        kp = a.chunk_key + off;
+        vp = a.chunk_value + off;
+      }
+      stk[r] = kp ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
+      stv[r] = vp ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // A chunk row that some query row of this workgroup masks.
+      if (key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) st_nonfinite = true;
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int kr = srow + 8 * r;
+      *reinterpret_cast<float4*>(&s_k[buf][kr * kKStride + scol * 4]) = stk[r];
+      *reinterpret_cast<float4*>(&s_v[buf][kr * D + scol * 4]) = stv[r];
+    }
+  };
+
+  const int nblocks = (key_end + kKeys - 1) / kKeys;
+  int exact_pv = 0;
+  if (nblocks > 0) {
+    stage_load(0);
+    stage_store(0);
+    exact_pv = __syncthreads_or(st_nonfinite);
+  }
+  for (int n = 0; n < nblocks; ++n) {
+    const int buf = n & 1;
+    if (n + 1 < nblocks) stage_load(n + 1);
+    const float* K = s_k[buf];
+    const float* V = s_v[buf];
+
+    // S^T = K Q^T: st[t] holds keys 4*grp + i (i = vector component) of
+    // query row t*16 + col.
+    v4f st[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKStride + 16 * c + 4 * grp]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(comp(kk, e), comp(q[t][c], e), st[t], 0,
+                                                       0, 0);
+        }
+      }
+    }
+
+    // Online softmax (exp2 domain), lane-local rescale of O.
+    float p[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float x[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = n * kKeys + 4 * grp + i;
+        const bool vis = key < key_end && (key < hist || key - hist <= qpos[t]);
+        x[i] = vis ? st[t][i] : -INFINITY;
+        mx = fmaxf(mx, x[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m[t], mx);
+      const float alpha = exp2_ratio(m[t], mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = n * kKeys + 4 * grp + i;
+        const bool vis = key < key_end && (key < hist || key - hist <= qpos[t]);
+        p[t][i] = vis ? exp2_ratio(x[i], mn) : 0.f;
+        sum += p[t][i];
+      }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      l[t] = l[t] * alpha + sum;
+      m[t] = mn;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
+    }
+
+    if (!exact_pv) {
+      // O^T += V^T P^T: k step i covers keys 4*g + i over the four lane
+      // groups g; A = V rows of those keys at dims 64h + 4*col + c.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 vv =
+              *reinterpret_cast<const float4*>(&V[(4 * grp + i) * D + 64 * h + 4 * col]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              o[t][h][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(comp(vv, c), p[t][i], o[t][h][c],
+                                                                0, 0, 0);
+            }
+          }
+        }
+      }
+    } else {
+      // Exact path: every key's term is added only to the rows that see it.
+      // Lane holds O[row][64h + 16*grp + 4*ii + c] in o[t][h][c][ii].
+#pragma unroll 1
+      for (int kk = 0; kk < kKeys; ++kk) {
+        const int i = kk & 3;
+        const int src = col + 16 * (kk >> 2);
+        const int key = n * kKeys + kk;
+        float pk[2];
+        bool vis[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const float sel = i == 0 ? p[t][0] : i == 1 ? p[t][1] : i == 2 ? p[t][2] : p[t][3];
+          pk[t] = __shfl(sel, src, 64);
+          vis[t] = key < key_end && (key < hist || key - hist <= qpos[t]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const float4 vv =
+                *reinterpret_cast<const float4*>(&V[kk * D + 64 * h + 16 * grp + 4 * ii]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              if (vis[t]) {
+                o[t][h][0][ii] += pk[t] * vv.x;
+                o[t][h][1][ii] += pk[t] * vv.y;
+                o[t][h][2][ii] += pk[t] * vv.z;
+                o[t][h][3][ii] += pk[t] * vv.w;
+              }
+            }
+          }
+        }
+      }
+    }
+
+    if (n + 1 < nblocks) stage_store(buf ^ 1);
+    exact_pv = __syncthreads_or(st_nonfinite);
+  }
+
+  const int any_bad = __syncthreads_or(bad);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (qpos[t] >= T) continue;
+    const bool nan_row = any_bad || m[t] == -INFINITY;
+    const float inv = nan_row ? NAN : 1.0f / l[t];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        float4 r = make_float4(o[t][h][0][ii] * inv, o[t][h][1][ii] * inv, o[t][h][2][ii] * inv,
+                               o[t][h][3][ii] * inv);
+        if (nan_row) r = make_float4(NAN, NAN, NAN, NAN);
+        *reinterpret_cast<float4*>(a.out + qrow[t] + 64 * h + 16 * grp + 4 * ii) = r;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool prefill_group_supported(std::size_t group) {
+  return group == 1 || group == 2 || group == 4 || group == 8;
+}
+
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  if (a.batch == 0 || a.tokens == 0) return hipSuccess;
+  const std::size_t group = a.q_heads / a.kv_heads;
+  const std::size_t pw = kRows / group;
+  PrefillKernelArgs k{};
+  k.query = a.query;
+  k.key_pool = a.key_pool;
+  k.value_pool = a.value_pool;
+  k.tables = a.tables;
+  k.lengths = a.lengths;
+  k.chunk_key = a.chunk_key;
+  k.chunk_value = a.chunk_value;
+  k.out = a.out;
+  k.q_heads = static_cast<int>(a.q_heads);
+  k.kv_heads = static_cast<int>(a.kv_heads);
+  k.tokens = static_cast<int>(a.tokens);
+  k.max_blocks = static_cast<int>(a.max_blocks);
+  k.pos_blocks = static_cast<int>((a.tokens + pw - 1) / pw);
+  k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
+  k.qscale = kLog2e / sqrtf(static_cast<float>(D));
+  const dim3 grid(static_cast<unsigned>(k.pos_blocks), static_cast<unsigned>(a.kv_heads),
+                  static_cast<unsigned>(a.batch));
+  switch (group) {
+    case 1: prefill_kernel<1><<<grid, 256, 0, stream>>>(k); break;
+    case 2: prefill_kernel<2><<<grid, 256, 0, stream>>>(k); break;
+    case 4: prefill_kernel<4><<<grid, 256, 0, stream>>>(k); break;
+    case 8: prefill_kernel<8><<<grid, 256, 0, stream>>>(k); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 }  // namespace helix::hip

@@ -267,19 +267,49 @@ int helix_paged_append_slots(const float* keys, const float* values, float* key_
                              size_t block_tokens, size_t head_dim, const int64_t* slots,
                              size_t count, helix_stream stream);
 
+/* -------------------------------------- chunked prefill (extension) ---- */
+/* The reference's paged attention with a T-token tail (cuda_paged.cu:483-548,
+ * paged_reference.cpp:173-384) for `batch` sequences at once, computed on
+ * the matrix cores (fp32 MFMA): query row t of sequence b sees the
+ * lengths[b] history tokens of row b of `tables` and chunk rows 0..t.
+ * head_dim 128, 16-token pages, q_heads / kv_heads in {1, 2, 4, 8}:
+ *   query, output [batch, q_heads, tokens, 128];
+ *   chunk_key, chunk_value [batch, kv_heads, tokens, 128];
+ *   tables [batch, max_blocks] uint32; lengths [batch] int32. */
+int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_heads,
+                                  size_t kv_heads, size_t tokens, const float* key_blocks,
+                                  const float* value_blocks, size_t physical_blocks,
+                                  const uint32_t* tables, size_t max_blocks,
+                                  const int32_t* lengths, const float* chunk_key,
+                                  const float* chunk_value, float* output, helix_stream stream);
+/* Chunk append (PagedKvCache::append_layer_major, paged.cpp:721-871, for one
+ * layer of `batch` sequences): rows [batch, kv_heads, tokens, head_dim] go
+ * to slots[b * tokens + t] = block * block_tokens + offset (negative:
+ * skipped). */
+int helix_paged_append_chunk(const float* keys, const float* values, float* key_blocks,
+                             float* value_blocks, size_t physical_blocks, size_t kv_heads,
+                             size_t block_tokens, size_t head_dim, const int64_t* slots,
+                             size_t batch, size_t tokens, helix_stream stream);
+
 /* A decode driver over a cache: persistent device block tables for a fixed
  * set of sequences.  prepare() reserves one slot per sequence (allocating
  * pages), append_layer() writes it, attention_layer() attends over the
- * history before the step plus the tail. */
+ * history before the step plus the tail.  prepare_chunk() reserves `tokens`
+ * slots per sequence instead; append_layer() then takes [batch, kv_heads,
+ * tokens, head_dim] rows and prefill_layer() runs the chunk attention. */
 int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* sequences,
                               size_t batch, size_t q_heads, size_t max_tokens,
                               size_t pages_per_split, helix_decode_batch** out);
 int helix_decode_batch_prepare(helix_decode_batch* b, helix_stream stream);
+int helix_decode_batch_prepare_chunk(helix_decode_batch* b, size_t tokens, helix_stream stream);
 int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
                                     const float* values, helix_stream stream);
 int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
                                        const float* tail_key, const float* tail_value,
                                        float* output, helix_stream stream);
+int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const float* query,
+                                     const float* chunk_key, const float* chunk_value,
+                                     float* output, helix_stream stream);
 int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tables,
                               const int32_t** lengths, const int64_t** slots,
                               size_t* max_blocks, size_t* pages_per_split);
