@@ -182,7 +182,7 @@ int helix_decode_view_layer_pools(const helix_decode_view* view, size_t layer,
 void helix_decode_view_poison(helix_decode_view* view);
 void helix_decode_view_release(helix_decode_view* view);
 
-/* PagedBlockTable (include/helix/kv_cache/cuda_block_table.hpp:134-169,
+/* PagedBlockTable (include/helix/kv_cache/cuda_block_table.hpp:16-47,
  * src/kv_cache/cuda_block_table.cpp:22-47): validates every ID against
  * physical_block_count, then uploads synchronously.  Empty tables own no
  * device memory and report a NULL data pointer. */
@@ -194,7 +194,7 @@ void helix_block_table_destroy(helix_block_table* table);
 
 /* ------------------------------------------- reference-shaped attention ---- */
 /* Shapes (the reference's attention::cuda contract, include/helix/attention/
- * cuda_paged.hpp:186-240):
+ * cuda_paged.hpp:15-69):
  *   query        [q_heads, queries, key_dim]
  *   key_blocks   [physical_blocks, kv_heads, block_tokens, key_dim]
  *   value_blocks [physical_blocks, kv_heads, block_tokens, value_dim]
