@@ -93,6 +93,66 @@ def build_workload(seed, batch, layers, steps_total, shuffle=True):
     return cache, seqs, lengths
 
 
+PREFIX_BATCH, PREFIX_TOKENS, PREFIX_PARTIAL = 128, 1024, 8
+
+
+def build_prefix_workload(seed, layers, steps_total):
+    """Config 4: 128 sequences share a 1024-token prefix (64 full pages at
+    refcount 128) plus an 8-token partial page that every fork copies on
+    write, so each sequence's first suffix token lands mid-page in its own
+    copy; then unique suffixes of uniform [64, 512] tokens."""
+    rng = np.random.default_rng(seed + 40)
+    root_len = PREFIX_TOKENS + PREFIX_PARTIAL
+    suffix = rng.integers(64, 513, size=PREFIX_BATCH)
+    own_pages = (PREFIX_PARTIAL + suffix + steps_total + P - 1) // P + 1
+    n_phys = int(root_len // P + 1 + own_pages.sum() + 16)
+    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys)
+    log(f"pool: {n_phys} blocks x {layers} layers ({n_phys * layers * 2 * HKV * P * D * 4 / 1e9:.1f} GB)")
+    tok = torch.zeros(layers, HKV, D, device="cuda:0")
+    dummies = []
+    for _ in range(n_phys):
+        s = cache.create_sequence()
+        cache.append(s, tok, tok)
+        dummies.append(s)
+    for i in rng.permutation(len(dummies)):
+        cache.release_sequence(dummies[int(i)])
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(seed)
+    n_src = HKV * max(root_len, int(suffix.max())) * D + 4096
+    src_k = torch.randn(layers, n_src, device="cuda:0", generator=gen)
+    src_v = torch.randn(layers, n_src, device="cuda:0", generator=gen)
+
+    def rows(src, n, off):
+        return [src[l, off: off + HKV * n * D].view(HKV, n, D) for l in range(layers)]
+
+    root = cache.create_sequence()
+    cache.append_layer_major(root, rows(src_k, root_len, 0), rows(src_v, root_len, 0))
+    seqs = [cache.fork_sequence(root, root_len, allow_cow=True) for _ in range(PREFIX_BATCH)]
+    cache.release_sequence(root)
+    for b, s in enumerate(seqs):
+        off = int(rng.integers(0, 1024)) * 4
+        n = int(suffix[b])
+        cache.append_layer_major(s, rows(src_k, n, off), rows(src_v, n, off))
+    del src_k, src_v
+    torch.cuda.empty_cache()
+    lengths = np.array([cache.length(s) for s in seqs], np.int64)
+    st = cache.stats()
+    log(f"prefix workload: shared blocks {st['shared_blocks']}, "
+        f"block references {st['block_reference_count']}")
+    return cache, seqs, lengths
+
+
+def unique_decode_bytes(lengths, shared_tokens=PREFIX_TOKENS, hq=HQ, hkv=HKV, d=D, p=P):
+    """HBM bytes of one config-4 decode launch when every shared prefix page
+    is read from HBM once: the logical formula with the shared tokens counted
+    once instead of once per sequence."""
+    lengths = np.asarray(lengths, np.int64)
+    shared = 2 * hkv * shared_tokens * d * 4
+    own = 2 * hkv * (lengths - shared_tokens) * d * 4
+    return int(shared + np.sum(own + 2 * hkv * d * 4 + 2 * hq * d * 4 +
+                               ((lengths + p - 1) // p) * 4))
+
+
 def cpu_baseline(cache, seqs, layers_multi, layers_single, threads, seed):
     """Times the CPU oracle (C++ restatement of the reference CPU paged
     attention, fp64 accumulation, GQA as replicated MHA) on the bench's own
@@ -358,9 +418,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shuffle", action="store_true",
                     help="allocate pages in pool order instead of scattering them")
-    ap.add_argument("--config", type=int, default=3, choices=(3, 5),
+    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
                     help="3: batched GQA decode (default, the headline metric); "
-                         "5: chunked prefill on the matrix cores")
+                         "4: prefix-sharing decode; 5: chunked prefill on the matrix cores")
     ap.add_argument("--cpu-seqs", type=int, default=4,
                     help="config 5: sequences of layer 0 timed on the CPU oracle")
     ap.add_argument("--copy-probe", action="store_true",
@@ -382,8 +442,12 @@ def main():
         return
     steps_total = args.warmup + args.steps + 2
     t_setup = time.perf_counter()
-    cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total,
-                                             shuffle=not args.no_shuffle)
+    if args.config == 4:
+        cache, seqs, lengths0 = build_prefix_workload(args.seed, args.layers, steps_total)
+    else:
+        cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total,
+                                                 shuffle=not args.no_shuffle)
+    nseq = len(seqs)
     log(f"setup {time.perf_counter() - t_setup:.1f}s; mean context {lengths0.mean():.0f}")
 
     batch = hx.DecodeBatch(cache, seqs, HQ, max_tokens=int(lengths0.max()) + steps_total + P,
@@ -392,10 +456,10 @@ def main():
     gen = torch.Generator(device="cuda:0")
     gen.manual_seed(args.seed + 1)
     L = args.layers
-    q = torch.randn(L, BATCH, HQ, D, device="cuda:0", generator=gen)
-    k = torch.randn(L, BATCH, HKV, D, device="cuda:0", generator=gen)
-    v = torch.randn(L, BATCH, HKV, D, device="cuda:0", generator=gen)
-    out = torch.empty(L, BATCH, HQ, D, device="cuda:0")
+    q = torch.randn(L, nseq, HQ, D, device="cuda:0", generator=gen)
+    k = torch.randn(L, nseq, HKV, D, device="cuda:0", generator=gen)
+    v = torch.randn(L, nseq, HKV, D, device="cuda:0", generator=gen)
+    out = torch.empty(L, nseq, HQ, D, device="cuda:0")
     stream = torch.cuda.current_stream()
     ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(L)]
           for _ in range(args.steps)]
@@ -428,16 +492,24 @@ def main():
     # warmup and earlier timed steps.
     per_step_decode = [decode_bytes(lengths0 + args.warmup + i) for i in range(args.steps)]
     launch_bytes = float(np.mean(per_step_decode))
-    step_decode = launch_bytes * L
-    step_append = append_bytes(BATCH) * L
+    if args.config == 4:
+        # Roofline on unique HBM bytes: shared prefix pages are read from HBM
+        # once per launch and served from cache to the other sequences.
+        roof_bytes = float(np.mean([unique_decode_bytes(lengths0 + args.warmup + i)
+                                    for i in range(args.steps)]))
+    else:
+        roof_bytes = launch_bytes
+    step_decode = roof_bytes * L
+    step_append = append_bytes(nseq) * L
     value = (step_decode + step_append) / (ms_per_step * 1e-3) / 1e9
     attn_avg_ms = float(np.mean(attn_ms))
     append_avg_ms = float(np.mean(append_ms))
-    achieved = launch_bytes / (attn_avg_ms * 1e-3) / 1e9
-    append_gbps = append_bytes(BATCH) / (append_avg_ms * 1e-3) / 1e9
+    achieved = roof_bytes / (attn_avg_ms * 1e-3) / 1e9
+    logical_gbps = launch_bytes / (attn_avg_ms * 1e-3) / 1e9
+    append_gbps = append_bytes(nseq) / (append_avg_ms * 1e-3) / 1e9
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_config3_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"decode_config{args.config}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -452,13 +524,30 @@ def main():
                "single_thread_value": None if gbps1 is None else round(gbps1, 3),
                "sample": f"CPU oracle (C++ restatement of the reference CPU paged attention, "
                          f"fp64 accumulation, GQA as replicated MHA), {threads} threads over "
-                         f"{args.cpu_layers} layers x all {BATCH} sequences ({secs:.1f} s wall), "
+                         f"{args.cpu_layers} layers x all {nseq} sequences ({secs:.1f} s wall), "
                          f"plus 1 thread over {args.cpu_single_layers} layer(s) ({secs1:.1f} s); "
                          f"same decode-bytes formula as the GPU; GPU kernel matched it on every "
                          f"sampled layer, max abs err {err:.2e}"}
 
+    if args.config == 4:
+        metric = ("prefix-sharing paged decode attn GB/s on unique HBM bytes + append GB/s, "
+                  "8B-GQA batch 128")
+        workload = {"workload": "config4: prefix-sharing decode, 128 sequences share a 1024-token "
+                                "prefix (refcount 128) + an 8-token copy-on-write partial page, "
+                                "unique suffixes U[64, 512], 32q/8kv heads, head_dim 128, page 16",
+                    "batch": nseq, "layers": L, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                    "block_tokens": P, "mean_context": float(lengths0.mean()),
+                    "pages_per_split": split}
+    else:
+        metric = "paged decode attn GB/s (% of HBM peak) + append GB/s, 8B-GQA batch 64"
+        workload = {"workload": "config3: Llama-3-8B GQA decode, 32 layers, batch 64, "
+                                "32q/8kv heads, head_dim 128, page 16, ctx log-uniform "
+                                "[512, 8192]",
+                    "batch": nseq, "layers": L, "q_heads": HQ, "kv_heads": HKV,
+                    "head_dim": D, "block_tokens": P, "mean_context": float(lengths0.mean()),
+                    "pages_per_split": split}
     line = {
-        "metric": "paged decode attn GB/s (% of HBM peak) + append GB/s, 8B-GQA batch 64",
+        "metric": metric,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -470,13 +559,10 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic N(0,1) K/V/Q, seeded; pages shuffled across the pool",
-        "config": {"workload": "config3: Llama-3-8B GQA decode, 32 layers, batch 64, "
-                               "32q/8kv heads, head_dim 128, page 16, ctx log-uniform [512, 8192]",
-                   "batch": BATCH, "layers": L, "q_heads": HQ, "kv_heads": HKV,
-                   "head_dim": D, "block_tokens": P, "mean_context": float(lengths0.mean()),
-                   "pages_per_split": split},
+        "config": workload,
         "decode_attn_gbps": round(achieved, 2),
         "decode_attn_hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "decode_attn_logical_gbps": round(logical_gbps, 2),
         "append_gbps": round(append_gbps, 2),
         "append_avg_us": round(append_avg_ms * 1e3, 2),
         "decode_avg_us": round(attn_avg_ms * 1e3, 2),

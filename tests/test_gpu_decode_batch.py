@@ -14,6 +14,7 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-5, 1e-4
+D, P = 128, 16
 
 
 def dev(a):
@@ -101,3 +102,72 @@ def test_decode_batch_validates(device):
     with pytest.raises(hx.HelixError):
         b.append_layer(1, x, x)  # layer out of range
     b.close()
+
+
+def test_prefix_sharing_decode_with_cow_forks(device):
+    """Config-4 shape in small: forks share the full prefix pages (refcount =
+    number of forks once the root is released) and copy the partial page on
+    write, so each first suffix token lands mid-page in a private copy.
+    Decode steps over the shared pages match the oracle; pages and stats
+    match the oracle pool bit-exactly."""
+    L, H, HQ = 2, 4, 16
+    rng = np.random.default_rng(44)
+    prefix, forks = 3 * P + 5, 6
+    suffix = [3, 11, 16, 27, 40, 64]
+    N = 64
+    cache = hx.PagedKvCache(L, H, D, P, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    root, root_o = cache.create_sequence(), pool.create_sequence()
+    k = rng.standard_normal((L, H, prefix, D), dtype=np.float32)
+    v = rng.standard_normal((L, H, prefix, D), dtype=np.float32)
+    cache.append_layer_major(root, [dev(k[l]) for l in range(L)], [dev(v[l]) for l in range(L)])
+    pool.append_layer_major(root_o, k, v)
+    seqs = []
+    for _ in range(forks):
+        s = cache.fork_sequence(root, prefix, allow_cow=True)
+        so = pool.fork_sequence(root_o, prefix, allow_cow=True)
+        seqs.append((s, so))
+    cache.release_sequence(root)
+    pool.release_sequence(root_o)
+    st = cache.stats()
+    assert st == pool.stats()
+    assert st["shared_blocks"] == prefix // P
+    for b, (s, so) in enumerate(seqs):
+        n = suffix[b]
+        k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        cache.append_layer_major(s, [dev(k[l]) for l in range(L)],
+                                 [dev(v[l]) for l in range(L)])
+        pool.append_layer_major(so, k, v)
+    B = len(seqs)
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], HQ, max_tokens=prefix + max(suffix) + 8)
+    for step in range(2):
+        batch.prepare()
+        hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+        tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+        for b, (_, so) in enumerate(seqs):
+            t = pool.block_table(so)
+            tables[b, : len(t)] = t
+        keys = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        values = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        for layer in range(L):
+            q = rng.standard_normal((B, HQ, D), dtype=np.float32)
+            out = torch.empty(B, HQ, D, device=device)
+            batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+            batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            torch.cuda.synchronize()
+            kp, vp = pool.layer_pages(layer)
+            ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
+                                        threads=8)
+            np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+        for b, (_, so) in enumerate(seqs):
+            pool.append(so, keys[:, b], values[:, b])
+    assert cache.stats() == pool.stats()
+    for s, so in seqs:
+        assert cache.block_table(s) == pool.block_table(so).tolist()
+        for layer in range(L):
+            gk, gv = cache.retrieve_layer(s, layer)
+            ok, ov = pool.copy_layer(so, layer)
+            np.testing.assert_array_equal(host(gk), ok)
+            np.testing.assert_array_equal(host(gv), ov)
+    batch.close()
