@@ -282,6 +282,7 @@ struct DecodeKernelArgs {
   int pages_per_split;
   std::uint32_t physical_blocks;
   float qscale;
+  int stream_waves;     // grid size of the stream kernel (stream mode)
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -652,6 +653,424 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeKernelArgs a) {
   }
 }
 
+// ------------------------------------------------------ stream decode ----
+// Persistent decode: the grid is one wavefront per resident slot, and the
+// work is the flat list of pages of all (sequence, kv head) units in order,
+// each unit contributing its history pages plus one pseudo-page for the
+// uncommitted tail.  Wavefront w takes the contiguous range
+// [w * C, (w + 1) * C) of that list, C = ceil(total / waves), so every
+// wavefront moves the same bytes and keeps its two-page prefetch running
+// across unit boundaries: a wavefront pays the start-up latency (length
+// scan, table, first pages) once per launch instead of once per split, and
+// the launch has no tail of short items.  Each page buffer carries its
+// unit's query rows, so switching units never waits on a load.
+//
+// A unit that one wavefront covers completely is finished in place.
+// Otherwise each wavefront touching unit u leaves a partial at slot u + w;
+// the slots of one unit are contiguous (u + w_first .. u + w_last) and no two
+// units share a slot, since the next unit starts at or after w_last.
+// decode_stream_merge_kernel combines them.
+__device__ __forceinline__ int unit_pages(int hist) {
+  return (hist < 0 ? 0 : (hist + 15) / 16) + 1;
+}
+
+// Marks a wave-uniform 64-bit value as such (scalar registers), so control
+// flow on it stays uniform and dependent loads stay scalar.
+__device__ __forceinline__ long long uniform64(long long v) {
+  const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(v));
+  const unsigned hi =
+      __builtin_amdgcn_readfirstlane(static_cast<unsigned>(static_cast<unsigned long long>(v) >> 32));
+  return static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ long long wave_sum(long long v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Total pages of the launch (all kv heads), computed identically by the
+// decode and the merge kernel.
+__device__ __forceinline__ long long stream_total_pages(const DecodeKernelArgs& a, int lane) {
+  long long total = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+    const int bb = c0 + lane;
+    const int w = bb < a.batch ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
+    total += wave_sum(w);
+  }
+  return total * a.kv_heads;
+}
+
+// First page of sequence b over all kv heads: kv_heads * sum_{b' < b} pages.
+__device__ __forceinline__ long long stream_sequence_start(const DecodeKernelArgs& a, int b,
+                                                           int lane) {
+  long long start = 0;
+  for (int c0 = 0; c0 < b; c0 += 64) {
+    const int bb = c0 + lane;
+    const int w = bb < b ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
+    start += wave_sum(w);
+  }
+  return start * a.kv_heads;
+}
+
+struct PageDesc {
+  int b, kvh, p, np, hist;
+  long long g;
+  bool skip;
+};
+
+template <int G>
+__global__ __launch_bounds__(64) void decode_stream_kernel(
+    DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
+    const std::int32_t* __restrict__ lengths, float* __restrict__ out,
+    float* __restrict__ part_o, float* __restrict__ part_ml) {
+  // The block table and lengths are read-only here and do not alias the
+  // outputs; with the restrict-qualified parameters their uniform reads
+  // become scalar loads.
+  a.tables = tables;
+  a.lengths = lengths;
+  a.out = out;
+  a.part_o = part_o;
+  a.part_ml = part_ml;
+  constexpr int D = 128;
+  constexpr int P = 16;
+  constexpr int R = G >= 4 ? G / 4 : 1;
+  constexpr int DUPB = G >= 4 ? 0 : (G == 2 ? 1 : 2);
+  constexpr int NV = 8 * G;
+
+  __shared__ __align__(16) float s_p[2][NV];
+  __shared__ __align__(16) float s_head[3][G];
+
+  const int lane = threadIdx.x;
+  const int parity = lane >> 5;
+  const int j = lane & 31;
+  const int wave = blockIdx.x;
+
+  const long long total = uniform64(stream_total_pages(a, lane));
+  const long long C = uniform64((total + a.stream_waves - 1) / a.stream_waves);
+  const long long g0 = uniform64(static_cast<long long>(wave) * C);
+  if (g0 >= total) return;
+  const long long g1 = uniform64(g0 + C < total ? g0 + C : total);
+
+  // Unit and page of g0: scan sequences weighted kv_heads * pages.
+  PageDesc cur{};
+  {
+    long long base = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+      const int bb = c0 + lane;
+      const int np = bb < a.batch ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
+      const long long w = static_cast<long long>(np) * a.kv_heads;
+      long long incl = w;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const long long t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+      }
+      const unsigned long long hit =
+          __ballot(bb < a.batch && base + incl - w <= g0 && g0 < base + incl);
+      if (hit != 0) {
+        const int src = __ffsll(static_cast<long long>(hit)) - 1;
+        cur.b = c0 + src;
+        const long long rem = g0 - (base + __shfl(incl - w, src, 64));
+        cur.np = __shfl(np, src, 64);
+        cur.kvh = static_cast<int>(rem / cur.np);
+        cur.p = static_cast<int>(rem % cur.np);
+        break;
+      }
+      base += __shfl(incl, 63, 64);
+    }
+  }
+  cur.b = __builtin_amdgcn_readfirstlane(cur.b);
+  cur.kvh = __builtin_amdgcn_readfirstlane(cur.kvh);
+  cur.p = __builtin_amdgcn_readfirstlane(cur.p);
+  cur.np = __builtin_amdgcn_readfirstlane(cur.np);
+  cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
+  cur.g = g0;
+  cur.skip = false;
+
+  const std::size_t page_elems = static_cast<std::size_t>(P) * D;
+  PageDesc last = cur;
+  // Descriptor of the next page to load; past the range it repeats the last
+  // real page (a valid address) marked skip.
+  auto next_desc = [&]() -> PageDesc {
+    if (cur.g >= g1) {
+      PageDesc d = last;
+      d.skip = true;
+      return d;
+    }
+    PageDesc d = cur;
+    last = cur;
+    ++cur.g;
+    if (++cur.p == cur.np) {
+      cur.p = 0;
+      if (++cur.kvh == a.kv_heads) {
+        cur.kvh = 0;
+        if (cur.g < g1) {
+          cur.b = __builtin_amdgcn_readfirstlane(cur.b + 1);
+          cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
+          cur.np = unit_pages(cur.hist);
+        }
+      }
+    }
+    return d;
+  };
+
+  // Unconditional loads of one page (or the tail row, every lane reading
+  // its 4 dims for all 8 slots) plus the unit's query rows.
+  auto load_page = [&](const PageDesc& d, float4 (&k)[8], float4 (&v)[8], float4 (&q)[G],
+                       bool& bad) {
+    const int b = __builtin_amdgcn_readfirstlane(d.b);
+    const int kvh = __builtin_amdgcn_readfirstlane(d.kvh);
+    const int p = __builtin_amdgcn_readfirstlane(d.p);
+    const bool tail = p == __builtin_amdgcn_readfirstlane(d.np) - 1;
+    const float* kb;
+    const float* vb;
+    bad = d.hist < 0;
+    if (tail) {
+      const std::size_t row = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * D;
+      kb = a.tail_key + row;
+      vb = a.tail_value + row;
+    } else {
+      std::uint32_t phys = __builtin_amdgcn_readfirstlane(
+          a.tables[static_cast<std::size_t>(b) * a.max_blocks + p]);
+      if (phys >= a.physical_blocks) {
+        bad = true;
+        phys = 0;
+      }
+      const std::size_t off = (static_cast<std::size_t>(phys) * a.kv_heads + kvh) * page_elems;
+      kb = a.key_pool + off;
+      vb = a.value_pool + off;
+    }
+    const int stride = tail ? 0 : 64;
+    const int li = tail ? j : lane;
+    const float4* kp = reinterpret_cast<const float4*>(kb);
+    const float4* vp = reinterpret_cast<const float4*>(vb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k[i] = kp[i * stride + li];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = vp[i * stride + li];
+    const float4* qp = reinterpret_cast<const float4*>(
+        a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D);
+#pragma unroll
+    for (int h = 0; h < G; ++h) q[h] = qp[h * (D / 4) + j];
+  };
+
+  float acc[G][4];
+  float m[R], l[R];
+  bool unit_bad = false;
+  auto reset = [&]() {
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      m[r] = -INFINITY;
+      l[r] = 0.0f;
+    }
+    unit_bad = false;
+  };
+  reset();
+
+  auto process = [&](const float4 (&k)[8], float4 (&v)[8], const float4 (&q)[G], int valid) {
+    float xs[NV];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        xs[i * G + h] = q[h].x * k[i].x + q[h].y * k[i].y + q[h].z * k[i].z + q[h].w * k[i].w;
+      }
+    }
+    reduce_scores<G>(xs, j);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int vi = (j >> DUPB) * R + r;
+      const int tok = 2 * (vi / G) + parity;
+      const bool ok = tok < valid;
+      const float s = ok ? xs[r] * a.qscale : -INFINITY;
+      const float mn = fmaxf(m[r], token_max(s));
+      const float alpha = exp2_ratio(m[r], mn);
+      const float pr = ok ? exp2_ratio(s, mn) : 0.0f;
+      l[r] = l[r] * alpha + token_sum(pr);
+      m[r] = mn;
+      if ((j & ((1 << DUPB) - 1)) == 0) s_p[parity][vi] = pr;
+      if (parity == 0 && vi < G && (j & ((1 << DUPB) - 1)) == 0) s_head[0][vi] = alpha;
+    }
+    __syncthreads();
+    float pp[NV];
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i) {
+      const float4 t4 = reinterpret_cast<const float4*>(s_p[parity])[i];
+      pp[4 * i] = t4.x;
+      pp[4 * i + 1] = t4.y;
+      pp[4 * i + 2] = t4.z;
+      pp[4 * i + 3] = t4.w;
+    }
+    float al[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) al[h] = s_head[0][h];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool keep = 2 * i + parity < valid;
+      v[i].x = keep ? v[i].x : 0.0f;
+      v[i].y = keep ? v[i].y : 0.0f;
+      v[i].z = keep ? v[i].z : 0.0f;
+      v[i].w = keep ? v[i].w : 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      acc[h][0] *= al[h];
+      acc[h][1] *= al[h];
+      acc[h][2] *= al[h];
+      acc[h][3] *= al[h];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float pv = pp[i * G + h];
+        acc[h][0] += pv * v[i].x;
+        acc[h][1] += pv * v[i].y;
+        acc[h][2] += pv * v[i].z;
+        acc[h][3] += pv * v[i].w;
+      }
+    }
+  };
+
+  // Publishes the unit's result: the output itself when this wavefront saw
+  // the whole unit, else a partial (m, l, o) at slot unit + wave.
+  auto finalize = [&](const PageDesc& d) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[h][c] += half_xor(acc[h][c]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int vi = (j >> DUPB) * R + r;
+      if (parity == 0 && vi < G && (j & ((1 << DUPB) - 1)) == 0) {
+        s_head[1][vi] = m[r];
+        s_head[2][vi] = unit_bad ? NAN : l[r];
+      }
+    }
+    __syncthreads();
+    const std::size_t unit = static_cast<std::size_t>(d.b) * a.kv_heads + d.kvh;
+    const bool complete = d.p == d.np - 1 && d.g - d.p >= g0;
+    if (parity == 0) {
+      if (complete) {
+        const std::size_t qrow0 = static_cast<std::size_t>(d.b) * a.q_heads + d.kvh * G;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float mh = s_head[1][h];
+          const float lh = s_head[2][h];
+          float4 o;
+          if (mh == -INFINITY) {
+            o = make_float4(NAN, NAN, NAN, NAN);
+          } else {
+            const float inv = 1.0f / lh;
+            o = make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+          }
+          reinterpret_cast<float4*>(a.out + (qrow0 + h) * D)[j] = o;
+        }
+      } else {
+        const std::size_t slot = unit + wave;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          reinterpret_cast<float4*>(a.part_o + (slot * G + h) * D)[j] =
+              make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        }
+        if (j < G) {
+          a.part_ml[(slot * G + j) * 2] = s_head[1][j];
+          a.part_ml[(slot * G + j) * 2 + 1] = s_head[2][j];
+        }
+      }
+    }
+    __syncthreads();
+    reset();
+  };
+
+  auto step = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8], const float4 (&q)[G],
+                  bool bad) {
+    int valid = 0;
+    if (!d.skip) {
+      valid = d.p == d.np - 1 ? 1 : min(P, d.hist - d.p * P);
+      unit_bad = unit_bad || bad;
+    }
+    process(k, v, q, valid);
+    if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
+  };
+
+  float4 ka[8], va[8], kb[8], vb[8];
+  float4 qa[G], qb[G];
+  bool bada, badb;
+  PageDesc da = next_desc();
+  load_page(da, ka, va, qa, bada);
+  PageDesc db = next_desc();
+  load_page(db, kb, vb, qb, badb);
+  for (long long g = g0; g < g1; g += 2) {
+    step(da, ka, va, qa, bada);
+    da = next_desc();
+    load_page(da, ka, va, qa, bada);
+    step(db, kb, vb, qb, badb);
+    db = next_desc();
+    load_page(db, kb, vb, qb, badb);
+  }
+}
+
+// Combines the partials of units that span several stream wavefronts.  One
+// workgroup per unit; thread (h, d4) of G * 32 threads owns 4 output dims of
+// query head h.
+template <int G>
+__global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeKernelArgs a) {
+  constexpr int D = 128;
+  __shared__ long long s_geo[2];
+  const int unit = blockIdx.x;
+  const int b = unit / a.kv_heads;
+  const int kvh = unit % a.kv_heads;
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    const long long total = stream_total_pages(a, tid);
+    const long long start = stream_sequence_start(a, b, tid);
+    if (tid == 0) {
+      s_geo[0] = total;
+      s_geo[1] = start;
+    }
+  }
+  __syncthreads();
+  const long long total = s_geo[0];
+  const int np = unit_pages(clamp_length(a.lengths[b], a.max_blocks));
+  const long long start = s_geo[1] + static_cast<long long>(kvh) * np;
+  const long long C = (total + a.stream_waves - 1) / a.stream_waves;
+  const long long w_first = start / C;
+  const long long w_last = (start + np - 1) / C;
+  if (w_first == w_last || tid >= G * (D / 4)) return;
+  const int h = tid / (D / 4);
+  const int d4 = tid % (D / 4);
+  const std::size_t slot0 = static_cast<std::size_t>(unit + w_first);
+  const int segs = static_cast<int>(w_last - w_first + 1);
+  float mx = -INFINITY;
+  for (int s = 0; s < segs; ++s) mx = fmaxf(mx, a.part_ml[((slot0 + s) * G + h) * 2]);
+  float den = 0.0f;
+  float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = 0; s < segs; ++s) {
+    const float w = exp2_ratio(a.part_ml[((slot0 + s) * G + h) * 2], mx);
+    den += w * a.part_ml[((slot0 + s) * G + h) * 2 + 1];
+    const float4 o = reinterpret_cast<const float4*>(a.part_o + ((slot0 + s) * G + h) * D)[d4];
+    num.x += w * o.x;
+    num.y += w * o.y;
+    num.z += w * o.z;
+    num.w += w * o.w;
+  }
+  float4 r;
+  if (mx == -INFINITY) {
+    r = make_float4(NAN, NAN, NAN, NAN);
+  } else {
+    const float inv = 1.0f / den;
+    r = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+  }
+  const std::size_t qrow = static_cast<std::size_t>(b) * a.q_heads + kvh * G + h;
+  reinterpret_cast<float4*>(a.out + qrow * D)[d4] = r;
+}
+
 __global__ void zero_words_kernel(unsigned* p, std::size_t n) {
   const std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
   if (i < n) p[i] = 0u;
@@ -918,16 +1337,27 @@ WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t k
   return l;
 }
 
+// Stream mode: one partial slot per (sequence, kv head) unit plus one per
+// wavefront (slot = unit + wavefront).
+WorkspaceLayout stream_layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads) {
+  return layout_for(batch * kv_heads + kMaxStreamWaves, q_heads / kv_heads, 1, 1);
+}
+
 }  // namespace
 
 std::size_t decode_max_splits(std::size_t max_blocks, std::size_t pages_per_split) {
+  if (pages_per_split == 0) return 1;
   const std::size_t s = (max_blocks + pages_per_split - 1) / pages_per_split;
   return s == 0 ? 1 : s;
 }
 
 std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
                                    std::size_t max_blocks, std::size_t pages_per_split) {
-  if (kv_heads == 0 || q_heads % kv_heads != 0 || pages_per_split == 0) return 0;
+  if (kv_heads == 0 || q_heads % kv_heads != 0) return 0;
+  if (pages_per_split == 0) {
+    // Stream mode: one partial slot per unit plus one per wavefront.
+    return stream_layout_for(batch, q_heads, kv_heads).total;
+  }
   return layout_for(batch, q_heads, kv_heads, decode_max_splits(max_blocks, pages_per_split)).total;
 }
 
@@ -945,6 +1375,7 @@ bool decode_group_supported(std::size_t group) {
 
 std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::size_t kv_heads,
                          std::size_t max_blocks, std::size_t pages_per_split) {
+  if (pages_per_split == 0) return 0;  // stream mode sizes its own grid
   std::size_t items = 0;
   for (std::size_t b = 0; b < batch; ++b) {
     const std::int64_t h = lengths[b];
@@ -956,10 +1387,35 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
   return items;
 }
 
+namespace {
+
+// Wavefronts the stream kernel launches: every resident slot of the device
+// (two per SIMD up to four query heads per kv head, one for eight, as the
+// kernels' register use allows), at most kMaxStreamWaves.
+std::size_t stream_waves(std::size_t group) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      n = 256;
+    }
+    cus[dev] = n;
+  }
+  const std::size_t per_simd = group >= 8 ? 1 : 2;
+  const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
+  return w < kMaxStreamWaves ? w : kMaxStreamWaves;
+}
+
+}  // namespace
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if (a.batch == 0) return hipSuccess;
+  const bool streamed = a.pages_per_split == 0;
   const std::size_t max_splits = decode_max_splits(a.max_blocks, a.pages_per_split);
-  const WorkspaceLayout lay = layout_for(a.batch, a.q_heads, a.kv_heads, max_splits);
+  const std::size_t group = a.q_heads / a.kv_heads;
   auto* ws = static_cast<unsigned char*>(a.workspace);
   DecodeKernelArgs k{};
   k.query = a.query;
@@ -970,8 +1426,6 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.tail_key = a.tail_key;
   k.tail_value = a.tail_value;
   k.out = a.out;
-  k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
-  k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   k.batch = static_cast<int>(a.batch);
   k.q_heads = static_cast<int>(a.q_heads);
   k.kv_heads = static_cast<int>(a.kv_heads);
@@ -980,11 +1434,39 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.pages_per_split = static_cast<int>(a.pages_per_split);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
+  if (streamed) {
+    const std::size_t waves = stream_waves(group);
+    const WorkspaceLayout lay = stream_layout_for(a.batch, a.q_heads, a.kv_heads);
+    k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+    k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+    k.stream_waves = static_cast<int>(waves);
+    const dim3 grid(static_cast<unsigned>(waves));
+    switch (group) {
+      case 1: decode_stream_kernel<1><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
+      case 2: decode_stream_kernel<2><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
+      case 4: decode_stream_kernel<4><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
+      case 8: decode_stream_kernel<8><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
+      default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
+    switch (group) {
+      case 1: decode_stream_merge_kernel<1><<<mgrid, 256, 0, stream>>>(k); break;
+      case 2: decode_stream_merge_kernel<2><<<mgrid, 256, 0, stream>>>(k); break;
+      case 4: decode_stream_merge_kernel<4><<<mgrid, 256, 0, stream>>>(k); break;
+      case 8: decode_stream_merge_kernel<8><<<mgrid, 256, 0, stream>>>(k); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  const WorkspaceLayout lay = layout_for(a.batch, a.q_heads, a.kv_heads, max_splits);
+  k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   // Items beyond the real work (when the caller passes no exact count)
   // return at once.
   const std::size_t items = a.items != 0 ? a.items : a.batch * a.kv_heads * max_splits;
   const dim3 grid(static_cast<unsigned>(items));
-  const std::size_t group = a.q_heads / a.kv_heads;
   switch (group) {
     case 1: decode_split_kernel<1><<<grid, 64, 0, stream>>>(k); break;
     case 2: decode_split_kernel<2><<<grid, 64, 0, stream>>>(k); break;

@@ -63,8 +63,9 @@ hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
                                 hipStream_t stream);
 
 // ------------------------------------------------------------- decode ----
-// Batched one-token decode with an uncommitted tail (split-K over pages with
-// an in-kernel merge).
+// Batched one-token decode with an uncommitted tail: split-K over pages
+// (explicit pages_per_split) or the persistent stream kernel (0), each
+// followed by a merge of the partials.
 //   query      [batch, q_heads, 128]
 //   tables     [batch, max_blocks] physical block IDs
 //   lengths    [batch] committed history tokens per sequence
@@ -93,9 +94,13 @@ struct DecodeArgs {
 
 constexpr std::size_t kDecodeHeadDim = 128;
 constexpr std::size_t kDecodeBlockTokens = 16;
-constexpr std::size_t kDefaultPagesPerSplit = 16;
-// Largest split count per sequence the merge kernel's LDS holds.
+// pages_per_split == 0 selects the persistent stream kernel (the default):
+// one wavefront per resident slot streams an equal share of all pages.
+constexpr std::size_t kDefaultPagesPerSplit = 0;
+// Largest split count per sequence the split-mode merge kernel's LDS holds.
 constexpr std::size_t kMaxDecodeSplits = 4096;
+// Most wavefronts a stream-mode launch uses (sizes its partial slots).
+constexpr std::size_t kMaxStreamWaves = 4096;
 
 std::size_t decode_max_splits(std::size_t max_blocks, std::size_t pages_per_split);
 std::size_t decode_workspace_bytes(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
