@@ -283,6 +283,7 @@ struct DecodeKernelArgs {
   std::uint32_t physical_blocks;
   float qscale;
   int stream_waves;     // grid size of the stream kernel (stream mode)
+  int* segments;        // [units] (first wavefront, wavefront count), stream mode
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -655,9 +656,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeKernelArgs a) {
 
 // ------------------------------------------------------ stream decode ----
 // Persistent decode: the grid is one wavefront per resident slot, and the
-// work is the flat list of pages of all (sequence, kv head) units in order,
-// each unit contributing its history pages plus one pseudo-page for the
-// uncommitted tail.  Wavefront w takes the contiguous range
+// work is the flat list of pages of all (sequence, kv head) units, kv head
+// major (unit index kvh * batch + b), each unit contributing its history
+// pages plus one pseudo-page for the uncommitted tail.  Kv-head-major order
+// keeps the wavefronts that run side by side on different sequences, i.e.
+// on unrelated physical blocks, rather than on the neighbouring kv-head
+// pages of one block.  Wavefront w takes the contiguous range
 // [w * C, (w + 1) * C) of that list, C = ceil(total / waves), so every
 // wavefront moves the same bytes and keeps its two-page prefetch running
 // across unit boundaries: a wavefront pays the start-up latency (length
@@ -689,28 +693,17 @@ __device__ __forceinline__ long long wave_sum(long long v) {
   return v;
 }
 
-// Total pages of the launch (all kv heads), computed identically by the
-// decode and the merge kernel.
-__device__ __forceinline__ long long stream_total_pages(const DecodeKernelArgs& a, int lane) {
-  long long total = 0;
-  for (int c0 = 0; c0 < a.batch; c0 += 64) {
+// Pages of sequences [0, upto) for one kv head: sum of unit_pages.  The
+// decode and the merge kernel compute it identically.
+__device__ __forceinline__ long long stream_pages_before(const DecodeKernelArgs& a, int upto,
+                                                         int lane) {
+  long long sum = 0;
+  for (int c0 = 0; c0 < upto; c0 += 64) {
     const int bb = c0 + lane;
-    const int w = bb < a.batch ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
-    total += wave_sum(w);
+    const int w = bb < upto ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
+    sum += wave_sum(w);
   }
-  return total * a.kv_heads;
-}
-
-// First page of sequence b over all kv heads: kv_heads * sum_{b' < b} pages.
-__device__ __forceinline__ long long stream_sequence_start(const DecodeKernelArgs& a, int b,
-                                                           int lane) {
-  long long start = 0;
-  for (int c0 = 0; c0 < b; c0 += 64) {
-    const int bb = c0 + lane;
-    const int w = bb < b ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
-    start += wave_sum(w);
-  }
-  return start * a.kv_heads;
+  return sum;
 }
 
 struct PageDesc {
@@ -723,7 +716,7 @@ template <int G>
 __global__ __launch_bounds__(64) void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
-    float* __restrict__ part_o, float* __restrict__ part_ml) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments) {
   // The block table and lengths are read-only here and do not alias the
   // outputs; with the restrict-qualified parameters their uniform reads
   // become scalar loads.
@@ -732,6 +725,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   a.out = out;
   a.part_o = part_o;
   a.part_ml = part_ml;
+  a.segments = segments;
   constexpr int D = 128;
   constexpr int P = 16;
   constexpr int R = G >= 4 ? G / 4 : 1;
@@ -746,35 +740,44 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   const int j = lane & 31;
   const int wave = blockIdx.x;
 
-  const long long total = uniform64(stream_total_pages(a, lane));
+  // One pass over the lengths when the batch fits a wavefront (lane b holds
+  // sequence b), a second one only for larger batches.
+  const int hist0 = lane < a.batch ? clamp_length(a.lengths[lane], a.max_blocks) : -1;
+  const int np0 = lane < a.batch ? unit_pages(hist0) : 0;
+  long long per_head = wave_sum(np0);
+  if (a.batch > 64) per_head += stream_pages_before(a, a.batch, lane) - per_head;
+  per_head = uniform64(per_head);
+  const long long total = per_head * a.kv_heads;
   const long long C = uniform64((total + a.stream_waves - 1) / a.stream_waves);
   const long long g0 = uniform64(static_cast<long long>(wave) * C);
   if (g0 >= total) return;
   const long long g1 = uniform64(g0 + C < total ? g0 + C : total);
 
-  // Unit and page of g0: scan sequences weighted kv_heads * pages.
+  // Unit and page of g0: kv head = g0 / per_head, then scan sequences.
   PageDesc cur{};
+  cur.kvh = static_cast<int>(g0 / per_head);
   {
+    const long long rem0 = g0 - static_cast<long long>(cur.kvh) * per_head;
     long long base = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
       const int bb = c0 + lane;
-      const int np = bb < a.batch ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
-      const long long w = static_cast<long long>(np) * a.kv_heads;
-      long long incl = w;
+      const int hist =
+          c0 == 0 ? hist0 : (bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1);
+      const int np = c0 == 0 ? np0 : (bb < a.batch ? unit_pages(hist) : 0);
+      long long incl = np;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const long long t = __shfl_up(incl, o, 64);
         if (lane >= o) incl += t;
       }
       const unsigned long long hit =
-          __ballot(bb < a.batch && base + incl - w <= g0 && g0 < base + incl);
+          __ballot(bb < a.batch && base + incl - np <= rem0 && rem0 < base + incl);
       if (hit != 0) {
         const int src = __ffsll(static_cast<long long>(hit)) - 1;
         cur.b = c0 + src;
-        const long long rem = g0 - (base + __shfl(incl - w, src, 64));
+        cur.p = static_cast<int>(rem0 - (base + __shfl(incl - np, src, 64)));
         cur.np = __shfl(np, src, 64);
-        cur.kvh = static_cast<int>(rem / cur.np);
-        cur.p = static_cast<int>(rem % cur.np);
+        cur.hist = __shfl(hist, src, 64);
         break;
       }
       base += __shfl(incl, 63, 64);
@@ -784,7 +787,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   cur.kvh = __builtin_amdgcn_readfirstlane(cur.kvh);
   cur.p = __builtin_amdgcn_readfirstlane(cur.p);
   cur.np = __builtin_amdgcn_readfirstlane(cur.np);
-  cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
+  cur.hist = __builtin_amdgcn_readfirstlane(cur.hist);
   cur.g = g0;
   cur.skip = false;
 
@@ -803,20 +806,23 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     ++cur.g;
     if (++cur.p == cur.np) {
       cur.p = 0;
-      if (++cur.kvh == a.kv_heads) {
-        cur.kvh = 0;
-        if (cur.g < g1) {
-          cur.b = __builtin_amdgcn_readfirstlane(cur.b + 1);
-          cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
-          cur.np = unit_pages(cur.hist);
-        }
+      if (++cur.b == a.batch) {
+        cur.b = 0;
+        ++cur.kvh;
+      }
+      if (cur.g < g1) {
+        cur.b = __builtin_amdgcn_readfirstlane(cur.b);
+        cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
+        cur.np = unit_pages(cur.hist);
       }
     }
     return d;
   };
 
-  // Unconditional loads of one page (or the tail row, every lane reading
-  // its 4 dims for all 8 slots) plus the unit's query rows.
+  // Loads of one page (or the tail row, every lane reading its 4 dims for
+  // all 8 slots).  The first page of a unit in this wavefront also brings the
+  // unit's query rows, issued ahead of the page so that waiting for the page
+  // covers them.
   auto load_page = [&](const PageDesc& d, float4 (&k)[8], float4 (&v)[8], float4 (&q)[G],
                        bool& bad) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
@@ -841,6 +847,12 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       kb = a.key_pool + off;
       vb = a.value_pool + off;
     }
+    if (p == 0 || d.g == g0) {
+      const float4* qp = reinterpret_cast<const float4*>(
+          a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D);
+#pragma unroll
+      for (int h = 0; h < G; ++h) q[h] = qp[h * (D / 4) + j];
+    }
     const int stride = tail ? 0 : 64;
     const int li = tail ? j : lane;
     const float4* kp = reinterpret_cast<const float4*>(kb);
@@ -849,10 +861,6 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     for (int i = 0; i < 8; ++i) k[i] = kp[i * stride + li];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = vp[i * stride + li];
-    const float4* qp = reinterpret_cast<const float4*>(
-        a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D);
-#pragma unroll
-    for (int h = 0; h < G; ++h) q[h] = qp[h * (D / 4) + j];
   };
 
   float acc[G][4];
@@ -953,7 +961,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       }
     }
     __syncthreads();
-    const std::size_t unit = static_cast<std::size_t>(d.b) * a.kv_heads + d.kvh;
+    const std::size_t unit = static_cast<std::size_t>(d.kvh) * a.batch + d.b;
     const bool complete = d.p == d.np - 1 && d.g - d.p >= g0;
     if (parity == 0) {
       if (complete) {
@@ -988,19 +996,33 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     reset();
   };
 
-  auto step = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8], const float4 (&q)[G],
+  float4 qc[G];  // query rows of the unit being processed
+  auto step = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8], const float4 (&qn)[G],
                   bool bad) {
     int valid = 0;
     if (!d.skip) {
       valid = d.p == d.np - 1 ? 1 : min(P, d.hist - d.p * P);
       unit_bad = unit_bad || bad;
+      if (d.p == 0 || d.g == g0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) qc[h] = qn[h];
+      }
+      if (d.p == 0 && lane == 0) {
+        // This wavefront holds the unit's first page: record which
+        // wavefronts hold its partials for the merge.
+        const long long last_wave = (d.g + d.np - 1) / C;
+        reinterpret_cast<int2*>(a.segments)[static_cast<std::size_t>(d.kvh) * a.batch + d.b] =
+            make_int2(wave, static_cast<int>(last_wave - wave + 1));
+      }
     }
-    process(k, v, q, valid);
+    process(k, v, qc, valid);
     if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
   };
 
   float4 ka[8], va[8], kb[8], vb[8];
   float4 qa[G], qb[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) qa[h] = qb[h] = qc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
   bool bada, badb;
   PageDesc da = next_desc();
   load_page(da, ka, va, qa, bada);
@@ -1017,48 +1039,58 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
 }
 
 // Combines the partials of units that span several stream wavefronts.  One
-// workgroup per unit; thread (h, d4) of G * 32 threads owns 4 output dims of
-// query head h.
+// workgroup of G * 32 threads per unit (kv head major: unit = kvh * batch +
+// b); thread (h, d4) owns 4 output dims of query head h.  The unit's
+// wavefront range was recorded by the stream kernel, so the partial loads
+// are issued at once.
 template <int G>
 __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeKernelArgs a) {
   constexpr int D = 128;
-  __shared__ long long s_geo[2];
   const int unit = blockIdx.x;
-  const int b = unit / a.kv_heads;
-  const int kvh = unit % a.kv_heads;
+  const int2 seg = reinterpret_cast<const int2*>(a.segments)[unit];
+  if (seg.y <= 1) return;
+  const int kvh = unit / a.batch;
+  const int b = unit % a.batch;
   const int tid = threadIdx.x;
-  if (tid < 64) {
-    const long long total = stream_total_pages(a, tid);
-    const long long start = stream_sequence_start(a, b, tid);
-    if (tid == 0) {
-      s_geo[0] = total;
-      s_geo[1] = start;
-    }
-  }
-  __syncthreads();
-  const long long total = s_geo[0];
-  const int np = unit_pages(clamp_length(a.lengths[b], a.max_blocks));
-  const long long start = s_geo[1] + static_cast<long long>(kvh) * np;
-  const long long C = (total + a.stream_waves - 1) / a.stream_waves;
-  const long long w_first = start / C;
-  const long long w_last = (start + np - 1) / C;
-  if (w_first == w_last || tid >= G * (D / 4)) return;
   const int h = tid / (D / 4);
   const int d4 = tid % (D / 4);
-  const std::size_t slot0 = static_cast<std::size_t>(unit + w_first);
-  const int segs = static_cast<int>(w_last - w_first + 1);
+  const std::size_t slot0 = static_cast<std::size_t>(unit) + seg.x;
+  // Online merge over chunks of 8 partials; each chunk's loads issue together.
+  constexpr int kChunk = 8;
   float mx = -INFINITY;
-  for (int s = 0; s < segs; ++s) mx = fmaxf(mx, a.part_ml[((slot0 + s) * G + h) * 2]);
   float den = 0.0f;
   float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s = 0; s < segs; ++s) {
-    const float w = exp2_ratio(a.part_ml[((slot0 + s) * G + h) * 2], mx);
-    den += w * a.part_ml[((slot0 + s) * G + h) * 2 + 1];
-    const float4 o = reinterpret_cast<const float4*>(a.part_o + ((slot0 + s) * G + h) * D)[d4];
-    num.x += w * o.x;
-    num.y += w * o.y;
-    num.z += w * o.z;
-    num.w += w * o.w;
+  for (int s0 = 0; s0 < seg.y; s0 += kChunk) {
+    float ms[kChunk], ls[kChunk];
+    float4 os[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const bool in = s0 + i < seg.y;
+      const std::size_t slot = slot0 + (in ? s0 + i : 0);
+      ms[i] = in ? a.part_ml[(slot * G + h) * 2] : -INFINITY;
+      ls[i] = in ? a.part_ml[(slot * G + h) * 2 + 1] : 0.0f;
+      os[i] = in ? reinterpret_cast<const float4*>(a.part_o + (slot * G + h) * D)[d4]
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float cm = mx;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, ms[i]);
+    const float sc = exp2_ratio(mx, cm);
+    den *= sc;
+    num.x *= sc;
+    num.y *= sc;
+    num.z *= sc;
+    num.w *= sc;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const float w = s0 + i < seg.y ? exp2_ratio(ms[i], cm) : 0.0f;
+      den += w * ls[i];
+      num.x += w * os[i].x;
+      num.y += w * os[i].y;
+      num.z += w * os[i].z;
+      num.w += w * os[i].w;
+    }
+    mx = cm;
   }
   float4 r;
   if (mx == -INFINITY) {
@@ -1323,7 +1355,7 @@ namespace {
 std::size_t align256(std::size_t n) { return (n + 255) & ~std::size_t{255}; }
 
 struct WorkspaceLayout {
-  std::size_t part_o, part_ml, total;
+  std::size_t part_o, part_ml, total, segments;
 };
 
 WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
@@ -1340,7 +1372,10 @@ WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t k
 // Stream mode: one partial slot per (sequence, kv head) unit plus one per
 // wavefront (slot = unit + wavefront).
 WorkspaceLayout stream_layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads) {
-  return layout_for(batch * kv_heads + kMaxStreamWaves, q_heads / kv_heads, 1, 1);
+  WorkspaceLayout l = layout_for(batch * kv_heads + kMaxStreamWaves, q_heads / kv_heads, 1, 1);
+  l.segments = l.total;
+  l.total += align256(batch * kv_heads * 2 * sizeof(int));
+  return l;
 }
 
 }  // namespace
@@ -1439,23 +1474,36 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const WorkspaceLayout lay = stream_layout_for(a.batch, a.q_heads, a.kv_heads);
     k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+    k.segments = reinterpret_cast<int*>(ws + lay.segments);
     k.stream_waves = static_cast<int>(waves);
     const dim3 grid(static_cast<unsigned>(waves));
     switch (group) {
-      case 1: decode_stream_kernel<1><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
-      case 2: decode_stream_kernel<2><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
-      case 4: decode_stream_kernel<4><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
-      case 8: decode_stream_kernel<8><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out, k.part_o, k.part_ml); break;
+      case 1:
+        decode_stream_kernel<1><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
+                                                         k.part_o, k.part_ml, k.segments);
+        break;
+      case 2:
+        decode_stream_kernel<2><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
+                                                         k.part_o, k.part_ml, k.segments);
+        break;
+      case 4:
+        decode_stream_kernel<4><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
+                                                         k.part_o, k.part_ml, k.segments);
+        break;
+      case 8:
+        decode_stream_kernel<8><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
+                                                         k.part_o, k.part_ml, k.segments);
+        break;
       default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
     switch (group) {
-      case 1: decode_stream_merge_kernel<1><<<mgrid, 256, 0, stream>>>(k); break;
-      case 2: decode_stream_merge_kernel<2><<<mgrid, 256, 0, stream>>>(k); break;
-      case 4: decode_stream_merge_kernel<4><<<mgrid, 256, 0, stream>>>(k); break;
-      case 8: decode_stream_merge_kernel<8><<<mgrid, 256, 0, stream>>>(k); break;
+      case 1: decode_stream_merge_kernel<1><<<mgrid, 1 * 32, 0, stream>>>(k); break;
+      case 2: decode_stream_merge_kernel<2><<<mgrid, 2 * 32, 0, stream>>>(k); break;
+      case 4: decode_stream_merge_kernel<4><<<mgrid, 4 * 32, 0, stream>>>(k); break;
+      case 8: decode_stream_merge_kernel<8><<<mgrid, 8 * 32, 0, stream>>>(k); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
