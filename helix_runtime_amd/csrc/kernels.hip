@@ -198,27 +198,46 @@ __global__ void table_update_kernel(std::uint32_t* tables, std::size_t cols,
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
 // ------------------------------------------------------------- decode ----
-// Cross-lane helpers.  ds_swizzle in bit mode exchanges with lane ^ MASK
-// inside each 32-lane half; the two halves are combined with ds_bpermute.
-template <int MASK>
-__device__ __forceinline__ float swz_xor(float x) {
-  static_assert(MASK >= 1 && MASK <= 16, "swizzle masks stay inside a 32-lane half");
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (MASK << 10) | 0x1F));
+// Cross-lane helpers, all VALU (no LDS pipe):
+//   DPP within a 16-lane row: row_ror:8 pairs lane i with i ^ 8, row_ror:4
+//   with (i + 4) mod 16, the row half-mirror pairs i with 7 - i inside each
+//   8-lane group, quad permutes give i ^ 1 and i ^ 2;
+//   v_permlane16_swap exchanges the odd 16-lane rows of its first operand
+//   with the even rows of its second, v_permlane32_swap the upper 32 lanes of
+//   the first with the lower 32 of the second.
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowHalfMirror = 0x141;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float half_xor(float x) { return __shfl_xor(x, 32, 64); }
 
-// Recursive halving: N values per lane, exchanged over xor masks 16, 8, ...
-// Each step keeps the half selected by the lane's mask bit and adds the
-// partner's copy of it, so after k steps a lane holds N / 2^k values summed
-// over 2^k lanes.
-template <int N, int MASK>
-__device__ __forceinline__ void halve(float* x, int j) {
-  const bool hi = (j & MASK) != 0;
+// Recursive halving: N values per lane; each step keeps the half selected by
+// a lane bit and adds the partner lane's copy of that half, so after k steps
+// a lane holds N / 2^k values summed over 2^k lanes.  The partner of a step
+// must differ from the lane in that step's bit only among the bits used so
+// far; the kept value index is the sequence of the lane's bits 4, 3, 2, 1, 0.
+template <int N>
+__device__ __forceinline__ void halve16(float* x) {
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) {
-    const float send = hi ? x[i] : x[i + N / 2];
-    const float keep = hi ? x[i + N / 2] : x[i];
-    x[i] = keep + swz_xor<MASK>(send);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[i]),
+                                                    __float_as_uint(x[i + N / 2]), false, false);
+    x[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+template <int N, int CTRL>
+__device__ __forceinline__ void halve_dpp(float* x, bool hi) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float lo_sum = x[i] + dpp<CTRL>(x[i]);
+    const float hi_sum = x[i + N / 2] + dpp<CTRL>(x[i + N / 2]);
+    x[i] = hi ? hi_sum : lo_sum;
   }
 }
 
@@ -228,34 +247,42 @@ __device__ __forceinline__ void halve(float* x, int j) {
 template <int G>
 __device__ __forceinline__ void reduce_scores(float* x, int j) {
   constexpr int NV = 8 * G;
-  halve<NV, 16>(x, j);
-  halve<NV / 2, 8>(x, j);
-  halve<NV / 4, 4>(x, j);
+  halve16<NV>(x);
+  halve_dpp<NV / 2, kDppRowRor8>(x, (j & 8) != 0);
+  halve_dpp<NV / 4, kDppRowHalfMirror>(x, (j & 4) != 0);
   if constexpr (NV / 8 >= 2) {
-    halve<NV / 8, 2>(x, j);
+    halve_dpp<NV / 8, kDppQuadXor2>(x, (j & 2) != 0);
   } else {
-    x[0] += swz_xor<2>(x[0]);
+    x[0] += dpp<kDppQuadXor2>(x[0]);
   }
   if constexpr (NV / 16 >= 2) {
-    halve<NV / 16, 1>(x, j);
+    halve_dpp<NV / 16, kDppQuadXor1>(x, (j & 1) != 0);
   } else {
-    x[0] += swz_xor<1>(x[0]);
+    x[0] += dpp<kDppQuadXor1>(x[0]);
   }
 }
 
 // Max / sum over the lanes that hold the same head: the token bits of the
 // lane index are bits 2..4 plus the half (bit 5).
 __device__ __forceinline__ float token_max(float v) {
-  v = fmaxf(v, swz_xor<4>(v));
-  v = fmaxf(v, swz_xor<8>(v));
-  v = fmaxf(v, swz_xor<16>(v));
-  return fmaxf(v, half_xor(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 __device__ __forceinline__ float token_sum(float v) {
-  v += swz_xor<4>(v);
-  v += swz_xor<8>(v);
-  v += swz_xor<16>(v);
-  return v + half_xor(v);
+  v += dpp<kDppRowRor8>(v);
+  v += dpp<kDppRowRor4>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
 __device__ __forceinline__ float exp2_ratio(float a, float b) {
@@ -734,6 +761,17 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
 
   __shared__ __align__(16) float s_p[2][NV];
   __shared__ __align__(16) float s_head[3][G];
+  // Results staged until the wavefront's last page.  On this architecture a
+  // store counts in the same in-order counter as the loads, so a store
+  // issued between prefetches would make the next page's wait also wait for
+  // the store to complete; staging keeps every global store after the last
+  // load.  A full stage is flushed early (many short units per wavefront).
+  constexpr int kStage = 4;
+  __shared__ __align__(16) float4 s_res_o[kStage][G][32];
+  __shared__ float s_res_ml[kStage][G][2];
+  __shared__ long long s_res_dst[kStage];  // >= 0: first output row; < 0: -1 - partial slot
+  __shared__ int2 s_seg[kStage];
+  __shared__ int s_seg_unit[kStage];
 
   const int lane = threadIdx.x;
   const int parity = lane >> 5;
@@ -944,6 +982,39 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     }
   };
 
+  int nres = 0;
+  int nseg = 0;
+  auto flush = [&]() {
+    for (int r = 0; r < nres; ++r) {
+      const long long dst = s_res_dst[r];
+      if (parity == 0) {
+        if (dst >= 0) {
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            reinterpret_cast<float4*>(a.out + (static_cast<std::size_t>(dst) + h) * D)[j] =
+                s_res_o[r][h][j];
+          }
+        } else {
+          const std::size_t slot = static_cast<std::size_t>(-1 - dst);
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            reinterpret_cast<float4*>(a.part_o + (slot * G + h) * D)[j] = s_res_o[r][h][j];
+          }
+          if (j < G) {
+            a.part_ml[(slot * G + j) * 2] = s_res_ml[r][j][0];
+            a.part_ml[(slot * G + j) * 2 + 1] = s_res_ml[r][j][1];
+          }
+        }
+      }
+    }
+    if (lane == 0) {
+      for (int r = 0; r < nseg; ++r) reinterpret_cast<int2*>(a.segments)[s_seg_unit[r]] = s_seg[r];
+    }
+    nres = 0;
+    nseg = 0;
+    __syncthreads();
+  };
+
   // Publishes the unit's result: the output itself when this wavefront saw
   // the whole unit, else a partial (m, l, o) at slot unit + wave.
   auto finalize = [&](const PageDesc& d) {
@@ -960,38 +1031,38 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
         s_head[2][vi] = unit_bad ? NAN : l[r];
       }
     }
+    if (nres == kStage) flush();
     __syncthreads();
     const std::size_t unit = static_cast<std::size_t>(d.kvh) * a.batch + d.b;
     const bool complete = d.p == d.np - 1 && d.g - d.p >= g0;
     if (parity == 0) {
-      if (complete) {
-        const std::size_t qrow0 = static_cast<std::size_t>(d.b) * a.q_heads + d.kvh * G;
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
+      for (int h = 0; h < G; ++h) {
+        float4 o = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        if (complete) {
           const float mh = s_head[1][h];
           const float lh = s_head[2][h];
-          float4 o;
           if (mh == -INFINITY) {
             o = make_float4(NAN, NAN, NAN, NAN);
           } else {
             const float inv = 1.0f / lh;
-            o = make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+            o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
           }
-          reinterpret_cast<float4*>(a.out + (qrow0 + h) * D)[j] = o;
         }
-      } else {
-        const std::size_t slot = unit + wave;
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          reinterpret_cast<float4*>(a.part_o + (slot * G + h) * D)[j] =
-              make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-        }
-        if (j < G) {
-          a.part_ml[(slot * G + j) * 2] = s_head[1][j];
-          a.part_ml[(slot * G + j) * 2 + 1] = s_head[2][j];
-        }
+        s_res_o[nres][h][j] = o;
+      }
+      if (j < G) {
+        s_res_ml[nres][j][0] = s_head[1][j];
+        s_res_ml[nres][j][1] = s_head[2][j];
       }
     }
+    if (lane == 0) {
+      s_res_dst[nres] = complete
+                            ? static_cast<long long>(static_cast<std::size_t>(d.b) * a.q_heads +
+                                                     d.kvh * G)
+                            : -1 - static_cast<long long>(unit + wave);
+    }
+    ++nres;
     __syncthreads();
     reset();
   };
@@ -1007,12 +1078,16 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
 #pragma unroll
         for (int h = 0; h < G; ++h) qc[h] = qn[h];
       }
-      if (d.p == 0 && lane == 0) {
+      if (d.p == 0) {
         // This wavefront holds the unit's first page: record which
         // wavefronts hold its partials for the merge.
-        const long long last_wave = (d.g + d.np - 1) / C;
-        reinterpret_cast<int2*>(a.segments)[static_cast<std::size_t>(d.kvh) * a.batch + d.b] =
-            make_int2(wave, static_cast<int>(last_wave - wave + 1));
+        if (nseg == kStage) flush();
+        if (lane == 0) {
+          const long long last_wave = (d.g + d.np - 1) / C;
+          s_seg[nseg] = make_int2(wave, static_cast<int>(last_wave - wave + 1));
+          s_seg_unit[nseg] = d.kvh * a.batch + d.b;
+        }
+        ++nseg;
       }
     }
     process(k, v, qc, valid);
@@ -1036,6 +1111,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     db = next_desc();
     load_page(db, kb, vb, qb, badb);
   }
+  flush();
 }
 
 // Combines the partials of units that span several stream wavefronts.  One
