@@ -485,6 +485,13 @@ class DecodeBatch:
                                                         _ptr(tail_key), _ptr(tail_value),
                                                         _ptr(output), _stream(stream)))
 
+    def set_timing_event(self, event):
+        """Record `event` (a torch.cuda.Event or None) between the main decode
+        kernel and the merge kernel of every attention_layer()."""
+        if event is not None:
+            event = ctypes.c_void_p(event.cuda_event if hasattr(event, "cuda_event") else event)
+        check(_lib().helix_decode_batch_set_timing_event(self._h, event))
+
     def device_state(self):
         t, l, s = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
         mb, ps = ctypes.c_size_t(), ctypes.c_size_t()

@@ -966,6 +966,13 @@ int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tabl
   });
 }
 
+int helix_decode_batch_set_timing_event(helix_decode_batch* b, void* event) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->set_between_event(static_cast<hipEvent_t>(event));
+  });
+}
+
 void helix_decode_batch_destroy(helix_decode_batch* b) { delete b; }
 
 }  // extern "C"

@@ -211,6 +211,14 @@ constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
 constexpr int kDppRowHalfMirror = 0x141;
 
+// Raw buffer descriptor word 3 for plain dword access on CDNA.
+constexpr int kBufferWord3 = 0x00020000;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 as_float4(u32x4 v) {
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                     __uint_as_float(v[3]));
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
@@ -858,9 +866,13 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   };
 
   // Loads of one page (or the tail row, every lane reading its 4 dims for
-  // all 8 slots).  The first page of a unit in this wavefront also brings the
-  // unit's query rows, issued ahead of the page so that waiting for the page
-  // covers them.
+  // all 8 slots) through per-page buffer descriptors: the lane offset is a
+  // constant register and the slot offset a scalar, so no per-load address
+  // arithmetic is needed.  The first page of a unit in this wavefront also
+  // brings the unit's query rows, issued ahead of the page so that waiting
+  // for the page covers them.
+  const int lane_off = lane * 16;
+  const int row_off = j * 16;
   auto load_page = [&](const PageDesc& d, float4 (&k)[8], float4 (&v)[8], float4 (&q)[G],
                        bool& bad) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
@@ -886,19 +898,22 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       vb = a.value_pool + off;
     }
     if (p == 0 || d.g == g0) {
-      const float4* qp = reinterpret_cast<const float4*>(
-          a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D);
+      const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D),
+          0, G * D * 4, kBufferWord3);
 #pragma unroll
-      for (int h = 0; h < G; ++h) q[h] = qp[h * (D / 4) + j];
+      for (int h = 0; h < G; ++h) q[h] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(qr, row_off, h * D * 4, 0));
     }
-    const int stride = tail ? 0 : 64;
-    const int li = tail ? j : lane;
-    const float4* kp = reinterpret_cast<const float4*>(kb);
-    const float4* vp = reinterpret_cast<const float4*>(vb);
+    const int voff = tail ? row_off : lane_off;
+    const int step = tail ? 0 : 1024;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb), 0, P * D * 4, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vb), 0, P * D * 4, kBufferWord3);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) k[i] = kp[i * stride + li];
+    for (int i = 0; i < 8; ++i) k[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(kr, voff, i * step, 0));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = vp[i * stride + li];
+    for (int i = 0; i < 8; ++i) v[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(vr, voff, i * step, 0));
   };
 
   float acc[G][4];
@@ -1574,6 +1589,10 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (a.between_event != nullptr) {
+      e = hipEventRecord(a.between_event, stream);
+      if (e != hipSuccess) return e;
+    }
     const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
     switch (group) {
       case 1: decode_stream_merge_kernel<1><<<mgrid, 1 * 32, 0, stream>>>(k); break;
@@ -1599,6 +1618,7 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
+  if (e == hipSuccess && a.between_event != nullptr) e = hipEventRecord(a.between_event, stream);
   if (e != hipSuccess || max_splits == 1) return e;
   const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
   const std::size_t lds = (group * max_splits + group) * sizeof(float);

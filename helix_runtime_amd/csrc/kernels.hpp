@@ -90,6 +90,9 @@ struct DecodeArgs {
   std::size_t physical_blocks;
   std::size_t pages_per_split;
   std::size_t items;
+  // Optional: recorded on the stream between the main kernel and the merge
+  // (measurement of the dominant kernel alone).
+  hipEvent_t between_event = nullptr;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;

@@ -550,6 +550,7 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.physical_blocks = c.physical_blocks;
   a.pages_per_split = pages_per_split_;
   a.items = items_;
+  a.between_event = between_event_;
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
 }

@@ -175,6 +175,9 @@ public:
   [[nodiscard]] std::size_t pages_per_split() const noexcept { return pages_per_split_; }
   [[nodiscard]] std::size_t batch() const noexcept { return sequences_.size(); }
   [[nodiscard]] std::size_t step_tokens() const noexcept { return step_tokens_; }
+  // Measurement hook: when set, attention_layer() records this event between
+  // the main decode kernel and the merge kernel.
+  void set_between_event(hipEvent_t e) noexcept { between_event_ = e; }
 
 private:
   std::shared_ptr<CacheState> state_;
@@ -194,6 +197,7 @@ private:
   std::size_t step_capacity_ = 0;  // tokens per sequence the step buffers hold
   std::size_t step_tokens_ = 0;    // tokens of the prepared step
   bool prepared_ = false;
+  hipEvent_t between_event_ = nullptr;
 
   void reserve_step(std::size_t tokens);
 };

@@ -313,6 +313,11 @@ int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const 
 int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tables,
                               const int32_t** lengths, const int64_t** slots,
                               size_t* max_blocks, size_t* pages_per_split);
+/* Measurement hook (no reference counterpart): when event (a hipEvent_t) is
+ * non-NULL, every attention_layer() records it on its stream between the
+ * main decode kernel and the merge kernel, so the dominant kernel can be
+ * timed alone.  NULL turns it off. */
+int helix_decode_batch_set_timing_event(helix_decode_batch* b, void* event);
 void helix_decode_batch_destroy(helix_decode_batch* b);
 
 /* ------------------------------------------------------- measurement ---- */
