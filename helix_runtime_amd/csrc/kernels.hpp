@@ -151,9 +151,14 @@ struct PrefillArgs {
   const float* chunk_value;
   float* out;
   std::size_t batch, q_heads, kv_heads, tokens, max_blocks, physical_blocks;
+  // Optional launch order of the batch * kv_heads * ceil(tokens / positions
+  // per block) work items, packed (b * kv_heads + kvh) * blocks + block.
+  const std::uint32_t* order = nullptr;
 };
 
 bool prefill_group_supported(std::size_t group);
+// Chunk positions one prefill work item covers for a query group size.
+std::size_t prefill_position_block(std::size_t group);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace helix::hip

@@ -425,15 +425,24 @@ const std::int64_t* DecodeBatch::slots() const {
 }
 
 // Step buffers for `tokens` slots per sequence: lengths [B] int32, slots
-// [B, tokens] int64 and up to B * (tokens / block_tokens + 1) table updates
-// of 3 words, in one device buffer and two pinned staging copies.
+// [B, tokens] int64, up to B * (tokens / block_tokens + 1) table updates of
+// 3 words, and for chunks the prefill work-item order, in one device buffer
+// and two pinned staging copies.
+std::size_t DecodeBatch::order_offset(std::size_t tokens) const {
+  const std::size_t B = batch();
+  const std::size_t max_updates = B * (tokens / state_->manager.config().block_tokens + 1);
+  return align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
+         3 * max_updates * sizeof(std::uint32_t);
+}
+
+std::size_t DecodeBatch::prefill_items(std::size_t tokens) const {
+  const std::size_t pw = hip::prefill_position_block(q_heads_ / state_->manager.config().kv_heads);
+  return batch() * state_->manager.config().kv_heads * ((tokens + pw - 1) / pw);
+}
+
 void DecodeBatch::reserve_step(std::size_t tokens) {
   if (tokens <= step_capacity_) return;
-  const PagedConfig& c = state_->manager.config();
-  const std::size_t B = batch();
-  const std::size_t max_updates = B * (tokens / c.block_tokens + 1);
-  const std::size_t bytes = align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
-                            3 * max_updates * sizeof(std::uint32_t);
+  const std::size_t bytes = order_offset(tokens) + prefill_items(tokens) * sizeof(std::uint32_t);
   for (hipEvent_t e : uploaded_) hip_check(hipEventSynchronize(e), "decode batch staging wait");
   DeviceGuard guard(state_->device);
   // The device buffer may still be read by queued kernels of earlier steps.
@@ -495,6 +504,32 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   DeviceGuard guard(s.device);
   const std::size_t used = align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
                            3 * n_updates * sizeof(std::uint32_t);
+  if (tokens > 1) {
+    // Longest-first order of the prefill work items: a (sequence, position
+    // block) sees its history plus the chunk rows up to the block's end.
+    const std::size_t H = c.kv_heads;
+    const std::size_t pw = hip::prefill_position_block(q_heads_ / H);
+    const std::size_t nb = (tokens + pw - 1) / pw;
+    std::vector<std::pair<std::size_t, std::uint32_t>> items;
+    items.reserve(B * H * nb);
+    for (std::size_t i = 0; i < B; ++i) {
+      for (std::size_t h = 0; h < H; ++h) {
+        for (std::size_t pb = 0; pb < nb; ++pb) {
+          const std::size_t work = static_cast<std::size_t>(lengths[i]) +
+                                   std::min(tokens, (pb + 1) * pw);
+          items.emplace_back(work, static_cast<std::uint32_t>((i * H + h) * nb + pb));
+        }
+      }
+    }
+    std::stable_sort(items.begin(), items.end(),
+                     [](const auto& x, const auto& y) { return x.first > y.first; });
+    auto* order = reinterpret_cast<std::uint32_t*>(host + order_offset(tokens));
+    for (std::size_t n = 0; n < items.size(); ++n) order[n] = items[n].second;
+    hip_check(hipMemcpyAsync(static_cast<unsigned char*>(step_.data()) + order_offset(tokens),
+                             order, items.size() * sizeof(std::uint32_t), hipMemcpyHostToDevice,
+                             stream),
+              "decode batch order upload");
+  }
   hip_check(hipMemcpyAsync(step_.data(), host, used, hipMemcpyHostToDevice, stream),
             "decode batch step upload");
   hip_check(hipEventRecord(uploaded_[which], stream), "decode batch event");
@@ -577,6 +612,10 @@ void DecodeBatch::prefill_layer(std::size_t layer, const float* query, const flo
   a.tokens = step_tokens_;
   a.max_blocks = max_blocks_;
   a.physical_blocks = c.physical_blocks;
+  if (step_tokens_ > 1) {
+    a.order = reinterpret_cast<const std::uint32_t*>(
+        static_cast<const unsigned char*>(step_.data()) + order_offset(step_tokens_));
+  }
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_prefill(a, stream), "decode batch prefill launch");
 }

@@ -200,6 +200,8 @@ private:
   hipEvent_t between_event_ = nullptr;
 
   void reserve_step(std::size_t tokens);
+  [[nodiscard]] std::size_t order_offset(std::size_t tokens) const;
+  [[nodiscard]] std::size_t prefill_items(std::size_t tokens) const;
 };
 
 }  // namespace helix

@@ -64,6 +64,7 @@ struct PrefillKernelArgs {
   int pos_blocks;
   std::uint32_t physical_blocks;
   float qscale;
+  const std::uint32_t* order;  // optional workgroup order (packed work items)
 };
 
 __device__ __forceinline__ float exp2_ratio(float a, float b) {
@@ -89,10 +90,20 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   const int wave = tid >> 6;
   const int col = lane & 15;  // MFMA column: query row of the tile / dim group
   const int grp = lane >> 4;  // MFMA k group
-  // Later position blocks see more keys: dispatch them first.
-  const int pb = a.pos_blocks - 1 - static_cast<int>(blockIdx.x);
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
+  // Work item = (sequence, kv head, position block), packed as
+  // (b * kv_heads + kvh) * pos_blocks + pb.  The caller may pass a
+  // longest-first order; by default later position blocks (more keys) of a
+  // (sequence, kv head) go first.
+  std::uint32_t item = blockIdx.x;
+  if (a.order != nullptr) {
+    item = a.order[blockIdx.x];
+  } else {
+    const std::uint32_t x = item % a.pos_blocks;
+    item = item - x + (a.pos_blocks - 1 - x);
+  }
+  const int pb = static_cast<int>(item % a.pos_blocks);
+  const int kvh = static_cast<int>((item / a.pos_blocks) % a.kv_heads);
+  const int b = static_cast<int>(item / a.pos_blocks / a.kv_heads);
   const int T = a.tokens;
   const int pos0 = pb * PW;
 
@@ -232,10 +243,13 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
       sum += __shfl_xor(sum, 32, 64);
       l[t] = l[t] * alpha + sum;
       m[t] = mn;
+      // Rows whose maximum did not move keep their accumulators as they are.
+      if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.0f)) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
+          for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
+      }
     }
 
     if (!exact_pv) {
@@ -318,6 +332,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
 
 }  // namespace
 
+std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
+
 bool prefill_group_supported(std::size_t group) {
   return group == 1 || group == 2 || group == 4 || group == 8;
 }
@@ -342,8 +358,8 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.pos_blocks = static_cast<int>((a.tokens + pw - 1) / pw);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(D));
-  const dim3 grid(static_cast<unsigned>(k.pos_blocks), static_cast<unsigned>(a.kv_heads),
-                  static_cast<unsigned>(a.batch));
+  k.order = a.order;
+  const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   switch (group) {
     case 1: prefill_kernel<1><<<grid, 256, 0, stream>>>(k); break;
     case 2: prefill_kernel<2><<<grid, 256, 0, stream>>>(k); break;
