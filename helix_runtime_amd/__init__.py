@@ -485,6 +485,12 @@ class DecodeBatch:
                                                         _ptr(tail_key), _ptr(tail_value),
                                                         _ptr(output), _stream(stream)))
 
+    def shared_pages(self):
+        """Leading pages the prepared decode step attends once for the batch."""
+        n = ctypes.c_size_t()
+        check(_lib().helix_decode_batch_shared_pages(self._h, ctypes.byref(n)))
+        return n.value
+
     def set_timing_event(self, event):
         """Record `event` (a torch.cuda.Event or None) between the main decode
         kernel and the merge kernel of every attention_layer()."""

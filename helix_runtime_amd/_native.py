@@ -138,6 +138,7 @@ SIGNATURES = {
     "helix_decode_batch_attention_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_tables": (c_int, [vp, P(vp), P(vp), P(vp), P(c_size), P(c_size)]),
     "helix_decode_batch_set_timing_event": (c_int, [vp, vp]),
+    "helix_decode_batch_shared_pages": (c_int, [vp, P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
     "helix_probe_stream_read": (c_int, [vp, c_size, vp, ctypes.c_uint, vp]),
 }

@@ -966,6 +966,14 @@ int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tabl
   });
 }
 
+int helix_decode_batch_shared_pages(const helix_decode_batch* b, size_t* out) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    require_out(out);
+    *out = b->batch->shared_pages();
+  });
+}
+
 int helix_decode_batch_set_timing_event(helix_decode_batch* b, void* event) {
   return guarded([&] {
     check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");

@@ -319,6 +319,9 @@ struct DecodeKernelArgs {
   float qscale;
   int stream_waves;     // grid size of the stream kernel (stream mode)
   int* segments;        // [units] (first wavefront, wavefront count), stream mode
+  int first_page;       // stream mode: pages before this are covered by the cascade
+  long long prefix_slot0;  // cascade: chunk c of unit u at prefix_slot0 + c * units + u
+  int prefix_chunks;    // cascade: key chunks of the shared prefix
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -709,8 +712,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeKernelArgs a) {
 // the slots of one unit are contiguous (u + w_first .. u + w_last) and no two
 // units share a slot, since the next unit starts at or after w_last.
 // decode_stream_merge_kernel combines them.
-__device__ __forceinline__ int unit_pages(int hist) {
-  return (hist < 0 ? 0 : (hist + 15) / 16) + 1;
+// Stream-mode pages of a unit: its history pages from `first` on, plus the
+// tail pseudo-page.
+__device__ __forceinline__ int unit_pages(int hist, int first) {
+  const int pages = (hist < 0 ? 0 : (hist + 15) / 16) - first;
+  return (pages < 0 ? 0 : pages) + 1;
 }
 
 // Marks a wave-uniform 64-bit value as such (scalar registers), so control
@@ -735,7 +741,7 @@ __device__ __forceinline__ long long stream_pages_before(const DecodeKernelArgs&
   long long sum = 0;
   for (int c0 = 0; c0 < upto; c0 += 64) {
     const int bb = c0 + lane;
-    const int w = bb < upto ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks)) : 0;
+    const int w = bb < upto ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks), a.first_page) : 0;
     sum += wave_sum(w);
   }
   return sum;
@@ -789,7 +795,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   // One pass over the lengths when the batch fits a wavefront (lane b holds
   // sequence b), a second one only for larger batches.
   const int hist0 = lane < a.batch ? clamp_length(a.lengths[lane], a.max_blocks) : -1;
-  const int np0 = lane < a.batch ? unit_pages(hist0) : 0;
+  const int np0 = lane < a.batch ? unit_pages(hist0, a.first_page) : 0;
   long long per_head = wave_sum(np0);
   if (a.batch > 64) per_head += stream_pages_before(a, a.batch, lane) - per_head;
   per_head = uniform64(per_head);
@@ -809,7 +815,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       const int bb = c0 + lane;
       const int hist =
           c0 == 0 ? hist0 : (bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1);
-      const int np = c0 == 0 ? np0 : (bb < a.batch ? unit_pages(hist) : 0);
+      const int np = c0 == 0 ? np0 : (bb < a.batch ? unit_pages(hist, a.first_page) : 0);
       long long incl = np;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -859,7 +865,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       if (cur.g < g1) {
         cur.b = __builtin_amdgcn_readfirstlane(cur.b);
         cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
-        cur.np = unit_pages(cur.hist);
+        cur.np = unit_pages(cur.hist, a.first_page);
       }
     }
     return d;
@@ -888,7 +894,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
       vb = a.tail_value + row;
     } else {
       std::uint32_t phys = __builtin_amdgcn_readfirstlane(
-          a.tables[static_cast<std::size_t>(b) * a.max_blocks + p]);
+          a.tables[static_cast<std::size_t>(b) * a.max_blocks + p + a.first_page]);
       if (phys >= a.physical_blocks) {
         bad = true;
         phys = 0;
@@ -1049,7 +1055,8 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     if (nres == kStage) flush();
     __syncthreads();
     const std::size_t unit = static_cast<std::size_t>(d.kvh) * a.batch + d.b;
-    const bool complete = d.p == d.np - 1 && d.g - d.p >= g0;
+    // With a cascade prefix every unit also has a prefix partial to merge.
+    const bool complete = a.first_page == 0 && d.p == d.np - 1 && d.g - d.p >= g0;
     if (parity == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
@@ -1087,7 +1094,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
                   bool bad) {
     int valid = 0;
     if (!d.skip) {
-      valid = d.p == d.np - 1 ? 1 : min(P, d.hist - d.p * P);
+      valid = d.p == d.np - 1 ? 1 : min(P, d.hist - (d.p + a.first_page) * P);
       unit_bad = unit_bad || bad;
       if (d.p == 0 || d.g == g0) {
 #pragma unroll
@@ -1139,7 +1146,8 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeKernelAr
   constexpr int D = 128;
   const int unit = blockIdx.x;
   const int2 seg = reinterpret_cast<const int2*>(a.segments)[unit];
-  if (seg.y <= 1) return;
+  const bool cascade = a.first_page > 0;
+  if (seg.y <= 1 && !cascade) return;
   const int kvh = unit / a.batch;
   const int b = unit % a.batch;
   const int tid = threadIdx.x;
@@ -1151,13 +1159,20 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeKernelAr
   float mx = -INFINITY;
   float den = 0.0f;
   float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < seg.y; s0 += kChunk) {
+  // Partials: the unit's stream segments, then (cascade) its prefix chunks.
+  const int nparts = seg.y + (cascade ? a.prefix_chunks : 0);
+  const long long units = static_cast<long long>(a.batch) * a.kv_heads;
+  for (int s0 = 0; s0 < nparts; s0 += kChunk) {
     float ms[kChunk], ls[kChunk];
     float4 os[kChunk];
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
-      const bool in = s0 + i < seg.y;
-      const std::size_t slot = slot0 + (in ? s0 + i : 0);
+      const bool in = s0 + i < nparts;
+      const std::size_t slot =
+          !in ? slot0
+              : (s0 + i < seg.y
+                     ? slot0 + s0 + i
+                     : static_cast<std::size_t>(a.prefix_slot0 + (s0 + i - seg.y) * units + unit));
       ms[i] = in ? a.part_ml[(slot * G + h) * 2] : -INFINITY;
       ls[i] = in ? a.part_ml[(slot * G + h) * 2 + 1] : 0.0f;
       os[i] = in ? reinterpret_cast<const float4*>(a.part_o + (slot * G + h) * D)[d4]
@@ -1174,7 +1189,7 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeKernelAr
     num.w *= sc;
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
-      const float w = s0 + i < seg.y ? exp2_ratio(ms[i], cm) : 0.0f;
+      const float w = s0 + i < nparts ? exp2_ratio(ms[i], cm) : 0.0f;
       den += w * ls[i];
       num.x += w * os[i].x;
       num.y += w * os[i].y;
@@ -1463,7 +1478,10 @@ WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t k
 // Stream mode: one partial slot per (sequence, kv head) unit plus one per
 // wavefront (slot = unit + wavefront).
 WorkspaceLayout stream_layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads) {
-  WorkspaceLayout l = layout_for(batch * kv_heads + kMaxStreamWaves, q_heads / kv_heads, 1, 1);
+  // Slots: [0, units + kMaxStreamWaves) stream partials (unit + wavefront),
+  // then kMaxCascadeChunks cascade prefix slots per unit.
+  WorkspaceLayout l = layout_for((1 + kMaxCascadeChunks) * batch * kv_heads + kMaxStreamWaves,
+                                 q_heads / kv_heads, 1, 1);
   l.segments = l.total;
   l.total += align256(batch * kv_heads * 2 * sizeof(int));
   return l;
@@ -1566,6 +1584,27 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
     k.segments = reinterpret_cast<int*>(ws + lay.segments);
+    k.first_page = static_cast<int>(a.shared_pages);
+    k.prefix_slot0 = static_cast<long long>(a.batch * a.kv_heads + kMaxStreamWaves);
+    if (a.shared_pages > 0) {
+      const std::size_t cp = cascade_chunk_pages(a.shared_pages, a.batch, group, a.kv_heads);
+      k.prefix_chunks = static_cast<int>((a.shared_pages + cp - 1) / cp);
+      CascadePrefixArgs c{};
+      c.query = a.query;
+      c.key_pool = a.key_pool;
+      c.value_pool = a.value_pool;
+      c.table = a.tables;
+      c.part_o = k.part_o;
+      c.part_ml = k.part_ml;
+      c.batch = a.batch;
+      c.q_heads = a.q_heads;
+      c.kv_heads = a.kv_heads;
+      c.shared_pages = a.shared_pages;
+      c.physical_blocks = a.physical_blocks;
+      c.prefix_slot0 = static_cast<std::size_t>(k.prefix_slot0);
+      const hipError_t e = launch_cascade_prefix(c, stream);
+      if (e != hipSuccess) return e;
+    }
     k.stream_waves = static_cast<int>(waves);
     const dim3 grid(static_cast<unsigned>(waves));
     switch (group) {

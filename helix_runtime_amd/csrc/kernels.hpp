@@ -93,6 +93,11 @@ struct DecodeArgs {
   // Optional: recorded on the stream between the main kernel and the merge
   // (measurement of the dominant kernel alone).
   hipEvent_t between_event = nullptr;
+  // Cascade (stream mode only): the first shared_pages pages of every
+  // sequence are the same physical pages (row 0 of tables); they are attended
+  // once for all sequences on the matrix cores and the stream kernel covers
+  // the rest.  0: off.
+  std::size_t shared_pages = 0;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;
@@ -155,6 +160,26 @@ struct PrefillArgs {
   // per block) work items, packed (b * kv_heads + kvh) * blocks + block.
   const std::uint32_t* order = nullptr;
 };
+
+// Shared-prefix attention for a decode batch (cascade): every query row of
+// every sequence against the first shared_pages pages of `table`, leaving a
+// partial (m, l, o) per (sequence, kv head) unit at prefix_slot0 + kvh *
+// batch + b of the decode workspace partials.
+struct CascadePrefixArgs {
+  const float* query;
+  const float* key_pool;
+  const float* value_pool;
+  const std::uint32_t* table;
+  float* part_o;
+  float* part_ml;
+  std::size_t batch, q_heads, kv_heads, shared_pages, physical_blocks, prefix_slot0;
+};
+hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream);
+// The shared prefix is split into key chunks (each leaving its own partial
+// per unit, at slot prefix_slot0 + chunk * units + unit).
+constexpr std::size_t kMaxCascadeChunks = 16;
+std::size_t cascade_chunk_pages(std::size_t shared_pages, std::size_t batch, std::size_t group,
+                                std::size_t kv_heads);
 
 bool prefill_group_supported(std::size_t group);
 // Chunk positions one prefill work item covers for a query group size.

@@ -539,6 +539,22 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   hip_check(hip::launch_table_updates(static_cast<std::uint32_t*>(tables_.data()), max_blocks_,
                                       dev_updates, n_updates, stream),
             "decode batch table update");
+  // Cascade for decode steps: the longest run of leading pages that every
+  // sequence shares (same physical IDs, all full before the step) is
+  // attended once for the whole batch.
+  shared_pages_ = 0;
+  if (tokens == 1 && pages_per_split_ == 0 && B >= kMinCascadeBatch) {
+    const auto& first = s.manager.blocks(sequences_[0]);
+    std::size_t shared = first.size();
+    for (std::size_t i = 0; i < B && shared > 0; ++i) {
+      const auto& blocks = s.manager.blocks(sequences_[i]);
+      shared = std::min(shared, static_cast<std::size_t>(host_lengths_[i]) / c.block_tokens);
+      std::size_t k = 0;
+      while (k < shared && blocks[k] == first[k]) ++k;
+      shared = k;
+    }
+    if (shared >= kMinCascadePages) shared_pages_ = shared;
+  }
   step_tokens_ = tokens;
   prepared_ = true;
 }
@@ -586,6 +602,7 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.pages_per_split = pages_per_split_;
   a.items = items_;
   a.between_event = between_event_;
+  a.shared_pages = shared_pages_;
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
 }

@@ -175,6 +175,7 @@ public:
   [[nodiscard]] std::size_t pages_per_split() const noexcept { return pages_per_split_; }
   [[nodiscard]] std::size_t batch() const noexcept { return sequences_.size(); }
   [[nodiscard]] std::size_t step_tokens() const noexcept { return step_tokens_; }
+  [[nodiscard]] std::size_t shared_pages() const noexcept { return shared_pages_; }
   // Measurement hook: when set, attention_layer() records this event between
   // the main decode kernel and the merge kernel.
   void set_between_event(hipEvent_t e) noexcept { between_event_ = e; }
@@ -198,6 +199,11 @@ private:
   std::size_t step_tokens_ = 0;    // tokens of the prepared step
   bool prepared_ = false;
   hipEvent_t between_event_ = nullptr;
+  std::size_t shared_pages_ = 0;  // cascade prefix of the prepared step (0: off)
+  // A decode step uses the cascade when at least this many sequences share
+  // at least this many leading pages.
+  static constexpr std::size_t kMinCascadeBatch = 4;
+  static constexpr std::size_t kMinCascadePages = 4;
 
   void reserve_step(std::size_t tokens);
   [[nodiscard]] std::size_t order_offset(std::size_t tokens) const;

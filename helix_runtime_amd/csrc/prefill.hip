@@ -65,6 +65,16 @@ struct PrefillKernelArgs {
   std::uint32_t physical_blocks;
   float qscale;
   const std::uint32_t* order;  // optional workgroup order (packed work items)
+  // Cascade mode (shared-prefix decode): rows are (sequence, head) pairs of
+  // one kv head, keys are the first cascade_keys tokens of table row 0, and
+  // each row leaves a partial (m, l, o) at slot prefix_slot0 + kvh * batch +
+  // sequence.
+  int batch;
+  int cascade_keys;
+  int cascade_chunk_pages;  // key pages per work item (the prefix is split)
+  float* part_o;
+  float* part_ml;
+  long long prefix_slot0;
 };
 
 __device__ __forceinline__ float exp2_ratio(float a, float b) {
@@ -79,7 +89,7 @@ __device__ __forceinline__ bool finite4(const float4& v) {
   return isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
 }
 
-template <int G>
+template <int G, bool CASCADE>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   constexpr int PW = kRows / G;  // chunk positions per workgroup
   __shared__ __align__(16) float s_k[2][kKeys * kKStride];
@@ -103,31 +113,47 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   }
   const int pb = static_cast<int>(item % a.pos_blocks);
   const int kvh = static_cast<int>((item / a.pos_blocks) % a.kv_heads);
-  const int b = static_cast<int>(item / a.pos_blocks / a.kv_heads);
+  // Prefill: the sequence.  Cascade: the key chunk of the shared prefix.
+  const int b = CASCADE ? 0 : static_cast<int>(item / a.pos_blocks / a.kv_heads);
+  const int chunk = CASCADE ? static_cast<int>(item / a.pos_blocks / a.kv_heads) : 0;
   const int T = a.tokens;
   const int pos0 = pb * PW;
 
-  int hist = a.lengths[b];
+  int hist = CASCADE ? a.cascade_keys : a.lengths[b];
   bool bad = hist < 0 || hist > a.max_blocks * P;
   if (bad) hist = 0;
-  const int key_end = hist + min(T, pos0 + PW);
+  const int key_begin = CASCADE ? chunk * a.cascade_chunk_pages * P : 0;
+  const int key_end =
+      CASCADE ? min(hist, (chunk + 1) * a.cascade_chunk_pages * P) : hist + min(T, pos0 + PW);
   const std::uint32_t* table = a.tables + static_cast<std::size_t>(b) * a.max_blocks;
   const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
 
   // Rows of this lane: tile t holds workgroup row wave * 32 + t * 16 + col.
+  // Prefill: G heads x PW chunk positions of sequence b.  Cascade: row R of
+  // the kv head is (sequence R / G, head R % G), one query token each.
   int qpos[2];
+  bool qvalid[2];
   std::size_t qrow[2];
   float4 q[2][8];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int r = wave * 32 + t * 16 + col;
-    const int head = kvh * G + r / PW;
-    qpos[t] = pos0 + r % PW;
-    qrow[t] = ((static_cast<std::size_t>(b) * a.q_heads + head) * T + qpos[t]) * D;
+    if constexpr (CASCADE) {
+      const int row = pb * kRows + r;
+      const int seq = row / G;
+      qvalid[t] = seq < a.batch;
+      qpos[t] = 0x3fffffff;  // no causal limit: every prefix key is visible
+      qrow[t] = (static_cast<std::size_t>(qvalid[t] ? seq : 0) * a.q_heads + kvh * G + row % G) * D;
+    } else {
+      const int head = kvh * G + r / PW;
+      qpos[t] = pos0 + r % PW;
+      qvalid[t] = qpos[t] < T;
+      qrow[t] = ((static_cast<std::size_t>(b) * a.q_heads + head) * T + qpos[t]) * D;
+    }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (qpos[t] < T) v = *reinterpret_cast<const float4*>(a.query + qrow[t] + 16 * c + 4 * grp);
+      if (qvalid[t]) v = *reinterpret_cast<const float4*>(a.query + qrow[t] + 16 * c + 4 * grp);
       q[t][c] = make_float4(v.x * a.qscale, v.y * a.qscale, v.z * a.qscale, v.w * a.qscale);
     }
   }
@@ -173,7 +199,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
       stk[r] = kp ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
       stv[r] = vp ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
       // A chunk row that some query row of this workgroup masks.
-      if (key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) st_nonfinite = true;
+      if (!CASCADE && key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) {
+        st_nonfinite = true;
+      }
     }
   };
   auto stage_store = [&](int buf) {
@@ -186,13 +214,14 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   };
 
   const int nblocks = (key_end + kKeys - 1) / kKeys;
+  const int nfirst = key_begin / kKeys;
   int exact_pv = 0;
-  if (nblocks > 0) {
-    stage_load(0);
-    stage_store(0);
+  if (nblocks > nfirst) {
+    stage_load(nfirst);
+    stage_store(nfirst & 1);
     exact_pv = __syncthreads_or(st_nonfinite);
   }
-  for (int n = 0; n < nblocks; ++n) {
+  for (int n = nfirst; n < nblocks; ++n) {
     const int buf = n & 1;
     if (n + 1 < nblocks) stage_load(n + 1);
     const float* K = s_k[buf];
@@ -312,6 +341,32 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   }
 
   const int any_bad = __syncthreads_or(bad);
+  if constexpr (CASCADE) {
+    // Partial (m, l, o) per row; lanes of the four k groups hold the row's
+    // 128 dims, the (m, l) pair is written by group 0.
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (!qvalid[t]) continue;
+      const int row = pb * kRows + wave * 32 + t * 16 + col;
+      const long long units = static_cast<long long>(a.kv_heads) * a.batch;
+      const std::size_t slot = static_cast<std::size_t>(
+          a.prefix_slot0 + chunk * units + static_cast<long long>(kvh) * a.batch + row / G);
+      const std::size_t base = (slot * G + row % G);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          *reinterpret_cast<float4*>(a.part_o + base * D + 64 * h + 16 * grp + 4 * ii) =
+              make_float4(o[t][h][0][ii], o[t][h][1][ii], o[t][h][2][ii], o[t][h][3][ii]);
+        }
+      }
+      if (grp == 0) {
+        a.part_ml[base * 2] = m[t];
+        a.part_ml[base * 2 + 1] = any_bad ? NAN : l[t];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     if (qpos[t] >= T) continue;
@@ -333,6 +388,19 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
 }  // namespace
 
 std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
+
+// Key pages per cascade work item: enough chunks that the launch has about
+// kCascadeTarget workgroups, at most kMaxCascadeChunks chunks.
+std::size_t cascade_chunk_pages(std::size_t shared_pages, std::size_t batch, std::size_t group,
+                                std::size_t kv_heads) {
+  constexpr std::size_t kCascadeTarget = 1024;
+  const std::size_t items = ((batch * group + kRows - 1) / kRows) * kv_heads;
+  std::size_t chunks = (kCascadeTarget + items - 1) / items;
+  if (chunks > kMaxCascadeChunks) chunks = kMaxCascadeChunks;
+  if (chunks > shared_pages) chunks = shared_pages;
+  if (chunks == 0) chunks = 1;
+  return (shared_pages + chunks - 1) / chunks;
+}
 
 bool prefill_group_supported(std::size_t group) {
   return group == 1 || group == 2 || group == 4 || group == 8;
@@ -359,12 +427,48 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(D));
   k.order = a.order;
+  k.batch = static_cast<int>(a.batch);
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   switch (group) {
-    case 1: prefill_kernel<1><<<grid, 256, 0, stream>>>(k); break;
-    case 2: prefill_kernel<2><<<grid, 256, 0, stream>>>(k); break;
-    case 4: prefill_kernel<4><<<grid, 256, 0, stream>>>(k); break;
-    case 8: prefill_kernel<8><<<grid, 256, 0, stream>>>(k); break;
+    case 1: prefill_kernel<1, false><<<grid, 256, 0, stream>>>(k); break;
+    case 2: prefill_kernel<2, false><<<grid, 256, 0, stream>>>(k); break;
+    case 4: prefill_kernel<4, false><<<grid, 256, 0, stream>>>(k); break;
+    case 8: prefill_kernel<8, false><<<grid, 256, 0, stream>>>(k); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream) {
+  if (a.batch == 0 || a.shared_pages == 0) return hipSuccess;
+  const std::size_t group = a.q_heads / a.kv_heads;
+  PrefillKernelArgs k{};
+  k.query = a.query;
+  k.key_pool = a.key_pool;
+  k.value_pool = a.value_pool;
+  k.tables = a.table;
+  k.q_heads = static_cast<int>(a.q_heads);
+  k.kv_heads = static_cast<int>(a.kv_heads);
+  k.tokens = 1;
+  k.max_blocks = static_cast<int>(a.shared_pages);
+  k.pos_blocks = static_cast<int>((a.batch * group + kRows - 1) / kRows);
+  k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
+  k.qscale = kLog2e / sqrtf(static_cast<float>(D));
+  k.batch = static_cast<int>(a.batch);
+  k.cascade_keys = static_cast<int>(a.shared_pages * P);
+  k.cascade_chunk_pages = static_cast<int>(cascade_chunk_pages(a.shared_pages, a.batch, group,
+                                                               a.kv_heads));
+  k.part_o = a.part_o;
+  k.part_ml = a.part_ml;
+  k.prefix_slot0 = static_cast<long long>(a.prefix_slot0);
+  const std::size_t chunks =
+      (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
+  const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * chunks));
+  switch (group) {
+    case 1: prefill_kernel<1, true><<<grid, 256, 0, stream>>>(k); break;
+    case 2: prefill_kernel<2, true><<<grid, 256, 0, stream>>>(k); break;
+    case 4: prefill_kernel<4, true><<<grid, 256, 0, stream>>>(k); break;
+    case 8: prefill_kernel<8, true><<<grid, 256, 0, stream>>>(k); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

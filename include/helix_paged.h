@@ -313,6 +313,10 @@ int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const 
 int helix_decode_batch_tables(const helix_decode_batch* b, const uint32_t** tables,
                               const int32_t** lengths, const int64_t** slots,
                               size_t* max_blocks, size_t* pages_per_split);
+/* Leading pages that every sequence of the prepared decode step shares and
+ * that attention_layer() attends once for the whole batch on the matrix
+ * cores (cascade; 0 when the step does not use it). */
+int helix_decode_batch_shared_pages(const helix_decode_batch* b, size_t* out);
 /* Measurement hook (no reference counterpart): when event (a hipEvent_t) is
  * non-NULL, every attention_layer() records it on its stream between the
  * main decode kernel and the merge kernel, so the dominant kernel can be

@@ -171,3 +171,60 @@ def test_prefix_sharing_decode_with_cow_forks(device):
             np.testing.assert_array_equal(host(gk), ok)
             np.testing.assert_array_equal(host(gv), ov)
     batch.close()
+
+
+@pytest.mark.parametrize("hq", [8, 32])
+def test_cascade_shared_prefix_decode(device, hq):
+    """Sequences forked from one root share its full leading pages; the decode
+    step attends them once for the batch (cascade) and the per-sequence rest
+    through the stream kernel.  Outputs match the oracle over several steps,
+    including a sequence whose history is exactly the shared prefix."""
+    L, H = 2, 4
+    rng = np.random.default_rng(77 + hq)
+    prefix, forks = 10 * P, 8
+    suffix = [0, 1, 5, 16, 17, 40, 100, 3]
+    N = 128
+    cache = hx.PagedKvCache(L, H, D, P, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    root, root_o = cache.create_sequence(), pool.create_sequence()
+    k = rng.standard_normal((L, H, prefix, D), dtype=np.float32)
+    v = rng.standard_normal((L, H, prefix, D), dtype=np.float32)
+    cache.append_layer_major(root, [dev(k[l]) for l in range(L)], [dev(v[l]) for l in range(L)])
+    pool.append_layer_major(root_o, k, v)
+    seqs = []
+    for b in range(forks):
+        s = cache.fork_sequence(root, prefix)
+        so = pool.fork_sequence(root_o, prefix)
+        n = suffix[b]
+        if n:
+            k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            cache.append_layer_major(s, [dev(k[l]) for l in range(L)],
+                                     [dev(v[l]) for l in range(L)])
+            pool.append_layer_major(so, k, v)
+        seqs.append((s, so))
+    B = len(seqs)
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], hq, max_tokens=prefix + max(suffix) + 8)
+    for step in range(3):
+        batch.prepare()
+        assert batch.shared_pages() == prefix // P
+        hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+        tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+        for b, (_, so) in enumerate(seqs):
+            t = pool.block_table(so)
+            tables[b, : len(t)] = t
+        keys = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        values = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        for layer in range(L):
+            q = rng.standard_normal((B, hq, D), dtype=np.float32)
+            out = torch.empty(B, hq, D, device=device)
+            batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+            batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            torch.cuda.synchronize()
+            kp, vp = pool.layer_pages(layer)
+            ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
+                                        threads=8)
+            np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+        for b, (_, so) in enumerate(seqs):
+            pool.append(so, keys[:, b], values[:, b])
+    batch.close()
