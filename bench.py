@@ -416,6 +416,8 @@ def main():
                     help="layers timed on the CPU oracle with one thread")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="launch the per-layer append separately instead of fused into decode")
     ap.add_argument("--no-shuffle", action="store_true",
                     help="allocate pages in pool order instead of scattering them")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
@@ -470,16 +472,22 @@ def main():
             e[3].record(stream)  # creates the event handle the library records
     torch.cuda.synchronize()
 
+    fused = not args.separate_append
+
     def step(events):
         batch.prepare(stream)
         for l in range(L):
             if events is not None:
                 events[l][0].record(stream)
-            batch.append_layer(l, k[l], v[l], stream)
+            if not fused:
+                batch.append_layer(l, k[l], v[l], stream)
             if events is not None:
                 events[l][1].record(stream)
                 batch.set_timing_event(events[l][3])
-            batch.attention_layer(l, q[l], k[l], v[l], out[l], stream)
+            if fused:
+                batch.append_attention_layer(l, q[l], k[l], v[l], out[l], stream)
+            else:
+                batch.attention_layer(l, q[l], k[l], v[l], out[l], stream)
             if events is not None:
                 events[l][2].record(stream)
         batch.set_timing_event(None)
@@ -493,7 +501,20 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    append_ms = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(args.steps) for l in range(L)]
+    if fused:
+        # The step's appends ran inside the decode kernel; time the standalone
+        # append kernel separately (it rewrites the same slots with the same
+        # rows) for the append rate.
+        aev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L * 3)]
+        for r in range(3 * L):
+            aev[r][0].record(stream)
+            batch.append_layer(r % L, k[r % L], v[r % L], stream)
+            aev[r][1].record(stream)
+        torch.cuda.synchronize()
+        append_ms = [e[0].elapsed_time(e[1]) for e in aev]
+    else:
+        append_ms = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(args.steps)
+                     for l in range(L)]
     attn_ms = [ev[i][l][1].elapsed_time(ev[i][l][2]) for i in range(args.steps) for l in range(L)]
     kern_ms = [ev[i][l][1].elapsed_time(ev[i][l][3]) for i in range(args.steps) for l in range(L)]
     merge_ms = [ev[i][l][3].elapsed_time(ev[i][l][2]) for i in range(args.steps) for l in range(L)]
@@ -509,8 +530,14 @@ def main():
                                     for i in range(args.steps)]))
     else:
         roof_bytes = launch_bytes
+    if fused:
+        # The decode kernel also writes the new token rows into their pages.
+        roof_bytes += append_bytes(nseq) / 2
+        launch_bytes += append_bytes(nseq) / 2
     step_decode = roof_bytes * L
-    step_append = append_bytes(nseq) * L
+    # Fused: the append's writes are in roof_bytes and its source rows are the
+    # attention tail, already counted there.
+    step_append = 0 if fused else append_bytes(nseq) * L
     value = (step_decode + step_append) / (ms_per_step * 1e-3) / 1e9
     attn_avg_ms = float(np.mean(attn_ms))
     kern_avg_ms = float(np.mean(kern_ms))
@@ -579,6 +606,8 @@ def main():
         "decode_attn_logical_gbps": round(logical_gbps, 2),
         "append_gbps": round(append_gbps, 2),
         "append_avg_us": round(append_avg_ms * 1e3, 2),
+        "append_mode": ("fused into the decode kernel; append_gbps is the standalone append "
+                        "kernel, timed separately" if fused else "separate append kernel"),
         "decode_avg_us": round(attn_avg_ms * 1e3, 2),
         "decode_median_us": round(float(np.median(attn_ms)) * 1e3, 2),
         "decode_kernel_avg_us": round(kern_avg_ms * 1e3, 2),

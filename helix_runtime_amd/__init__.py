@@ -467,6 +467,13 @@ class DecodeBatch:
     def prepare(self, stream=None):
         check(_lib().helix_decode_batch_prepare(self._h, _stream(stream)))
 
+    def append_attention_layer(self, layer, query, keys, values, output, stream=None):
+        """append_layer + attention_layer in one decode launch (the new token
+        rows are the attention tail and are written to their slots)."""
+        check(_lib().helix_decode_batch_append_attention_layer(
+            self._h, layer, _ptr(query), _ptr(keys), _ptr(values), _ptr(output),
+            _stream(stream)))
+
     def prepare_chunk(self, tokens, stream=None):
         """Reserve `tokens` slots per sequence (chunked prefill step)."""
         check(_lib().helix_decode_batch_prepare_chunk(self._h, tokens, _stream(stream)))

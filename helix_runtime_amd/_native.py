@@ -131,6 +131,7 @@ SIGNATURES = {
     "helix_paged_append_chunk": (
         c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, c_size, vp]),
     "helix_decode_batch_prepare_chunk": (c_int, [vp, c_size, vp]),
+    "helix_decode_batch_append_attention_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_prefill_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_create": (c_int, [vp, P(Sequence), c_size, c_size, c_size, c_size, P(vp)]),
     "helix_decode_batch_prepare": (c_int, [vp, vp]),

@@ -944,6 +944,18 @@ int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, cons
   });
 }
 
+int helix_decode_batch_append_attention_layer(helix_decode_batch* b, size_t layer,
+                                              const float* query, const float* keys,
+                                              const float* values, float* output,
+                                              helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    check(keys != nullptr && values != nullptr, Status::kInvalidArgument,
+          "decode batch append needs key and value rows");
+    b->batch->append_attention_layer(layer, query, keys, values, output, as_stream(stream));
+  });
+}
+
 int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const float* query,
                                      const float* chunk_key, const float* chunk_value,
                                      float* output, helix_stream stream) {

@@ -322,6 +322,11 @@ struct DecodeKernelArgs {
   int first_page;       // stream mode: pages before this are covered by the cascade
   long long prefix_slot0;  // cascade: chunk c of unit u at prefix_slot0 + c * units + u
   int prefix_chunks;    // cascade: key chunks of the shared prefix
+  // Fused append (stream mode): the tail row of sequence b is also written
+  // to physical slot append_slots[b] of these pools (negative: skipped).
+  const std::int64_t* append_slots;
+  float* append_key_pool;
+  float* append_value_pool;
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -757,7 +762,8 @@ template <int G>
 __global__ __launch_bounds__(64) void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
+    const std::int64_t* __restrict__ append_slots) {
   // The block table and lengths are read-only here and do not alias the
   // outputs; with the restrict-qualified parameters their uniform reads
   // become scalar loads.
@@ -767,6 +773,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   a.part_o = part_o;
   a.part_ml = part_ml;
   a.segments = segments;
+  a.append_slots = append_slots;
   constexpr int D = 128;
   constexpr int P = 16;
   constexpr int R = G >= 4 ? G / 4 : 1;
@@ -786,6 +793,9 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   __shared__ long long s_res_dst[kStage];  // >= 0: first output row; < 0: -1 - partial slot
   __shared__ int2 s_seg[kStage];
   __shared__ int s_seg_unit[kStage];
+  __shared__ __align__(16) float4 s_app_k[kStage][32];
+  __shared__ __align__(16) float4 s_app_v[kStage][32];
+  __shared__ long long s_app_dst[kStage];  // element offset of the row, < 0: none
 
   const int lane = threadIdx.x;
   const int parity = lane >> 5;
@@ -1005,7 +1015,15 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
 
   int nres = 0;
   int nseg = 0;
+  int napp = 0;
   auto flush = [&]() {
+    for (int r = 0; r < napp; ++r) {
+      const long long dst = s_app_dst[r];
+      if (parity == 0 && dst >= 0) {
+        reinterpret_cast<float4*>(a.append_key_pool + dst)[j] = s_app_k[r][j];
+        reinterpret_cast<float4*>(a.append_value_pool + dst)[j] = s_app_v[r][j];
+      }
+    }
     for (int r = 0; r < nres; ++r) {
       const long long dst = s_res_dst[r];
       if (parity == 0) {
@@ -1033,6 +1051,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
     }
     nres = 0;
     nseg = 0;
+    napp = 0;
     __syncthreads();
   };
 
@@ -1110,6 +1129,22 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
           s_seg_unit[nseg] = d.kvh * a.batch + d.b;
         }
         ++nseg;
+      }
+      if (a.append_slots != nullptr && d.p == d.np - 1) {
+        // The tail row is this step's new token: stage its page write.
+        if (napp == kStage) flush();
+        if (parity == 0) {
+          s_app_k[napp][j] = k[0];
+          s_app_v[napp][j] = v[0];
+        }
+        if (lane == 0) {
+          const std::int64_t slot = a.append_slots[d.b];
+          s_app_dst[napp] =
+              slot < 0 ? -1
+                       : ((slot / P * static_cast<long long>(a.kv_heads) + d.kvh) * P + slot % P) * D;
+        }
+        ++napp;
+        __syncthreads();
       }
     }
     process(k, v, qc, valid);
@@ -1585,6 +1620,9 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
     k.segments = reinterpret_cast<int*>(ws + lay.segments);
     k.first_page = static_cast<int>(a.shared_pages);
+    k.append_slots = a.append_slots;
+    k.append_key_pool = a.append_key_pool;
+    k.append_value_pool = a.append_value_pool;
     k.prefix_slot0 = static_cast<long long>(a.batch * a.kv_heads + kMaxStreamWaves);
     if (a.shared_pages > 0) {
       const std::size_t cp = cascade_chunk_pages(a.shared_pages, a.batch, group, a.kv_heads);
@@ -1610,19 +1648,23 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     switch (group) {
       case 1:
         decode_stream_kernel<1><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments);
+                                                         k.part_o, k.part_ml, k.segments,
+                                                         k.append_slots);
         break;
       case 2:
         decode_stream_kernel<2><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments);
+                                                         k.part_o, k.part_ml, k.segments,
+                                                         k.append_slots);
         break;
       case 4:
         decode_stream_kernel<4><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments);
+                                                         k.part_o, k.part_ml, k.segments,
+                                                         k.append_slots);
         break;
       case 8:
         decode_stream_kernel<8><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments);
+                                                         k.part_o, k.part_ml, k.segments,
+                                                         k.append_slots);
         break;
       default: return hipErrorInvalidValue;
     }

@@ -98,6 +98,11 @@ struct DecodeArgs {
   // once for all sequences on the matrix cores and the stream kernel covers
   // the rest.  0: off.
   std::size_t shared_pages = 0;
+  // Fused append (stream mode only): also write tail row b to physical slot
+  // append_slots[b] (block * 16 + offset, negative: skipped) of these pools.
+  const std::int64_t* append_slots = nullptr;
+  float* append_key_pool = nullptr;
+  float* append_value_pool = nullptr;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;

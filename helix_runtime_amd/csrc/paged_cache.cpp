@@ -575,8 +575,20 @@ void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float
             "decode batch append launch");
 }
 
+void DecodeBatch::append_attention_layer(std::size_t layer, const float* query,
+                                         const float* keys, const float* values, float* out,
+                                         hipStream_t stream) const {
+  if (pages_per_split_ != 0) {
+    append_layer(layer, keys, values, stream);
+    attention_layer(layer, query, keys, values, out, stream);
+    return;
+  }
+  attention_layer(layer, query, keys, values, out, stream, true);
+}
+
 void DecodeBatch::attention_layer(std::size_t layer, const float* query, const float* tail_key,
-                                  const float* tail_value, float* out, hipStream_t stream) const {
+                                  const float* tail_value, float* out, hipStream_t stream,
+                                  bool fused_append) const {
   const PagedConfig& c = state_->manager.config();
   check(prepared_, Status::kInvalidArgument, "decode batch attention before prepare");
   check(step_tokens_ == 1, Status::kInvalidArgument,
@@ -603,6 +615,11 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.items = items_;
   a.between_event = between_event_;
   a.shared_pages = shared_pages_;
+  if (fused_append) {
+    a.append_slots = slots();
+    a.append_key_pool = state_->key_pool(layer);
+    a.append_value_pool = state_->value_pool(layer);
+  }
   DeviceGuard guard(state_->device);
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
 }

@@ -164,9 +164,15 @@ public:
   void append_layer(std::size_t layer, const float* keys, const float* values,
                     hipStream_t stream) const;
   void attention_layer(std::size_t layer, const float* query, const float* tail_key,
-                       const float* tail_value, float* out, hipStream_t stream) const;
+                       const float* tail_value, float* out, hipStream_t stream,
+                       bool fused_append = false) const;
   void prefill_layer(std::size_t layer, const float* query, const float* chunk_key,
                      const float* chunk_value, float* out, hipStream_t stream) const;
+  // append_layer + attention_layer in one decode launch where the decode
+  // kernel supports it (stream mode): the kernel writes each sequence's new
+  // token into its slot as it reads the token as the attention tail.
+  void append_attention_layer(std::size_t layer, const float* query, const float* keys,
+                              const float* values, float* out, hipStream_t stream) const;
 
   [[nodiscard]] const std::uint32_t* tables() const;
   [[nodiscard]] const std::int32_t* lengths() const;

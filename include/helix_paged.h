@@ -301,6 +301,14 @@ int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* se
                               size_t batch, size_t q_heads, size_t max_tokens,
                               size_t pages_per_split, helix_decode_batch** out);
 int helix_decode_batch_prepare(helix_decode_batch* b, helix_stream stream);
+/* append_layer() + attention_layer() of a one-token step in one decode launch
+ * (keys/values [batch, kv_heads, 128] are both the rows to append and the
+ * attention tail): the decode kernel writes each new token into its reserved
+ * slot as it reads it, so the step needs no separate append launch. */
+int helix_decode_batch_append_attention_layer(helix_decode_batch* b, size_t layer,
+                                              const float* query, const float* keys,
+                                              const float* values, float* output,
+                                              helix_stream stream);
 int helix_decode_batch_prepare_chunk(helix_decode_batch* b, size_t tokens, helix_stream stream);
 int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
                                     const float* values, helix_stream stream);

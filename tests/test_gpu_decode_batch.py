@@ -25,8 +25,9 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("hq", [8, 32])
-def test_decode_batch_steps_match_oracle(device, hq):
+def test_decode_batch_steps_match_oracle(device, hq, fused):
     L, H, D, P = 2, 8, 128, 16
     rng = np.random.default_rng(hq)
     lengths = [1, 15, 16, 31, 47, 200]
@@ -59,8 +60,12 @@ def test_decode_batch_steps_match_oracle(device, hq):
         for layer in range(L):
             q = rng.standard_normal((B, hq, D), dtype=np.float32)
             out = torch.empty(B, hq, D, device=device)
-            batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
-            batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            if fused:
+                batch.append_attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]),
+                                             out)
+            else:
+                batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+                batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
             torch.cuda.synchronize()
             kp, vp = pool.layer_pages(layer)
             for b, (_, so) in enumerate(seqs):
@@ -173,8 +178,9 @@ def test_prefix_sharing_decode_with_cow_forks(device):
     batch.close()
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("hq", [8, 32])
-def test_cascade_shared_prefix_decode(device, hq):
+def test_cascade_shared_prefix_decode(device, hq, fused):
     """Sequences forked from one root share its full leading pages; the decode
     step attends them once for the batch (cascade) and the per-sequence rest
     through the stream kernel.  Outputs match the oracle over several steps,
@@ -218,8 +224,12 @@ def test_cascade_shared_prefix_decode(device, hq):
         for layer in range(L):
             q = rng.standard_normal((B, hq, D), dtype=np.float32)
             out = torch.empty(B, hq, D, device=device)
-            batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
-            batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            if fused:
+                batch.append_attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]),
+                                             out)
+            else:
+                batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+                batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
             torch.cuda.synchronize()
             kp, vp = pool.layer_pages(layer)
             ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
@@ -227,4 +237,11 @@ def test_cascade_shared_prefix_decode(device, hq):
             np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
         for b, (_, so) in enumerate(seqs):
             pool.append(so, keys[:, b], values[:, b])
+    assert cache.stats() == pool.stats()
+    for s, so in seqs:
+        for layer in range(L):
+            gk, gv = cache.retrieve_layer(s, layer)
+            ok, ov = pool.copy_layer(so, layer)
+            np.testing.assert_array_equal(host(gk), ok)
+            np.testing.assert_array_equal(host(gv), ov)
     batch.close()
