@@ -758,8 +758,9 @@ struct PageDesc {
   bool skip;
 };
 
-template <int G>
-__global__ __launch_bounds__(64) void decode_stream_kernel(
+template <int G, bool APPEND>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
+void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
@@ -773,7 +774,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   a.part_o = part_o;
   a.part_ml = part_ml;
   a.segments = segments;
-  a.append_slots = append_slots;
+  a.append_slots = APPEND ? append_slots : nullptr;
   constexpr int D = 128;
   constexpr int P = 16;
   constexpr int R = G >= 4 ? G / 4 : 1;
@@ -985,20 +986,27 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
 #pragma unroll
     for (int h = 0; h < G; ++h) al[h] = s_head[0][h];
     __syncthreads();
+    if (valid < P) {  // wave-uniform: only partial pages and the tail
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool keep = 2 * i + parity < valid;
-      v[i].x = keep ? v[i].x : 0.0f;
-      v[i].y = keep ? v[i].y : 0.0f;
-      v[i].z = keep ? v[i].z : 0.0f;
-      v[i].w = keep ? v[i].w : 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        const bool keep = 2 * i + parity < valid;
+        v[i].x = keep ? v[i].x : 0.0f;
+        v[i].y = keep ? v[i].y : 0.0f;
+        v[i].z = keep ? v[i].z : 0.0f;
+        v[i].w = keep ? v[i].w : 0.0f;
+      }
     }
+    bool rescale = false;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      acc[h][0] *= al[h];
-      acc[h][1] *= al[h];
-      acc[h][2] *= al[h];
-      acc[h][3] *= al[h];
+    for (int h = 0; h < G; ++h) rescale = rescale || al[h] != 1.0f;
+    if (rescale) {  // wave-uniform: some head's running maximum moved
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        acc[h][0] *= al[h];
+        acc[h][1] *= al[h];
+        acc[h][2] *= al[h];
+        acc[h][3] *= al[h];
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1017,7 +1025,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
   int nseg = 0;
   int napp = 0;
   auto flush = [&]() {
-    for (int r = 0; r < napp; ++r) {
+    for (int r = 0; r < (APPEND ? napp : 0); ++r) {
       const long long dst = s_app_dst[r];
       if (parity == 0 && dst >= 0) {
         reinterpret_cast<float4*>(a.append_key_pool + dst)[j] = s_app_k[r][j];
@@ -1130,7 +1138,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(
         }
         ++nseg;
       }
-      if (a.append_slots != nullptr && d.p == d.np - 1) {
+      if (APPEND && d.p == d.np - 1) {
         // The tail row is this step's new token: stage its page write.
         if (napp == kStage) flush();
         if (parity == 0) {
@@ -1647,24 +1655,40 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(waves));
     switch (group) {
       case 1:
-        decode_stream_kernel<1><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments,
-                                                         k.append_slots);
+        if (k.append_slots != nullptr) {
+          decode_stream_kernel<1, true><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
+        } else {
+          decode_stream_kernel<1, false><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
+        }
         break;
       case 2:
-        decode_stream_kernel<2><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments,
-                                                         k.append_slots);
+        if (k.append_slots != nullptr) {
+          decode_stream_kernel<2, true><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
+        } else {
+          decode_stream_kernel<2, false><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
+        }
         break;
       case 4:
-        decode_stream_kernel<4><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments,
-                                                         k.append_slots);
+        if (k.append_slots != nullptr) {
+          decode_stream_kernel<4, true><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
+        } else {
+          decode_stream_kernel<4, false><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
+        }
         break;
       case 8:
-        decode_stream_kernel<8><<<grid, 64, 0, stream>>>(k, k.tables, k.lengths, k.out,
-                                                         k.part_o, k.part_ml, k.segments,
-                                                         k.append_slots);
+        if (k.append_slots != nullptr) {
+          decode_stream_kernel<8, true><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
+        } else {
+          decode_stream_kernel<8, false><<<grid, 64, 0, stream>>>(
+              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
+        }
         break;
       default: return hipErrorInvalidValue;
     }
