@@ -12,8 +12,8 @@
 // kv head times 128 / G consecutive chunk positions, so every K/V byte
 // staged in LDS feeds all G heads.  Each wavefront holds 32 of those rows
 // (two 16-row tiles) and keeps its Q rows in registers.  Keys stream through
-// a double-buffered LDS stage 32 at a time: history pages through the block
-// table, then the chunk rows.
+// a double-buffered LDS stage one page (16 keys) at a time: history pages
+// through the block table, then the chunk rows.
 //
 // Layout trick.  Scores are computed transposed, S^T = K Q^T, so the MFMA
 // result leaves each lane holding 4 keys of one query row; the row's max and
@@ -52,7 +52,6 @@ struct PrefillKernelArgs {
   const float* query;
   const float* key_pool;
   const float* value_pool;
-  const std::uint32_t* tables;
   const std::int32_t* lengths;
   const float* chunk_key;
   const float* chunk_value;
@@ -64,7 +63,6 @@ struct PrefillKernelArgs {
   int pos_blocks;
   std::uint32_t physical_blocks;
   float qscale;
-  const std::uint32_t* order;  // optional workgroup order (packed work items)
   // Cascade mode (shared-prefix decode): rows are (sequence, head) pairs of
   // one kv head, keys are the first cascade_keys tokens of table row 0, and
   // each row leaves a partial (m, l, o) at slot prefix_slot0 + kvh * batch +
@@ -90,7 +88,9 @@ __device__ __forceinline__ bool finite4(const float4& v) {
 }
 
 template <int G, bool CASCADE>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
+                                                         const std::uint32_t* __restrict__ tables,
+                                                         const std::uint32_t* __restrict__ order) {
   constexpr int PW = kRows / G;  // chunk positions per workgroup
   __shared__ __align__(16) float s_k[2][kKeys * kKStride];
   __shared__ __align__(16) float s_v[2][kKeys * D];
@@ -105,8 +105,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   // longest-first order; by default later position blocks (more keys) of a
   // (sequence, kv head) go first.
   std::uint32_t item = blockIdx.x;
-  if (a.order != nullptr) {
-    item = a.order[blockIdx.x];
+  if (order != nullptr) {
+    item = order[blockIdx.x];
   } else {
     const std::uint32_t x = item % a.pos_blocks;
     item = item - x + (a.pos_blocks - 1 - x);
@@ -125,7 +125,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   const int key_begin = CASCADE ? chunk * a.cascade_chunk_pages * P : 0;
   const int key_end =
       CASCADE ? min(hist, (chunk + 1) * a.cascade_chunk_pages * P) : hist + min(T, pos0 + PW);
-  const std::uint32_t* table = a.tables + static_cast<std::size_t>(b) * a.max_blocks;
+  // Read-only and indexed by workgroup-uniform values: scalar loads.
+  const std::uint32_t* __restrict__ table = tables + static_cast<std::size_t>(b) * a.max_blocks;
   const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
 
   // Rows of this lane: tile t holds workgroup row wave * 32 + t * 16 + col.
@@ -173,53 +174,73 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
   const int srow = tid >> 5;
   const int scol = tid & 31;
   float4 stk[2], stv[2];
-  bool st_nonfinite = false;
+  // A 16-key block is exactly one page, so a history block needs one
+  // (uniform) table entry.  The non-finite check runs at store time, when
+  // the values have arrived, so the loads stay in flight across the block's
+  // compute.
+  // lane_off: this lane's float offset inside a 16-row block (page or chunk).
+  const int lane_off = srow * D + scol * 4;
   auto stage_load = [&](int blk) {
-    st_nonfinite = false;
+    const int key0 = blk * kKeys;
+    // Uniform bases: the history page of this block and the chunk rows.
+    const float* kpage = a.key_pool;
+    const float* vpage = a.value_pool;
+    bool page_ok = false;
+    if (key0 < hist) {
+      const std::uint32_t page = table[blk];
+      page_ok = page < a.physical_blocks;
+      bad = bad || !page_ok;
+      const std::size_t off =
+          page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
+      kpage += off;
+      vpage += off;
+    }
+    const long long crow = static_cast<long long>(chunk_row0) + key0 - hist;
+    const float* kchunk = a.chunk_key + crow * D;
+    const float* vchunk = a.chunk_value + crow * D;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int key = blk * kKeys + srow + 8 * r;
-      const float* kp = nullptr;
-      const float* vp = nullptr;
-      if (key < hist) {
-        std::uint32_t page = table[key / P];
-        if (page >= a.physical_blocks) {
-          bad = true;
-        } else {
-          const std::size_t off =
-              ((static_cast<std::size_t>(page) * a.kv_heads + kvh) * P + key % P) * D + scol * 4;
-          kp = a.key_pool + off;
-          vp = a.value_pool + off;
-        }
-      } else if (key < key_end) {
-        const std::size_t off = (chunk_row0 + (key - hist)) * D + scol * 4;
-        kp = a.chunk_key + off;
-        vp = a.chunk_value + off;
-      }
-      stk[r] = kp ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
-      stv[r] = vp ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
-      // A chunk row that some query row of this workgroup masks.
-      if (!CASCADE && key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) {
-        st_nonfinite = true;
-      }
+      const int key = key0 + srow + 8 * r;
+      const bool in_hist = key < hist;
+      const bool valid = key < key_end && (!in_hist || page_ok);
+      const int o = lane_off + 8 * r * D;
+      const float* kp = (in_hist ? kpage : kchunk) + o;
+      const float* vp = (in_hist ? vpage : vchunk) + o;
+      stk[r] = valid ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
+      stv[r] = valid ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  auto stage_store = [&](int buf) {
+  // Returns whether a staged value row is non-finite and some query row of
+  // this workgroup masks it (a chunk row past the first position).
+  auto stage_store = [&](int buf, int blk) {
+    bool nonfinite = false;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int kr = srow + 8 * r;
       *reinterpret_cast<float4*>(&s_k[buf][kr * kKStride + scol * 4]) = stk[r];
       *reinterpret_cast<float4*>(&s_v[buf][kr * D + scol * 4]) = stv[r];
+      const int key = blk * kKeys + kr;
+      if (!CASCADE && key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) {
+        nonfinite = true;
+      }
     }
+    return nonfinite;
   };
 
+  // Only a block holding chunk rows past the workgroup's first position can
+  // carry a masked value row; every other block needs a plain barrier
+  // (__syncthreads_or costs two more).
+  auto staged_barrier = [&](bool nonfinite, int blk) -> int {
+    if (!CASCADE && blk * kKeys + kKeys > hist + pos0 + 1) return __syncthreads_or(nonfinite);
+    __syncthreads();
+    return 0;
+  };
   const int nblocks = (key_end + kKeys - 1) / kKeys;
   const int nfirst = key_begin / kKeys;
   int exact_pv = 0;
   if (nblocks > nfirst) {
     stage_load(nfirst);
-    stage_store(nfirst & 1);
-    exact_pv = __syncthreads_or(st_nonfinite);
+    exact_pv = staged_barrier(stage_store(nfirst & 1, nfirst), nfirst);
   }
   for (int n = nfirst; n < nblocks; ++n) {
     const int buf = n & 1;
@@ -336,8 +357,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a) {
       }
     }
 
-    if (n + 1 < nblocks) stage_store(buf ^ 1);
-    exact_pv = __syncthreads_or(st_nonfinite);
+    const bool nonfinite = n + 1 < nblocks && stage_store(buf ^ 1, n + 1);
+    exact_pv = staged_barrier(nonfinite, n + 1);
   }
 
   const int any_bad = __syncthreads_or(bad);
@@ -414,7 +435,6 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.query = a.query;
   k.key_pool = a.key_pool;
   k.value_pool = a.value_pool;
-  k.tables = a.tables;
   k.lengths = a.lengths;
   k.chunk_key = a.chunk_key;
   k.chunk_value = a.chunk_value;
@@ -426,14 +446,13 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.pos_blocks = static_cast<int>((a.tokens + pw - 1) / pw);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(D));
-  k.order = a.order;
   k.batch = static_cast<int>(a.batch);
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   switch (group) {
-    case 1: prefill_kernel<1, false><<<grid, 256, 0, stream>>>(k); break;
-    case 2: prefill_kernel<2, false><<<grid, 256, 0, stream>>>(k); break;
-    case 4: prefill_kernel<4, false><<<grid, 256, 0, stream>>>(k); break;
-    case 8: prefill_kernel<8, false><<<grid, 256, 0, stream>>>(k); break;
+    case 1: prefill_kernel<1, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
+    case 2: prefill_kernel<2, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
+    case 4: prefill_kernel<4, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
+    case 8: prefill_kernel<8, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -446,7 +465,6 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
   k.query = a.query;
   k.key_pool = a.key_pool;
   k.value_pool = a.value_pool;
-  k.tables = a.table;
   k.q_heads = static_cast<int>(a.q_heads);
   k.kv_heads = static_cast<int>(a.kv_heads);
   k.tokens = 1;
@@ -465,10 +483,10 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
       (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * chunks));
   switch (group) {
-    case 1: prefill_kernel<1, true><<<grid, 256, 0, stream>>>(k); break;
-    case 2: prefill_kernel<2, true><<<grid, 256, 0, stream>>>(k); break;
-    case 4: prefill_kernel<4, true><<<grid, 256, 0, stream>>>(k); break;
-    case 8: prefill_kernel<8, true><<<grid, 256, 0, stream>>>(k); break;
+    case 1: prefill_kernel<1, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
+    case 2: prefill_kernel<2, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
+    case 4: prefill_kernel<4, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
+    case 8: prefill_kernel<8, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
