@@ -35,6 +35,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 namespace helix::hip {
 namespace {
@@ -75,8 +76,30 @@ struct PrefillKernelArgs {
   long long prefix_slot0;
 };
 
+// exp2(a - b), with a == b (also +inf == +inf, -inf == -inf) giving 1 and
+// a = -inf < b giving 0.  v_exp_f32 directly: results below 2^-126 flush to
+// zero, far under the tolerance of a probability normalised by a sum >= 1.
 __device__ __forceinline__ float exp2_ratio(float a, float b) {
-  return a == b ? 1.0f : exp2f(a - b);
+  return a == b ? 1.0f : __builtin_amdgcn_exp2f(a - b);
+}
+
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
+// four key groups) with the cross-row lane swaps.
+__device__ __forceinline__ float row_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float row_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
 __device__ __forceinline__ float comp(const float4& v, int c) {
@@ -264,42 +287,44 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
       }
     }
 
-    // Online softmax (exp2 domain), lane-local rescale of O.
+    // Online softmax (exp2 domain), lane-local rescale of O.  A block whose
+    // keys every row of the workgroup sees (all but the last blocks) skips
+    // the mask.
     float p[2][4];
+    const bool full = (n + 1) * kKeys <= min(key_end, hist + pos0 + 1);
+    auto softmax = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float x[4];
-      float mx = -INFINITY;
+      for (int t = 0; t < 2; ++t) {
+        float x[4];
+        bool vis[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = n * kKeys + 4 * grp + i;
-        const bool vis = key < key_end && (key < hist || key - hist <= qpos[t]);
-        x[i] = vis ? st[t][i] : -INFINITY;
-        mx = fmaxf(mx, x[i]);
+        for (int i = 0; i < 4; ++i) {
+          const int key = n * kKeys + 4 * grp + i;
+          vis[i] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
+          x[i] = vis[i] ? st[t][i] : -INFINITY;
+        }
+        const float mx = row_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+        const float mn = fmaxf(m[t], mx);
+        const float alpha = exp2_ratio(m[t], mn);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[t][i] = vis[i] ? exp2_ratio(x[i], mn) : 0.f;
+        const float sum = row_sum((p[t][0] + p[t][1]) + (p[t][2] + p[t][3]));
+        l[t] = l[t] * alpha + sum;
+        m[t] = mn;
+        // Rows whose maximum did not move keep their accumulators as they are.
+        if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.0f)) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
+        }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m[t], mx);
-      const float alpha = exp2_ratio(m[t], mn);
-      float sum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = n * kKeys + 4 * grp + i;
-        const bool vis = key < key_end && (key < hist || key - hist <= qpos[t]);
-        p[t][i] = vis ? exp2_ratio(x[i], mn) : 0.f;
-        sum += p[t][i];
-      }
-      sum += __shfl_xor(sum, 16, 64);
-      sum += __shfl_xor(sum, 32, 64);
-      l[t] = l[t] * alpha + sum;
-      m[t] = mn;
-      // Rows whose maximum did not move keep their accumulators as they are.
-      if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.0f)) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
-      }
+    };
+    if (full) {
+      softmax(std::true_type{});
+    } else {
+      softmax(std::false_type{});
     }
 
     if (!exact_pv) {
