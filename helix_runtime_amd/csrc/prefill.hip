@@ -275,12 +275,12 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     // query row t*16 + col.
     v4f st[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKStride + 16 * c + 4 * grp]);
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int c = 0; c < 8; ++c) {
+        const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKStride + 16 * c + 4 * grp]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int e = 0; e < 4; ++e) {
           st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(comp(kk, e), comp(q[t][c], e), st[t], 0,
                                                        0, 0);
         }
@@ -312,13 +312,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
         const float sum = row_sum((p[t][0] + p[t][1]) + (p[t][2] + p[t][3]));
         l[t] = l[t] * alpha + sum;
         m[t] = mn;
-        // Rows whose maximum did not move keep their accumulators as they are.
-        if (__builtin_amdgcn_read_exec() & __ballot(alpha != 1.0f)) {
+        // Branch-free rescale (alpha is 1 for rows whose maximum held).
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
-        }
+          for (int c = 0; c < 4; ++c) o[t][h][c] *= alpha;
       }
     };
     if (full) {
@@ -436,10 +434,13 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
 std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
 
 // Key pages per cascade work item: enough chunks that the launch has about
-// kCascadeTarget workgroups, at most kMaxCascadeChunks chunks.
+// one workgroup per CU, at most kMaxCascadeChunks chunks.  Every extra chunk
+// re-loads the query tile, writes one more partial per row and adds merge
+// work; beyond one workgroup per CU that costs more than the added
+// parallelism gains (128 sequences x 32 heads: 8 chunks beat both 16 and 4).
 std::size_t cascade_chunk_pages(std::size_t shared_pages, std::size_t batch, std::size_t group,
                                 std::size_t kv_heads) {
-  constexpr std::size_t kCascadeTarget = 1024;
+  constexpr std::size_t kCascadeTarget = 256;
   const std::size_t items = ((batch * group + kRows - 1) / kRows) * kv_heads;
   std::size_t chunks = (kCascadeTarget + items - 1) / items;
   if (chunks > kMaxCascadeChunks) chunks = kMaxCascadeChunks;
