@@ -1578,8 +1578,10 @@ namespace {
 
 // Wavefronts the stream kernel launches: every resident slot of the device
 // (two per SIMD up to four query heads per kv head, one for eight, as the
-// kernels' register use allows), at most kMaxStreamWaves.
-std::size_t stream_waves(std::size_t group) {
+// kernels' register use allows), at most kMaxStreamWaves.  beside_prefix:
+// one per SIMD whatever the group, so the concurrent cascade prefix pass
+// finds registers on every SIMD.
+std::size_t stream_waves(std::size_t group, bool beside_prefix) {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -1591,7 +1593,7 @@ std::size_t stream_waves(std::size_t group) {
     }
     cus[dev] = n;
   }
-  const std::size_t per_simd = group >= 8 ? 1 : 2;
+  const std::size_t per_simd = group >= 8 || beside_prefix ? 1 : 2;
   const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
   return w < kMaxStreamWaves ? w : kMaxStreamWaves;
 }
@@ -1622,7 +1624,9 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
   if (streamed) {
-    const std::size_t waves = stream_waves(group);
+    const bool overlap = a.shared_pages > 0 && a.side_stream != nullptr &&
+                         a.fork_event != nullptr && a.join_event != nullptr;
+    const std::size_t waves = stream_waves(group, overlap);
     const WorkspaceLayout lay = stream_layout_for(a.batch, a.q_heads, a.kv_heads);
     k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
@@ -1648,8 +1652,22 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
       c.shared_pages = a.shared_pages;
       c.physical_blocks = a.physical_blocks;
       c.prefix_slot0 = static_cast<std::size_t>(k.prefix_slot0);
-      const hipError_t e = launch_cascade_prefix(c, stream);
-      if (e != hipSuccess) return e;
+      if (overlap) {
+        hipError_t e = hipEventRecord(a.fork_event, stream);
+        if (e == hipSuccess) e = hipStreamWaitEvent(a.side_stream, a.fork_event, 0);
+        if (e == hipSuccess) e = launch_cascade_prefix(c, a.side_stream);
+        if (e == hipSuccess) e = hipEventRecord(a.join_event, a.side_stream);
+        if (e != hipSuccess) return e;
+        // The stream kernel then runs one wavefront per SIMD: with two,
+        // the prefix workgroups find no registers until stream waves
+        // retire, and the late-starting waves of the static partition
+        // stretch the kernel (128 sequences sharing 64 pages, per layer:
+        // overlapped 103 us, back to back 111 us, overlapped with two
+        // waves per SIMD 124 us).
+      } else {
+        const hipError_t e = launch_cascade_prefix(c, stream);
+        if (e != hipSuccess) return e;
+      }
     }
     k.stream_waves = static_cast<int>(waves);
     const dim3 grid(static_cast<unsigned>(waves));
@@ -1694,8 +1712,14 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // The timing event goes before the join: recorded after a cross-stream
+    // wait it cost about 5 us per launch.
     if (a.between_event != nullptr) {
       e = hipEventRecord(a.between_event, stream);
+      if (e != hipSuccess) return e;
+    }
+    if (overlap) {
+      e = hipStreamWaitEvent(stream, a.join_event, 0);
       if (e != hipSuccess) return e;
     }
     const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));

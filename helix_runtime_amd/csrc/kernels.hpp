@@ -98,6 +98,15 @@ struct DecodeArgs {
   // once for all sequences on the matrix cores and the stream kernel covers
   // the rest.  0: off.
   std::size_t shared_pages = 0;
+  // Optional second stream for the cascade prefix pass: when set (with the
+  // two events), the prefix runs on side_stream concurrently with the
+  // stream kernel, which then takes one wavefront per SIMD and leaves the
+  // other half of each register file to the prefix workgroups.  The merge
+  // waits for both; between_event then marks the end of the stream kernel
+  // only.
+  hipStream_t side_stream = nullptr;
+  hipEvent_t fork_event = nullptr;
+  hipEvent_t join_event = nullptr;
   // Fused append (stream mode only): also write tail row b to physical slot
   // append_slots[b] (block * 16 + offset, negative: skipped) of these pools.
   const std::int64_t* append_slots = nullptr;

@@ -405,12 +405,24 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
 }
 
 DecodeBatch::~DecodeBatch() {
+  // Destructors must not throw: switch devices without the checked guard.
+  int previous = -1;
+  const bool switched = hipGetDevice(&previous) == hipSuccess && previous != state_->device &&
+                        hipSetDevice(state_->device) == hipSuccess;
   for (hipEvent_t e : uploaded_) {
     if (e != nullptr) {
       (void)hipEventSynchronize(e);
       (void)hipEventDestroy(e);
     }
   }
+  if (side_stream_ != nullptr) {
+    (void)hipStreamSynchronize(side_stream_);
+    (void)hipStreamDestroy(side_stream_);
+  }
+  for (hipEvent_t e : {fork_event_, join_event_}) {
+    if (e != nullptr) (void)hipEventDestroy(e);
+  }
+  if (switched) (void)hipSetDevice(previous);
 }
 
 const std::uint32_t* DecodeBatch::tables() const {
@@ -555,6 +567,12 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
     }
     if (shared >= kMinCascadePages) shared_pages_ = shared;
   }
+  if (shared_pages_ > 0 && side_stream_ == nullptr) {
+    // The cascade prefix pass runs on this stream beside the stream kernel.
+    hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "hipStreamCreate");
+    hip_check(hipEventCreateWithFlags(&fork_event_, hipEventDisableTiming), "hipEventCreate");
+    hip_check(hipEventCreateWithFlags(&join_event_, hipEventDisableTiming), "hipEventCreate");
+  }
   step_tokens_ = tokens;
   prepared_ = true;
 }
@@ -615,6 +633,9 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.items = items_;
   a.between_event = between_event_;
   a.shared_pages = shared_pages_;
+  a.side_stream = side_stream_;
+  a.fork_event = fork_event_;
+  a.join_event = join_event_;
   if (fused_append) {
     a.append_slots = slots();
     a.append_key_pool = state_->key_pool(layer);

@@ -206,6 +206,11 @@ private:
   bool prepared_ = false;
   hipEvent_t between_event_ = nullptr;
   std::size_t shared_pages_ = 0;  // cascade prefix of the prepared step (0: off)
+  // Created with the first cascade step: the prefix pass's stream and the
+  // events that fork it from and join it to the caller's stream.
+  hipStream_t side_stream_ = nullptr;
+  hipEvent_t fork_event_ = nullptr;
+  hipEvent_t join_event_ = nullptr;
   // A decode step uses the cascade when at least this many sequences share
   // at least this many leading pages.
   static constexpr std::size_t kMinCascadeBatch = 4;
