@@ -23,6 +23,7 @@ __all__ = [
     "build", "load", "HelixError", "Sequence", "BlockManager", "PagedKvCache", "DecodeBatch",
     "PagedBlockTable", "paged_attention_out", "paged_attention_with_tail_out",
     "paged_decode_attention", "decode_workspace_bytes", "decode_workspace", "append_slots",
+    "PagedPrefixCache", "PREFIX_INSERTED", "PREFIX_ALREADY_PRESENT", "PREFIX_REJECTED_TOO_LARGE",
     "INVALID_ARGUMENT", "OUT_OF_RANGE", "UNSUPPORTED", "RESOURCE_EXHAUSTED", "RUNTIME", "INTERNAL",
 ]
 
@@ -138,6 +139,98 @@ class BlockManager:
         check(_lib().helix_block_manager_geometry(self._h, ctypes.byref(a), ctypes.byref(b),
                                                   ctypes.byref(c)))
         return a.value, b.value, c.value
+
+
+# ---------------------------------------------------------- prefix cache ----
+PREFIX_INSERTED, PREFIX_ALREADY_PRESENT, PREFIX_REJECTED_TOO_LARGE = 0, 1, 2
+
+
+def _tokens(tokens):
+    arr = (ctypes.c_uint32 * max(len(tokens), 1))(*[int(t) for t in tokens])
+    return arr, len(tokens)
+
+
+class PagedPrefixCache:
+    """helix::kv_cache::PagedPrefixCache (include/helix/kv_cache/prefix.hpp:
+    66-112) over a ``PagedKvCache`` (device pool) or a ``BlockManager`` (host
+    bookkeeping only).  ``insert`` returns one of PREFIX_INSERTED,
+    PREFIX_ALREADY_PRESENT, PREFIX_REJECTED_TOO_LARGE; ``lookup_longest``
+    returns ``(sequence, matched_tokens)`` or None, and the caller releases
+    the sequence."""
+
+    def __init__(self, pool, maximum_entries, maximum_block_references):
+        h = ctypes.c_void_p()
+        cfg = _native.PrefixConfig(maximum_entries, maximum_block_references)
+        if isinstance(pool, BlockManager):
+            check(_lib().helix_prefix_cache_create_host(pool._h, ctypes.byref(cfg),
+                                                        ctypes.byref(h)))
+        elif isinstance(pool, PagedKvCache):
+            check(_lib().helix_prefix_cache_create(pool._h, ctypes.byref(cfg), ctypes.byref(h)))
+        else:
+            check(_lib().helix_prefix_cache_create(None, ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self._pool = pool  # the host manager must outlive the index
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib().helix_prefix_cache_destroy(h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def insert(self, namespace_id, tokens, source):
+        arr, n = _tokens(tokens)
+        out = ctypes.c_int()
+        check(_lib().helix_prefix_cache_insert(self._h, namespace_id, arr, n, source,
+                                               ctypes.byref(out)))
+        return out.value
+
+    def lookup_longest(self, namespace_id, tokens, maximum_prefix_tokens=None):
+        arr, n = _tokens(tokens)
+        limit = (1 << 64) - 1 if maximum_prefix_tokens is None else maximum_prefix_tokens
+        hit, seq, matched = ctypes.c_int(), Sequence(), ctypes.c_size_t()
+        check(_lib().helix_prefix_cache_lookup_longest(self._h, namespace_id, arr, n, limit,
+                                                       ctypes.byref(hit), ctypes.byref(seq),
+                                                       ctypes.byref(matched)))
+        return (seq, matched.value) if hit.value else None
+
+    def contains(self, namespace_id, tokens):
+        arr, n = _tokens(tokens)
+        out = ctypes.c_int()
+        check(_lib().helix_prefix_cache_contains(self._h, namespace_id, arr, n,
+                                                 ctypes.byref(out)))
+        return bool(out.value)
+
+    def erase(self, namespace_id, tokens):
+        arr, n = _tokens(tokens)
+        out = ctypes.c_int()
+        check(_lib().helix_prefix_cache_erase(self._h, namespace_id, arr, n, ctypes.byref(out)))
+        return bool(out.value)
+
+    def evict_lru(self):
+        out = ctypes.c_int()
+        check(_lib().helix_prefix_cache_evict_lru(self._h, ctypes.byref(out)))
+        return bool(out.value)
+
+    def clear(self):
+        check(_lib().helix_prefix_cache_clear(self._h))
+
+    def stats(self):
+        s = _native.PrefixStats()
+        check(_lib().helix_prefix_cache_stats(self._h, ctypes.byref(s)))
+        return s.as_dict()
+
+    def config(self):
+        c = _native.PrefixConfig()
+        check(_lib().helix_prefix_cache_config(self._h, ctypes.byref(c)))
+        return c.maximum_entries, c.maximum_block_references
+
+    def block_tokens(self):
+        out = ctypes.c_size_t()
+        check(_lib().helix_prefix_cache_block_tokens(self._h, ctypes.byref(out)))
+        return out.value
 
 
 # ---------------------------------------------------------------- device ----

@@ -61,6 +61,24 @@ class CowCopy(ctypes.Structure):
     _fields_ = [("from_block", c_u32), ("to_block", c_u32), ("tokens", c_size)]
 
 
+PREFIX_STAT_FIELDS = (
+    "maximum_entries", "maximum_block_references", "entry_count", "retained_tokens",
+    "retained_block_references", "peak_entries", "peak_block_references",
+    "lookup_count", "hit_count", "miss_count", "insertion_count", "duplicate_insertion_count",
+    "rejected_insertion_count", "eviction_count", "erase_count")
+
+
+class PrefixStats(ctypes.Structure):
+    _fields_ = [(n, c_u64) for n in PREFIX_STAT_FIELDS]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n in PREFIX_STAT_FIELDS}
+
+
+class PrefixConfig(ctypes.Structure):
+    _fields_ = [("maximum_entries", c_size), ("maximum_block_references", c_size)]
+
+
 P = ctypes.POINTER
 
 # name -> (restype, argtypes)
@@ -142,6 +160,20 @@ SIGNATURES = {
     "helix_decode_batch_shared_pages": (c_int, [vp, P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
     "helix_probe_stream_read": (c_int, [vp, c_size, vp, ctypes.c_uint, vp]),
+    # prefix cache
+    "helix_prefix_cache_create": (c_int, [vp, P(PrefixConfig), P(vp)]),
+    "helix_prefix_cache_create_host": (c_int, [vp, P(PrefixConfig), P(vp)]),
+    "helix_prefix_cache_destroy": (None, [vp]),
+    "helix_prefix_cache_insert": (c_int, [vp, c_u64, P(c_u32), c_size, Sequence, P(c_int)]),
+    "helix_prefix_cache_lookup_longest": (c_int, [vp, c_u64, P(c_u32), c_size, c_size, P(c_int),
+                                                  P(Sequence), P(c_size)]),
+    "helix_prefix_cache_contains": (c_int, [vp, c_u64, P(c_u32), c_size, P(c_int)]),
+    "helix_prefix_cache_erase": (c_int, [vp, c_u64, P(c_u32), c_size, P(c_int)]),
+    "helix_prefix_cache_evict_lru": (c_int, [vp, P(c_int)]),
+    "helix_prefix_cache_clear": (c_int, [vp]),
+    "helix_prefix_cache_stats": (c_int, [vp, P(PrefixStats)]),
+    "helix_prefix_cache_config": (c_int, [vp, P(PrefixConfig)]),
+    "helix_prefix_cache_block_tokens": (c_int, [vp, P(c_size)]),
 }
 
 _lib = None

@@ -5,6 +5,7 @@
 #include "block_manager.hpp"
 #include "kernels.hpp"
 #include "paged_cache.hpp"
+#include "prefix_cache.hpp"
 #include "status.hpp"
 
 #include <hip/hip_runtime.h>
@@ -137,6 +138,71 @@ void validate_attention(const AttentionShape& s, bool allow_empty_history, const
   check(s.queries <= s.keys - s.offset, Status::kInvalidArgument,
         o + ": query range extends beyond the KV token count");
   check(s.value_dim <= 1024, Status::kUnsupported, o + ": value dimension above 1024");
+}
+
+}  // namespace
+
+struct helix_prefix_cache {
+  explicit helix_prefix_cache(std::unique_ptr<helix::PrefixCache> p) : index(std::move(p)) {}
+  std::unique_ptr<helix::PrefixCache> index;
+};
+
+namespace {
+
+// Anchor pools of the prefix cache: host bookkeeping under its handle mutex,
+// or the device cache's state under the cache mutex (block-aligned forks
+// need no page copy).
+class ManagerAnchors final : public helix::AnchorPool {
+public:
+  explicit ManagerAnchors(helix_block_manager* m) : m_(m) {}
+  std::size_t block_tokens() const override { return m_->manager.config().block_tokens; }
+  std::uint64_t cache_id() const override { return m_->manager.cache_id(); }
+  std::size_t length(std::uint64_t id, std::uint64_t cache_id) override {
+    std::scoped_lock lock(m_->mutex);
+    check(id != 0 && cache_id == m_->manager.cache_id(), Status::kInvalidArgument,
+          "prefix cache: sequence handle belongs to another cache or is empty");
+    return m_->manager.length(id);
+  }
+  std::uint64_t fork(std::uint64_t id, std::size_t tokens) override {
+    std::scoped_lock lock(m_->mutex);
+    return m_->manager.commit_fork(m_->manager.plan_fork(id, tokens, false));
+  }
+  void release(std::uint64_t id) override {
+    std::scoped_lock lock(m_->mutex);
+    m_->manager.release(id);
+  }
+
+private:
+  helix_block_manager* m_;
+};
+
+class DeviceAnchors final : public helix::AnchorPool {
+public:
+  explicit DeviceAnchors(std::shared_ptr<helix::CacheState> s) : s_(std::move(s)) {}
+  std::size_t block_tokens() const override { return s_->manager.config().block_tokens; }
+  std::uint64_t cache_id() const override { return s_->manager.cache_id(); }
+  std::size_t length(std::uint64_t id, std::uint64_t cache_id) override {
+    std::scoped_lock lock(s_->mutex);
+    s_->require_sequence(id, cache_id, "prefix cache insert");
+    return s_->manager.length(id);
+  }
+  std::uint64_t fork(std::uint64_t id, std::size_t tokens) override {
+    std::scoped_lock lock(s_->mutex);
+    s_->require_healthy("prefix cache fork");
+    return s_->manager.commit_fork(s_->manager.plan_fork(id, tokens, false));
+  }
+  void release(std::uint64_t id) override {
+    std::scoped_lock lock(s_->mutex);
+    s_->manager.release(id);
+  }
+
+private:
+  std::shared_ptr<helix::CacheState> s_;
+};
+
+helix::PrefixCacheConfig to_prefix_config(const helix_prefix_config* c) {
+  check(c != nullptr, Status::kInvalidArgument, "prefix cache config must not be NULL");
+  return helix::PrefixCacheConfig{c->maximum_entries, c->maximum_block_references};
 }
 
 }  // namespace
@@ -994,5 +1060,129 @@ int helix_decode_batch_set_timing_event(helix_decode_batch* b, void* event) {
 }
 
 void helix_decode_batch_destroy(helix_decode_batch* b) { delete b; }
+
+// ------------------------------------------------------------ prefix cache
+
+#define REQUIRE_PREFIXES() \
+  check(prefixes != nullptr, Status::kInvalidArgument, "prefix cache must not be NULL")
+
+int helix_prefix_cache_create(helix_paged_cache* cache, const helix_prefix_config* config,
+                              helix_prefix_cache** out) {
+  return guarded([&] {
+    check(cache != nullptr, Status::kInvalidArgument, "prefix cache: paged cache must not be null");
+    require_out(out);
+    *out = new helix_prefix_cache(std::make_unique<helix::PrefixCache>(
+        std::make_unique<DeviceAnchors>(cache->cache.state()), to_prefix_config(config)));
+  });
+}
+
+int helix_prefix_cache_create_host(helix_block_manager* manager, const helix_prefix_config* config,
+                                   helix_prefix_cache** out) {
+  return guarded([&] {
+    check(manager != nullptr, Status::kInvalidArgument,
+          "prefix cache: paged cache must not be null");
+    require_out(out);
+    *out = new helix_prefix_cache(std::make_unique<helix::PrefixCache>(
+        std::make_unique<ManagerAnchors>(manager), to_prefix_config(config)));
+  });
+}
+
+void helix_prefix_cache_destroy(helix_prefix_cache* prefixes) { delete prefixes; }
+
+int helix_prefix_cache_insert(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                              const uint32_t* tokens, size_t count, helix_sequence source,
+                              int* status) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(status);
+    *status = static_cast<int>(
+        prefixes->index->insert(namespace_id, tokens, count, source.id, source.cache_id));
+  });
+}
+
+int helix_prefix_cache_lookup_longest(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                                      const uint32_t* tokens, size_t count,
+                                      size_t maximum_prefix_tokens, int* hit,
+                                      helix_sequence* sequence, size_t* matched_tokens) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(hit);
+    require_out(sequence);
+    require_out(matched_tokens);
+    std::uint64_t id = 0;
+    std::size_t matched = 0;
+    const bool found = prefixes->index->lookup_longest(namespace_id, tokens, count,
+                                                       maximum_prefix_tokens, &id, &matched);
+    *hit = found ? 1 : 0;
+    *sequence = found ? helix_sequence{id, prefixes->index->cache_id()} : helix_sequence{0, 0};
+    *matched_tokens = matched;
+  });
+}
+
+int helix_prefix_cache_contains(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                                const uint32_t* tokens, size_t count, int* out) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(out);
+    *out = prefixes->index->contains(namespace_id, tokens, count) ? 1 : 0;
+  });
+}
+
+int helix_prefix_cache_erase(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                             const uint32_t* tokens, size_t count, int* erased) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(erased);
+    *erased = prefixes->index->erase(namespace_id, tokens, count) ? 1 : 0;
+  });
+}
+
+int helix_prefix_cache_evict_lru(helix_prefix_cache* prefixes, int* evicted) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(evicted);
+    *evicted = prefixes->index->evict_lru() ? 1 : 0;
+  });
+}
+
+int helix_prefix_cache_clear(helix_prefix_cache* prefixes) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    prefixes->index->clear();
+  });
+}
+
+int helix_prefix_cache_stats(helix_prefix_cache* prefixes, helix_prefix_stats* out) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(out);
+    const helix::PrefixStats s = prefixes->index->stats();
+    *out = helix_prefix_stats{s.maximum_entries,       s.maximum_block_references,
+                              s.entry_count,           s.retained_tokens,
+                              s.retained_block_references, s.peak_entries,
+                              s.peak_block_references, s.lookup_count,
+                              s.hit_count,             s.miss_count,
+                              s.insertion_count,       s.duplicate_insertion_count,
+                              s.rejected_insertion_count, s.eviction_count,
+                              s.erase_count};
+  });
+}
+
+int helix_prefix_cache_config(helix_prefix_cache* prefixes, helix_prefix_config* out) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(out);
+    const helix::PrefixCacheConfig& c = prefixes->index->config();
+    *out = helix_prefix_config{c.maximum_entries, c.maximum_block_references};
+  });
+}
+
+int helix_prefix_cache_block_tokens(helix_prefix_cache* prefixes, size_t* out) {
+  return guarded([&] {
+    REQUIRE_PREFIXES();
+    require_out(out);
+    *out = prefixes->index->block_tokens();
+  });
+}
 
 }  // extern "C"

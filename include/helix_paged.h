@@ -332,6 +332,68 @@ int helix_decode_batch_shared_pages(const helix_decode_batch* b, size_t* out);
 int helix_decode_batch_set_timing_event(helix_decode_batch* b, void* event);
 void helix_decode_batch_destroy(helix_decode_batch* b);
 
+/* ------------------------------------------------------ prefix cache ---- */
+/* PagedPrefixCache (include/helix/kv_cache/prefix.hpp:66-112,
+ * src/kv_cache/prefix.cpp): a bounded index from (namespace, exact token
+ * IDs of a block-aligned prefix) to an anchor sequence the index owns in
+ * the pool.  Namespace 0 is invalid.  Public calls take the index lock, then
+ * the pool's (prefix.hpp:62-63). */
+typedef struct helix_prefix_cache helix_prefix_cache;
+
+/* PagedPrefixCacheConfig (prefix.hpp:34-37). */
+typedef struct helix_prefix_config {
+  size_t maximum_entries;
+  size_t maximum_block_references;
+} helix_prefix_config;
+
+/* PrefixInsertStatus (prefix.hpp:39-43). */
+typedef enum helix_prefix_insert_status {
+  HELIX_PREFIX_INSERTED = 0,
+  HELIX_PREFIX_ALREADY_PRESENT = 1,
+  HELIX_PREFIX_REJECTED_TOO_LARGE = 2
+} helix_prefix_insert_status;
+
+/* PagedPrefixCacheStats (prefix.hpp:47-63), 64-bit. */
+typedef struct helix_prefix_stats {
+  uint64_t maximum_entries, maximum_block_references, entry_count, retained_tokens;
+  uint64_t retained_block_references, peak_entries, peak_block_references;
+  uint64_t lookup_count, hit_count, miss_count, insertion_count, duplicate_insertion_count;
+  uint64_t rejected_insertion_count, eviction_count, erase_count;
+} helix_prefix_stats;
+
+/* PagedPrefixCache::PagedPrefixCache (prefix.cpp:124-139, 270-275) over the
+ * device cache's pool; the index keeps the pool alive until destroyed. */
+int helix_prefix_cache_create(helix_paged_cache* cache, const helix_prefix_config* config,
+                              helix_prefix_cache** out);
+/* The same index over host page bookkeeping only (no device memory); the
+ * manager must outlive the index. */
+int helix_prefix_cache_create_host(helix_block_manager* manager, const helix_prefix_config* config,
+                                   helix_prefix_cache** out);
+/* ~PagedPrefixCache (prefix.cpp:277-287): releases every retained anchor. */
+void helix_prefix_cache_destroy(helix_prefix_cache* prefixes);
+/* PagedPrefixCache::insert (prefix.cpp:296-358); *status is a
+ * helix_prefix_insert_status. */
+int helix_prefix_cache_insert(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                              const uint32_t* tokens, size_t count, helix_sequence source,
+                              int* status);
+/* PagedPrefixCache::lookup_longest (prefix.cpp:360-403): *hit = 1 and a new
+ * sequence the caller must release, or *hit = 0. */
+int helix_prefix_cache_lookup_longest(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                                      const uint32_t* tokens, size_t count,
+                                      size_t maximum_prefix_tokens, int* hit,
+                                      helix_sequence* sequence, size_t* matched_tokens);
+/* contains / erase / evict_lru / clear (prefix.cpp:405-446). */
+int helix_prefix_cache_contains(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                                const uint32_t* tokens, size_t count, int* out);
+int helix_prefix_cache_erase(helix_prefix_cache* prefixes, uint64_t namespace_id,
+                             const uint32_t* tokens, size_t count, int* erased);
+int helix_prefix_cache_evict_lru(helix_prefix_cache* prefixes, int* evicted);
+int helix_prefix_cache_clear(helix_prefix_cache* prefixes);
+/* stats / config / block_tokens (prefix.cpp:448-463). */
+int helix_prefix_cache_stats(helix_prefix_cache* prefixes, helix_prefix_stats* out);
+int helix_prefix_cache_config(helix_prefix_cache* prefixes, helix_prefix_config* out);
+int helix_prefix_cache_block_tokens(helix_prefix_cache* prefixes, size_t* out);
+
 /* ------------------------------------------------------- measurement ---- */
 /* Streaming-read probe (no reference counterpart): reads n_floats floats
  * with 128-bit loads using `blocks` workgroups of 256 threads and writes one
