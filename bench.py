@@ -35,6 +35,9 @@ import helix_runtime_amd as hx  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 LAYERS, HQ, HKV, D, P, BATCH = 32, 32, 8, 128, 16, 64
+# Page element type (--page-dtype): "f32" is the reference's format and the
+# headline; "bf16" is the reduced-precision extension.
+PAGE_DTYPE, PAGE_BYTES = "f32", 4
 
 
 def log(msg):
@@ -46,13 +49,19 @@ def decode_bytes(lengths, hq=HQ, hkv=HKV, d=D, p=P):
     sum over sequences of K+V history (each byte once per KV head), the K/V
     tail, Q in and O out, and the block-table entries."""
     lengths = np.asarray(lengths, np.int64)
-    return int(np.sum(2 * hkv * lengths * d * 4 + 2 * hkv * d * 4 + 2 * hq * d * 4 +
+    return int(np.sum(2 * hkv * lengths * d * PAGE_BYTES + 2 * hkv * d * 4 + 2 * hq * d * 4 +
                       ((lengths + p - 1) // p) * 4))
 
 
 def append_bytes(batch, hkv=HKV, d=D):
-    """Read source + write page, keys and values, one token per sequence."""
-    return 2 * 2 * hkv * d * 4 * batch
+    """Read the fp32 source row + write the page row, keys and values, one
+    token per sequence."""
+    return 2 * hkv * d * (4 + PAGE_BYTES) * batch
+
+
+def append_write_bytes(batch, hkv=HKV, d=D):
+    """The page writes of append_bytes alone."""
+    return 2 * hkv * d * PAGE_BYTES * batch
 
 
 def build_workload(seed, batch, layers, steps_total, shuffle=True):
@@ -61,8 +70,9 @@ def build_workload(seed, batch, layers, steps_total, shuffle=True):
     pages = (lengths + P - 1) // P
     grow = (steps_total + P) // P + 1
     n_phys = int(pages.sum() + batch * grow + 16)
-    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys)
-    log(f"pool: {n_phys} blocks x {layers} layers ({n_phys * layers * 2 * HKV * P * D * 4 / 1e9:.1f} GB)")
+    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys, page_dtype=PAGE_DTYPE)
+    log(f"pool: {n_phys} blocks x {layers} layers "
+        f"({n_phys * layers * 2 * HKV * P * D * PAGE_BYTES / 1e9:.1f} GB)")
     # Shuffle the free queue: allocate every block once, release in a seeded
     # random order, so later allocations scatter each sequence over the pool.
     tok = torch.zeros(layers, HKV, D, device="cuda:0")
@@ -106,8 +116,9 @@ def build_prefix_workload(seed, layers, steps_total):
     suffix = rng.integers(64, 513, size=PREFIX_BATCH)
     own_pages = (PREFIX_PARTIAL + suffix + steps_total + P - 1) // P + 1
     n_phys = int(root_len // P + 1 + own_pages.sum() + 16)
-    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys)
-    log(f"pool: {n_phys} blocks x {layers} layers ({n_phys * layers * 2 * HKV * P * D * 4 / 1e9:.1f} GB)")
+    cache = hx.PagedKvCache(layers, HKV, D, P, n_phys, page_dtype=PAGE_DTYPE)
+    log(f"pool: {n_phys} blocks x {layers} layers "
+        f"({n_phys * layers * 2 * HKV * P * D * PAGE_BYTES / 1e9:.1f} GB)")
     tok = torch.zeros(layers, HKV, D, device="cuda:0")
     dummies = []
     for _ in range(n_phys):
@@ -147,8 +158,8 @@ def unique_decode_bytes(lengths, shared_tokens=PREFIX_TOKENS, hq=HQ, hkv=HKV, d=
     is read from HBM once: the logical formula with the shared tokens counted
     once instead of once per sequence."""
     lengths = np.asarray(lengths, np.int64)
-    shared = 2 * hkv * shared_tokens * d * 4
-    own = 2 * hkv * (lengths - shared_tokens) * d * 4
+    shared = 2 * hkv * shared_tokens * d * PAGE_BYTES
+    own = 2 * hkv * (lengths - shared_tokens) * d * PAGE_BYTES
     return int(shared + np.sum(own + 2 * hkv * d * 4 + 2 * hq * d * 4 +
                                ((lengths + p - 1) // p) * 4))
 
@@ -267,8 +278,8 @@ def run_prefill(args):
     hists = rng.integers(0, 4097, size=CHUNK_BATCH)
     T = CHUNK_TOKENS
     n_phys = int(((hists + T + P - 1) // P).sum() + CHUNK_BATCH + 16)
-    cache = hx.PagedKvCache(L, HKV, D, P, n_phys)
-    log(f"pool: {n_phys} blocks x {L} layers ({n_phys * L * 2 * HKV * P * D * 4 / 1e9:.1f} GB)")
+    cache = hx.PagedKvCache(L, HKV, D, P, n_phys, page_dtype=PAGE_DTYPE)
+    log(f"pool: {n_phys} blocks x {L} layers ({n_phys * L * 2 * HKV * P * D * PAGE_BYTES / 1e9:.1f} GB)")
     tok = torch.zeros(L, HKV, D, device="cuda:0")
     dummies = []
     for _ in range(n_phys):
@@ -329,11 +340,11 @@ def run_prefill(args):
     flops = prefill_flops(hists)
     attn_avg = float(np.mean(attn_ms))
     tflops = flops / (attn_avg * 1e-3) / 1e12
-    chunk_bytes = 2 * 2 * CHUNK_BATCH * HKV * T * D * 4
+    chunk_bytes = 2 * CHUNK_BATCH * HKV * T * D * (4 + PAGE_BYTES)
     append_gbps = chunk_bytes / (float(np.mean(append_ms)) * 1e-3) / 1e9
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and PAGE_DTYPE == "f32":
         # Bounded sample: layer 0 of the first `cpu_seqs` sequences, one
         # thread per sequence, checked against the GPU output of that layer.
         nseq = min(args.cpu_seqs, CHUNK_BATCH)
@@ -369,8 +380,11 @@ def run_prefill(args):
                          f"{nseq} of {CHUNK_BATCH} sequences, one thread each, {secs:.1f} s; "
                          f"GPU matched it to max abs err {err:.2e}"}
         del kp, vp, mb
+    metric = "chunked-prefill attention TFLOP/s (fp32 MFMA), 8B-GQA 16 x 512-token chunks"
+    if PAGE_DTYPE != "f32":
+        metric += f" [{PAGE_DTYPE} pages]"
     line = {
-        "metric": "chunked-prefill attention TFLOP/s (fp32 MFMA), 8B-GQA 16 x 512-token chunks",
+        "metric": metric,
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -386,7 +400,7 @@ def run_prefill(args):
                                "history U[0, 4096], 32q/8kv heads, head_dim 128, page 16",
                    "batch": CHUNK_BATCH, "chunk_tokens": T, "layers": L, "q_heads": HQ,
                    "kv_heads": HKV, "head_dim": D, "block_tokens": P,
-                   "mean_history": float(hists.mean())},
+                   "mean_history": float(hists.mean()), "page_dtype": PAGE_DTYPE},
         "prefill_avg_us": round(attn_avg * 1e3, 2),
         "prefill_median_us": round(float(np.median(attn_ms)) * 1e3, 2),
         "append_gbps": round(append_gbps, 2),
@@ -425,6 +439,9 @@ def main():
                          "4: prefix-sharing decode; 5: chunked prefill on the matrix cores")
     ap.add_argument("--cpu-seqs", type=int, default=4,
                     help="config 5: sequences of layer 0 timed on the CPU oracle")
+    ap.add_argument("--page-dtype", default="f32", choices=("f32", "bf16"),
+                    help="page element type (bf16: the reduced-precision extension; the CPU "
+                         "baseline is reported for f32 pages only)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM probe / counter calibration)")
     args = ap.parse_args()
@@ -435,6 +452,8 @@ def main():
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    global PAGE_DTYPE, PAGE_BYTES
+    PAGE_DTYPE, PAGE_BYTES = args.page_dtype, (2 if args.page_dtype == "bf16" else 4)
     torch.cuda.set_device(0)
     if args.copy_probe:
         copy_probe()
@@ -532,8 +551,8 @@ def main():
         roof_bytes = launch_bytes
     if fused:
         # The decode kernel also writes the new token rows into their pages.
-        roof_bytes += append_bytes(nseq) / 2
-        launch_bytes += append_bytes(nseq) / 2
+        roof_bytes += append_write_bytes(nseq)
+        launch_bytes += append_write_bytes(nseq)
     step_decode = roof_bytes * L
     # Fused: the append's writes are in roof_bytes and its source rows are the
     # attention tail, already counted there.
@@ -554,13 +573,14 @@ def main():
     append_gbps = append_bytes(nseq) / (append_avg_ms * 1e-3) / 1e9
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"decode_config{args.config}_traffic.json")
+    suffix = "" if PAGE_DTYPE == "f32" else f"_{PAGE_DTYPE}"
+    tpath = os.path.join(ROOT, "profiles", f"decode_config{args.config}{suffix}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and PAGE_DTYPE == "f32":
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         rate, err = cpu_baseline(cache, seqs, args.cpu_layers, args.cpu_single_layers, threads,
                                  args.seed)
@@ -591,6 +611,9 @@ def main():
                     "batch": nseq, "layers": L, "q_heads": HQ, "kv_heads": HKV,
                     "head_dim": D, "block_tokens": P, "mean_context": float(lengths0.mean()),
                     "pages_per_split": split}
+    if PAGE_DTYPE != "f32":
+        metric += f" [{PAGE_DTYPE} pages]"
+        workload["page_dtype"] = PAGE_DTYPE
     line = {
         "metric": metric,
         "value": round(value, 2),

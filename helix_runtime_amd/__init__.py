@@ -141,6 +141,8 @@ class BlockManager:
         return a.value, b.value, c.value
 
 
+PAGE_DTYPES = {"f32": 0, "bf16": 1}
+
 # ---------------------------------------------------------- prefix cache ----
 PREFIX_INSERTED, PREFIX_ALREADY_PRESENT, PREFIX_REJECTED_TOO_LARGE = 0, 1, 2
 
@@ -238,11 +240,17 @@ class PagedKvCache:
     """GPU paged KV pool (CudaPagedKvCache + the CPU cache's fork/bulk append)."""
 
     def __init__(self, layers, kv_heads, head_dimension, block_tokens, physical_blocks,
-                 device=0):
+                 device=0, page_dtype="f32"):
+        """``page_dtype`` "bf16" stores pages as bf16 (extension: appended
+        fp32 rows rounded to nearest even, gathers widen back to fp32)."""
         h = ctypes.c_void_p()
         cfg = _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
-        check(_lib().helix_paged_cache_create(ctypes.byref(cfg), device, ctypes.byref(h)))
+        if page_dtype not in PAGE_DTYPES:
+            raise HelixError(INVALID_ARGUMENT, f"page_dtype must be one of {sorted(PAGE_DTYPES)}")
+        check(_lib().helix_paged_cache_create_typed(ctypes.byref(cfg), device,
+                                                    PAGE_DTYPES[page_dtype], ctypes.byref(h)))
         self._h = h
+        self.page_dtype = page_dtype
         self.layers, self.kv_heads, self.head_dimension = layers, kv_heads, head_dimension
         self.block_tokens, self.physical_blocks, self.device = block_tokens, physical_blocks, device
 
@@ -353,14 +361,16 @@ class PagedKvCache:
         return k.value, v.value
 
     def layer_pools(self, layer):
-        """Device copies of layer `layer`'s pools [physical, kv_heads, block_tokens, dim]."""
+        """Device copies of layer `layer`'s pools [physical, kv_heads, block_tokens, dim]
+        (float32, or bfloat16 for a bf16 cache)."""
         import torch
         kp, vp = self.layer_pool_pointers(layer)
         shape = (self.physical_blocks, self.kv_heads, self.block_tokens, self.head_dimension)
+        dtype = torch.bfloat16 if self.page_dtype == "bf16" else torch.float32
         out = []
         for p in (kp, vp):
-            t = torch.empty(shape, dtype=torch.float32, device=f"cuda:{self.device}")
-            device_copy(t.data_ptr(), p, t.numel() * 4)
+            t = torch.empty(shape, dtype=dtype, device=f"cuda:{self.device}")
+            device_copy(t.data_ptr(), p, t.numel() * t.element_size())
             out.append(t)
         return out[0], out[1]
 

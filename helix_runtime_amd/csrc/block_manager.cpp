@@ -30,7 +30,10 @@ std::size_t blocks_for(std::size_t tokens, std::size_t block_tokens) {
 
 // Pool geometry checks and byte formulas of make_layout
 // (src/kv_cache/paged.cpp:53-106).
-BlockManager::BlockManager(const PagedConfig& config) : config_(config) {
+BlockManager::BlockManager(const PagedConfig& config, std::size_t element_bytes)
+    : config_(config) {
+  check(element_bytes == 4 || element_bytes == 2, Status::kInvalidArgument,
+        "paged KV cache page elements are 4 (fp32) or 2 (bf16) bytes");
   check(config.layers != 0, Status::kInvalidArgument, "paged KV cache layer count must be positive");
   check(config.kv_heads != 0, Status::kInvalidArgument, "paged KV cache head count must be positive");
   check(config.head_dimension != 0, Status::kInvalidArgument,
@@ -44,7 +47,7 @@ BlockManager::BlockManager(const PagedConfig& config) : config_(config) {
   std::size_t token_elems = checked_mul(config.layers, 2, "bytes per token");
   token_elems = checked_mul(token_elems, config.kv_heads, "bytes per token");
   token_elems = checked_mul(token_elems, config.head_dimension, "bytes per token");
-  bytes_per_token_ = checked_mul(token_elems, sizeof(float), "bytes per token");
+  bytes_per_token_ = checked_mul(token_elems, element_bytes, "bytes per token");
   block_bytes_ = checked_mul(bytes_per_token_, config.block_tokens, "block bytes");
   const std::size_t pool = checked_mul(block_bytes_, config.physical_blocks, "pool bytes");
   static_cast<void>(checked_mul(config.physical_blocks, config.block_tokens, "token capacity"));

@@ -83,7 +83,9 @@ struct ForkPlan {
 
 class BlockManager {
 public:
-  explicit BlockManager(const PagedConfig& config);
+  // element_bytes: 4 for fp32 pages (the reference's), 2 for bf16 pages;
+  // it scales the byte figures of the geometry and statistics only.
+  explicit BlockManager(const PagedConfig& config, std::size_t element_bytes = 4);
 
   [[nodiscard]] const PagedConfig& config() const noexcept { return config_; }
   [[nodiscard]] std::uint64_t cache_id() const noexcept { return cache_id_; }

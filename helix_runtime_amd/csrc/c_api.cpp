@@ -28,7 +28,9 @@ struct helix_block_manager {
 };
 
 struct helix_paged_cache {
-  helix_paged_cache(const helix::PagedConfig& c, int device) : cache(c, device) {}
+  helix_paged_cache(const helix::PagedConfig& c, int device,
+                    helix::hip::PageType type = helix::hip::PageType::kF32)
+      : cache(c, device, type) {}
   helix::DevicePagedCache cache;
 };
 
@@ -374,9 +376,30 @@ int helix_paged_cache_create(const helix_paged_config* config, int device,
   });
 }
 
+int helix_paged_cache_create_typed(const helix_paged_config* config, int device, int page_dtype,
+                                   helix_paged_cache** out) {
+  return guarded([&] {
+    require_out(out);
+    *out = nullptr;
+    check(page_dtype == HELIX_PAGE_F32 || page_dtype == HELIX_PAGE_BF16,
+          Status::kInvalidArgument, "page dtype must be HELIX_PAGE_F32 or HELIX_PAGE_BF16");
+    *out = new helix_paged_cache(to_config(config), device,
+                                 page_dtype == HELIX_PAGE_BF16 ? helix::hip::PageType::kBF16
+                                                               : helix::hip::PageType::kF32);
+  });
+}
+
 void helix_paged_cache_destroy(helix_paged_cache* cache) { delete cache; }
 
 #define REQUIRE_CACHE() check(cache != nullptr, Status::kInvalidArgument, "cache must not be NULL")
+
+int helix_paged_cache_page_dtype(helix_paged_cache* cache, int* out) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(out);
+    *out = cache->cache.state()->bf16() ? HELIX_PAGE_BF16 : HELIX_PAGE_F32;
+  });
+}
 
 int helix_paged_cache_create_sequence(helix_paged_cache* cache, helix_sequence* out) {
   return guarded([&] {

@@ -8,11 +8,14 @@
 // in one allocation (see paged_cache.cpp).
 #include "kernels.hpp"
 
+#include "bf16.hpp"
+
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdint>
 #include <limits>
+#include <type_traits>
 
 namespace helix::hip {
 namespace {
@@ -26,45 +29,75 @@ inline unsigned grid_for(std::size_t work, std::size_t per_block, std::size_t ca
   return static_cast<unsigned>(blocks < cap ? blocks : cap);
 }
 
-template <typename T>
-__device__ __forceinline__ T load_vec(const float* p) {
-  return *reinterpret_cast<const T*>(p);
-}
-template <typename T>
-__device__ __forceinline__ void store_vec(float* p, const T& v) {
-  *reinterpret_cast<T*>(p) = v;
-}
-template <typename T>
-constexpr int vec_width() {
-  return sizeof(T) / sizeof(float);
-}
+// --------------------------------------------------------- page elements ----
+// Pages hold fp32 (the reference's format) or bf16 (bf16.hpp).  Rows passed
+// in and gather outputs are fp32 either way.
+// W consecutive elements between fp32 rows and pages of element type S.
+template <typename S, int W>
+struct Elems;
+template <int W>
+struct Elems<float, W> {
+  static __device__ __forceinline__ void put(float* dst, const float* src) {
+    if constexpr (W == 4) {
+      *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+  static __device__ __forceinline__ void get(float* dst, const float* src) { put(dst, src); }
+  static __device__ __forceinline__ void copy(float* dst, const float* src) { put(dst, src); }
+};
+template <int W>
+struct Elems<unsigned short, W> {
+  static __device__ __forceinline__ void put(unsigned short* dst, const float* src) {
+    if constexpr (W == 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src);
+      *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pack(v.x, v.y), bf16_pack(v.z, v.w));
+    } else {
+      *dst = bf16_round(*src);
+    }
+  }
+  static __device__ __forceinline__ void get(float* dst, const unsigned short* src) {
+    if constexpr (W == 4) {
+      const uint2 p = *reinterpret_cast<const uint2*>(src);
+      *reinterpret_cast<float4*>(dst) = bf16_widen(p.x, p.y);
+    } else {
+      *dst = bf16_value(*src);
+    }
+  }
+  static __device__ __forceinline__ void copy(unsigned short* dst, const unsigned short* src) {
+    if constexpr (W == 4) {
+      *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+};
 
 // ------------------------------------------------------------- append ----
 // Reference: CudaPagedKvCache::append issues 2 * layers * kv_heads
 // cudaMemcpyAsync D2D copies of one head vector (src/kv_cache/cuda_paged.cpp:
 // 561-577).  Here one launch moves every (layer, head) vector of K and V with
 // 128-bit accesses; blockIdx.y selects keys (0) or values (1).
-template <typename V>
+template <typename S, int W>
 __global__ void append_token_kernel(const float* __restrict__ keys,
-                                    const float* __restrict__ values, float* key_base,
-                                    float* value_base, std::size_t layer_stride,
-                                    std::size_t layers, std::size_t heads, std::size_t block_tokens,
-                                    std::size_t dim, std::uint32_t block, std::size_t offset) {
-  constexpr int W = vec_width<V>();
+                                    const float* __restrict__ values, S* key_base, S* value_base,
+                                    std::size_t layer_stride, std::size_t layers,
+                                    std::size_t heads, std::size_t block_tokens, std::size_t dim,
+                                    std::uint32_t block, std::size_t offset) {
   const std::size_t dv = dim / W;
   const std::size_t total = layers * heads * dv;
   const float* src = blockIdx.y == 0 ? keys : values;
-  float* base = blockIdx.y == 0 ? key_base : value_base;
+  S* base = blockIdx.y == 0 ? key_base : value_base;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t c = e % dv;
     const std::size_t lh = e / dv;
     const std::size_t h = lh % heads;
     const std::size_t l = lh / heads;
-    float* dst = base + l * layer_stride +
-                 ((static_cast<std::size_t>(block) * heads + h) * block_tokens + offset) * dim +
-                 c * W;
-    store_vec<V>(dst, load_vec<V>(src + e * W));
+    S* dst = base + l * layer_stride +
+             ((static_cast<std::size_t>(block) * heads + h) * block_tokens + offset) * dim + c * W;
+    Elems<S, W>::put(dst, src + e * W);
   }
 }
 
@@ -75,18 +108,17 @@ struct LayerPointers {
   const float* const* values;
 };
 
-template <typename V>
-__global__ void append_bulk_kernel(LayerPointers src, float* key_base, float* value_base,
+template <typename S, int W>
+__global__ void append_bulk_kernel(LayerPointers src, S* key_base, S* value_base,
                                    std::size_t layer_stride, std::size_t layers,
                                    std::size_t heads, std::size_t block_tokens, std::size_t dim,
                                    const std::uint32_t* __restrict__ blocks,
                                    std::size_t first_block, std::size_t old_length,
                                    std::size_t tokens) {
-  constexpr int W = vec_width<V>();
   const std::size_t dv = dim / W;
   const std::size_t per_layer = heads * tokens * dv;
   const std::size_t total = layers * per_layer;
-  float* base = blockIdx.y == 0 ? key_base : value_base;
+  S* base = blockIdx.y == 0 ? key_base : value_base;
   const float* const* layer_src = blockIdx.y == 0 ? src.keys : src.values;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
@@ -98,9 +130,9 @@ __global__ void append_bulk_kernel(LayerPointers src, float* key_base, float* va
     const std::size_t h = ht / tokens;
     const std::size_t pos = old_length + t;
     const std::size_t phys = blocks[pos / block_tokens - first_block];
-    float* dst = base + l * layer_stride +
-                 ((phys * heads + h) * block_tokens + pos % block_tokens) * dim + c * W;
-    store_vec<V>(dst, load_vec<V>(layer_src[l] + r * W));
+    S* dst = base + l * layer_stride +
+             ((phys * heads + h) * block_tokens + pos % block_tokens) * dim + c * W;
+    Elems<S, W>::put(dst, layer_src[l] + r * W);
   }
 }
 
@@ -108,17 +140,16 @@ __global__ void append_bulk_kernel(LayerPointers src, float* key_base, float* va
 // [batch, heads, tokens, dim] (tokens = 1 for a decode step, the chunk
 // length for chunked prefill); token t of sequence b goes to physical slot
 // slots[b * tokens + t] = block * block_tokens + offset (negative: skipped).
-template <typename V>
+template <typename S, int W>
 __global__ void append_slots_kernel(const float* __restrict__ keys,
-                                    const float* __restrict__ values, float* key_pool,
-                                    float* value_pool, std::size_t heads, std::size_t block_tokens,
-                                    std::size_t dim, const std::int64_t* __restrict__ slots,
-                                    std::size_t count, std::size_t tokens) {
-  constexpr int W = vec_width<V>();
+                                    const float* __restrict__ values, S* key_pool, S* value_pool,
+                                    std::size_t heads, std::size_t block_tokens, std::size_t dim,
+                                    const std::int64_t* __restrict__ slots, std::size_t count,
+                                    std::size_t tokens) {
   const std::size_t dv = dim / W;
   const std::size_t total = count * heads * tokens * dv;
   const float* src = blockIdx.y == 0 ? keys : values;
-  float* pool = blockIdx.y == 0 ? key_pool : value_pool;
+  S* pool = blockIdx.y == 0 ? key_pool : value_pool;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t c = e % dv;
@@ -131,23 +162,20 @@ __global__ void append_slots_kernel(const float* __restrict__ keys,
     if (slot < 0) continue;
     const std::size_t block = static_cast<std::size_t>(slot) / block_tokens;
     const std::size_t off = static_cast<std::size_t>(slot) % block_tokens;
-    store_vec<V>(pool + ((block * heads + h) * block_tokens + off) * dim + c * W,
-                 load_vec<V>(src + e * W));
+    Elems<S, W>::put(pool + ((block * heads + h) * block_tokens + off) * dim + c * W, src + e * W);
   }
 }
 
 // Reference: PagedKvCache copy_layer / copy_layer_prefix_out
 // (src/kv_cache/paged.cpp:242-280, 895-950).
-template <typename V>
-__global__ void gather_kernel(const float* __restrict__ key_pool,
-                              const float* __restrict__ value_pool, std::size_t heads,
-                              std::size_t block_tokens, std::size_t dim,
+template <typename S, int W>
+__global__ void gather_kernel(const S* __restrict__ key_pool, const S* __restrict__ value_pool,
+                              std::size_t heads, std::size_t block_tokens, std::size_t dim,
                               const std::uint32_t* __restrict__ blocks, std::size_t length,
                               float* keys_out, float* values_out, std::size_t dest_tokens) {
-  constexpr int W = vec_width<V>();
   const std::size_t dv = dim / W;
   const std::size_t total = heads * length * dv;
-  const float* pool = blockIdx.y == 0 ? key_pool : value_pool;
+  const S* pool = blockIdx.y == 0 ? key_pool : value_pool;
   float* out = blockIdx.y == 0 ? keys_out : values_out;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
@@ -156,22 +184,20 @@ __global__ void gather_kernel(const float* __restrict__ key_pool,
     const std::size_t t = ht % length;
     const std::size_t h = ht / length;
     const std::size_t phys = blocks[t / block_tokens];
-    store_vec<V>(out + (h * dest_tokens + t) * dim + c * W,
-                 load_vec<V>(pool + ((phys * heads + h) * block_tokens + t % block_tokens) * dim +
-                             c * W));
+    Elems<S, W>::get(out + (h * dest_tokens + t) * dim + c * W,
+                     pool + ((phys * heads + h) * block_tokens + t % block_tokens) * dim + c * W);
   }
 }
 
-template <typename V>
-__global__ void page_copy_kernel(float* key_base, float* value_base, std::size_t layer_stride,
+template <typename S, int W>
+__global__ void page_copy_kernel(S* key_base, S* value_base, std::size_t layer_stride,
                                  std::size_t layers, std::size_t heads, std::size_t block_tokens,
                                  std::size_t dim, std::uint32_t from, std::uint32_t to,
                                  std::size_t tokens) {
-  constexpr int W = vec_width<V>();
   const std::size_t dv = dim / W;
   const std::size_t run = tokens * dv;  // contiguous prefix of one (block, head) page
   const std::size_t total = layers * heads * run;
-  float* base = blockIdx.y == 0 ? key_base : value_base;
+  S* base = blockIdx.y == 0 ? key_base : value_base;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t i = e % run;
@@ -179,9 +205,9 @@ __global__ void page_copy_kernel(float* key_base, float* value_base, std::size_t
     const std::size_t h = lh % heads;
     const std::size_t l = lh / heads;
     const std::size_t page = block_tokens * dim;
-    float* layer = base + l * layer_stride;
-    store_vec<V>(layer + (static_cast<std::size_t>(to) * heads + h) * page + i * W,
-                 load_vec<V>(layer + (static_cast<std::size_t>(from) * heads + h) * page + i * W));
+    S* layer = base + l * layer_stride;
+    Elems<S, W>::copy(layer + (static_cast<std::size_t>(to) * heads + h) * page + i * W,
+                      layer + (static_cast<std::size_t>(from) * heads + h) * page + i * W);
   }
 }
 
@@ -218,6 +244,9 @@ __device__ __forceinline__ float4 as_float4(u32x4 v) {
   return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                      __uint_as_float(v[3]));
 }
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 as_uint2(u32x2 v) { return make_uint2(v[0], v[1]); }
+
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -758,7 +787,10 @@ struct PageDesc {
   bool skip;
 };
 
-template <int G, bool APPEND>
+// BF16: pages hold bf16 (4 per 64-bit lane load) and are widened to fp32 in
+// registers.  The fp32 tail row is rounded to bf16 as it is read (it is the
+// value the page will hold once appended).
+template <int G, bool APPEND, bool BF16>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
 void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
@@ -888,16 +920,16 @@ void decode_stream_kernel(
   // arithmetic is needed.  The first page of a unit in this wavefront also
   // brings the unit's query rows, issued ahead of the page so that waiting
   // for the page covers them.
-  const int lane_off = lane * 16;
+  const int lane_off = lane * (BF16 ? 8 : 16);
   const int row_off = j * 16;
-  auto load_page = [&](const PageDesc& d, float4 (&k)[8], float4 (&v)[8], float4 (&q)[G],
-                       bool& bad) {
+  using Raw = std::conditional_t<BF16, uint2, float4>;
+  auto load_page = [&](const PageDesc& d, Raw (&k)[8], Raw (&v)[8], float4 (&q)[G], bool& bad) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
     const int kvh = __builtin_amdgcn_readfirstlane(d.kvh);
     const int p = __builtin_amdgcn_readfirstlane(d.p);
     const bool tail = p == __builtin_amdgcn_readfirstlane(d.np) - 1;
-    const float* kb;
-    const float* vb;
+    const void* kb;
+    const void* vb;
     bad = d.hist < 0;
     if (tail) {
       const std::size_t row = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * D;
@@ -911,8 +943,13 @@ void decode_stream_kernel(
         phys = 0;
       }
       const std::size_t off = (static_cast<std::size_t>(phys) * a.kv_heads + kvh) * page_elems;
-      kb = a.key_pool + off;
-      vb = a.value_pool + off;
+      if constexpr (BF16) {
+        kb = reinterpret_cast<const unsigned short*>(a.key_pool) + off;
+        vb = reinterpret_cast<const unsigned short*>(a.value_pool) + off;
+      } else {
+        kb = a.key_pool + off;
+        vb = a.value_pool + off;
+      }
     }
     if (p == 0 || d.g == g0) {
       const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
@@ -921,16 +958,60 @@ void decode_stream_kernel(
 #pragma unroll
       for (int h = 0; h < G; ++h) q[h] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(qr, row_off, h * D * 4, 0));
     }
-    const int voff = tail ? row_off : lane_off;
-    const int step = tail ? 0 : 1024;
+    const int bytes = BF16 ? (tail ? D * 4 : P * D * 2) : P * D * 4;
     const __amdgpu_buffer_rsrc_t kr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb), 0, P * D * 4, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kb), 0, bytes, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vb), 0, P * D * 4, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vb), 0, bytes, kBufferWord3);
+    if constexpr (BF16) {
+      if (tail) {
+        // The fp32 row's 4 dims of this lane: two 64-bit halves in slots 0, 1.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) k[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(kr, voff, i * step, 0));
+        for (int i = 0; i < 2; ++i) {
+          k[i] = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(kr, row_off, i * 8, 0));
+          v[i] = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(vr, row_off, i * 8, 0));
+        }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(vr, voff, i * step, 0));
+        for (int i = 2; i < 8; ++i) k[i] = v[i] = make_uint2(0u, 0u);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(kr, lane_off, i * 512, 0));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = as_uint2(__builtin_amdgcn_raw_buffer_load_b64(vr, lane_off, i * 512, 0));
+      }
+    } else {
+      const int voff = tail ? row_off : lane_off;
+      const int step = tail ? 0 : 1024;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) k[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(kr, voff, i * step, 0));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(vr, voff, i * step, 0));
+    }
+  };
+
+  // fp32 view of a loaded page: bf16 pairs widened, the bf16 tail row (fp32
+  // in slots 0, 1) rounded to bf16 and copied to every slot.
+  auto widen = [&](const Raw (&k)[8], const Raw (&v)[8], bool tail, float4 (&kf)[8],
+                   float4 (&vf)[8]) {
+    if constexpr (BF16) {
+      if (tail) {
+        const float4 tk = bf16_rounded(make_float4(__uint_as_float(k[0].x), __uint_as_float(k[0].y),
+                                                   __uint_as_float(k[1].x), __uint_as_float(k[1].y)));
+        const float4 tv = bf16_rounded(make_float4(__uint_as_float(v[0].x), __uint_as_float(v[0].y),
+                                                   __uint_as_float(v[1].x), __uint_as_float(v[1].y)));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          kf[i] = tk;
+          vf[i] = tv;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          kf[i] = bf16_widen(k[i].x, k[i].y);
+          vf[i] = bf16_widen(v[i].x, v[i].y);
+        }
+      }
+    }
   };
 
   float acc[G][4];
@@ -1028,8 +1109,18 @@ void decode_stream_kernel(
     for (int r = 0; r < (APPEND ? napp : 0); ++r) {
       const long long dst = s_app_dst[r];
       if (parity == 0 && dst >= 0) {
-        reinterpret_cast<float4*>(a.append_key_pool + dst)[j] = s_app_k[r][j];
-        reinterpret_cast<float4*>(a.append_value_pool + dst)[j] = s_app_v[r][j];
+        if constexpr (BF16) {
+          // Staged values are already bf16-exact: packing does not round.
+          const float4 kk = s_app_k[r][j];
+          const float4 vv = s_app_v[r][j];
+          reinterpret_cast<uint2*>(reinterpret_cast<unsigned short*>(a.append_key_pool) + dst)[j] =
+              make_uint2(bf16_pack(kk.x, kk.y), bf16_pack(kk.z, kk.w));
+          reinterpret_cast<uint2*>(reinterpret_cast<unsigned short*>(a.append_value_pool) + dst)[j] =
+              make_uint2(bf16_pack(vv.x, vv.y), bf16_pack(vv.z, vv.w));
+        } else {
+          reinterpret_cast<float4*>(a.append_key_pool + dst)[j] = s_app_k[r][j];
+          reinterpret_cast<float4*>(a.append_value_pool + dst)[j] = s_app_v[r][j];
+        }
       }
     }
     for (int r = 0; r < nres; ++r) {
@@ -1117,8 +1208,8 @@ void decode_stream_kernel(
   };
 
   float4 qc[G];  // query rows of the unit being processed
-  auto step = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8], const float4 (&qn)[G],
-                  bool bad) {
+  auto step_body = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8],
+                       const float4 (&qn)[G], bool bad) {
     int valid = 0;
     if (!d.skip) {
       valid = d.p == d.np - 1 ? 1 : min(P, d.hist - (d.p + a.first_page) * P);
@@ -1158,8 +1249,19 @@ void decode_stream_kernel(
     process(k, v, qc, valid);
     if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
   };
+  auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad) {
+    if constexpr (BF16) {
+      float4 k[8], v[8];
+      widen(kr, vr, !d.skip && d.p == d.np - 1, k, v);
+      step_body(d, k, v, qn, bad);
+    } else {
+      step_body(d, kr, vr, qn, bad);
+    }
+  };
 
-  float4 ka[8], va[8], kb[8], vb[8];
+  // Two pages in flight, each in its own register buffer (a deeper bf16
+  // pipeline spills: the query rows ride with every buffer).
+  Raw ka[8], va[8], kb[8], vb[8];
   float4 qa[G], qb[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) qa[h] = qb[h] = qc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1393,101 +1495,117 @@ __global__ __launch_bounds__(kThreads) void generic_attention_kernel(GenericArgs
 }  // namespace
 
 // ------------------------------------------------------------ launchers ----
-hipError_t launch_append_token(const float* keys, const float* values, float* key_base,
-                               float* value_base, std::size_t layer_stride, std::size_t layers,
-                               const PageGeometry& g, std::uint32_t block, std::size_t offset,
-                               hipStream_t stream) {
-  const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
-  const std::size_t work = layers * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
-  dim3 grid(grid_for(work, kThreads), 2);
-  if (vec) {
-    append_token_kernel<float4><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_base, value_base, layer_stride, layers, g.kv_heads, g.block_tokens,
-        g.head_dim, block, offset);
+namespace {
+
+using Bf16 = unsigned short;
+
+// Runs body(S*, W) with the page element type of `type` and the widest
+// element group the geometry and the fp32 pointers allow.
+template <typename F>
+hipError_t with_page_type(PageType type, bool vec, F&& body) {
+  if (type == PageType::kBF16) {
+    if (vec) {
+      body(Bf16{}, std::integral_constant<int, 4>{});
+    } else {
+      body(Bf16{}, std::integral_constant<int, 1>{});
+    }
+  } else if (vec) {
+    body(float{}, std::integral_constant<int, 4>{});
   } else {
-    append_token_kernel<float><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_base, value_base, layer_stride, layers, g.kv_heads, g.block_tokens,
-        g.head_dim, block, offset);
+    body(float{}, std::integral_constant<int, 1>{});
   }
   return hipGetLastError();
+}
+
+template <typename S>
+S* as_pages(void* p) {
+  return static_cast<S*>(p);
+}
+template <typename S>
+const S* as_pages(const void* p) {
+  return static_cast<const S*>(p);
+}
+
+}  // namespace
+
+hipError_t launch_append_token(const float* keys, const float* values, void* key_base,
+                               void* value_base, std::size_t layer_stride, std::size_t layers,
+                               const PageGeometry& g, std::uint32_t block, std::size_t offset,
+                               hipStream_t stream, PageType type) {
+  const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
+  const std::size_t work = layers * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
+  const dim3 grid(grid_for(work, kThreads), 2);
+  return with_page_type(type, vec, [&](auto s, auto w) {
+    using S = decltype(s);
+    append_token_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
+        keys, values, as_pages<S>(key_base), as_pages<S>(value_base), layer_stride, layers,
+        g.kv_heads, g.block_tokens, g.head_dim, block, offset);
+  });
 }
 
 hipError_t launch_append_bulk(const float* const* layer_keys, const float* const* layer_values,
-                              float* key_base, float* value_base, std::size_t layer_stride,
+                              void* key_base, void* value_base, std::size_t layer_stride,
                               std::size_t layers, const PageGeometry& g,
                               const std::uint32_t* blocks, std::size_t first_block,
                               std::size_t old_length, std::size_t tokens, hipStream_t stream,
-                              bool vec) {
+                              bool vec, PageType type) {
   const std::size_t work = layers * g.kv_heads * tokens * (vec ? g.head_dim / 4 : g.head_dim);
-  dim3 grid(grid_for(work, kThreads), 2);
-  LayerPointers src{layer_keys, layer_values};
-  if (vec) {
-    append_bulk_kernel<float4><<<grid, kThreads, 0, stream>>>(
-        src, key_base, value_base, layer_stride, layers, g.kv_heads, g.block_tokens, g.head_dim,
-        blocks, first_block, old_length, tokens);
-  } else {
-    append_bulk_kernel<float><<<grid, kThreads, 0, stream>>>(
-        src, key_base, value_base, layer_stride, layers, g.kv_heads, g.block_tokens, g.head_dim,
-        blocks, first_block, old_length, tokens);
-  }
-  return hipGetLastError();
+  const dim3 grid(grid_for(work, kThreads), 2);
+  const LayerPointers src{layer_keys, layer_values};
+  return with_page_type(type, vec, [&](auto s, auto w) {
+    using S = decltype(s);
+    append_bulk_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
+        src, as_pages<S>(key_base), as_pages<S>(value_base), layer_stride, layers, g.kv_heads,
+        g.block_tokens, g.head_dim, blocks, first_block, old_length, tokens);
+  });
 }
 
-hipError_t launch_append_slots(const float* keys, const float* values, float* key_pool,
-                               float* value_pool, const PageGeometry& g, const std::int64_t* slots,
-                               std::size_t count, hipStream_t stream, std::size_t tokens) {
+hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
+                               void* value_pool, const PageGeometry& g, const std::int64_t* slots,
+                               std::size_t count, hipStream_t stream, std::size_t tokens,
+                               PageType type) {
   if (count == 0 || tokens == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
   const std::size_t work = count * tokens * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
-  dim3 grid(grid_for(work, kThreads), 2);
-  if (vec) {
-    append_slots_kernel<float4><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count,
-        tokens);
-  } else {
-    append_slots_kernel<float><<<grid, kThreads, 0, stream>>>(
-        keys, values, key_pool, value_pool, g.kv_heads, g.block_tokens, g.head_dim, slots, count,
-        tokens);
-  }
-  return hipGetLastError();
+  const dim3 grid(grid_for(work, kThreads), 2);
+  return with_page_type(type, vec, [&](auto s, auto w) {
+    using S = decltype(s);
+    append_slots_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
+        keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), g.kv_heads, g.block_tokens,
+        g.head_dim, slots, count, tokens);
+  });
 }
 
-hipError_t launch_gather(const float* key_pool, const float* value_pool, const PageGeometry& g,
+hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
-                         float* values_out, std::size_t dest_tokens, hipStream_t stream) {
+                         float* values_out, std::size_t dest_tokens, hipStream_t stream,
+                         PageType type) {
   if (length == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys_out) && aligned16(values_out);
   const std::size_t work = g.kv_heads * length * (vec ? g.head_dim / 4 : g.head_dim);
-  dim3 grid(grid_for(work, kThreads), 2);
-  if (vec) {
-    gather_kernel<float4><<<grid, kThreads, 0, stream>>>(key_pool, value_pool, g.kv_heads,
-                                                         g.block_tokens, g.head_dim, blocks,
-                                                         length, keys_out, values_out, dest_tokens);
-  } else {
-    gather_kernel<float><<<grid, kThreads, 0, stream>>>(key_pool, value_pool, g.kv_heads,
-                                                        g.block_tokens, g.head_dim, blocks, length,
-                                                        keys_out, values_out, dest_tokens);
-  }
-  return hipGetLastError();
+  const dim3 grid(grid_for(work, kThreads), 2);
+  return with_page_type(type, vec, [&](auto s, auto w) {
+    using S = decltype(s);
+    gather_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
+        as_pages<S>(key_pool), as_pages<S>(value_pool), g.kv_heads, g.block_tokens, g.head_dim,
+        blocks, length, keys_out, values_out, dest_tokens);
+  });
 }
 
-hipError_t launch_page_copy(float* key_base, float* value_base, std::size_t layer_stride,
+hipError_t launch_page_copy(void* key_base, void* value_base, std::size_t layer_stride,
                             std::size_t layers, const PageGeometry& g, std::uint32_t from,
-                            std::uint32_t to, std::size_t tokens, hipStream_t stream) {
+                            std::uint32_t to, std::size_t tokens, hipStream_t stream,
+                            PageType type) {
   if (tokens == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0;
   const std::size_t work = layers * g.kv_heads * tokens * (vec ? g.head_dim / 4 : g.head_dim);
-  dim3 grid(grid_for(work, kThreads), 2);
-  if (vec) {
-    page_copy_kernel<float4><<<grid, kThreads, 0, stream>>>(key_base, value_base, layer_stride,
-                                                            layers, g.kv_heads, g.block_tokens,
-                                                            g.head_dim, from, to, tokens);
-  } else {
-    page_copy_kernel<float><<<grid, kThreads, 0, stream>>>(key_base, value_base, layer_stride,
-                                                           layers, g.kv_heads, g.block_tokens,
-                                                           g.head_dim, from, to, tokens);
-  }
-  return hipGetLastError();
+  const dim3 grid(grid_for(work, kThreads), 2);
+  return with_page_type(type, vec, [&](auto s, auto w) {
+    using S = decltype(s);
+    page_copy_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
+        as_pages<S>(key_base), as_pages<S>(value_base), layer_stride, layers, g.kv_heads,
+        g.block_tokens, g.head_dim, from, to, tokens);
+  });
 }
 
 hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
@@ -1600,6 +1718,33 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix) {
 
 }  // namespace
 
+namespace {
+
+template <int G, bool APPEND, bool BF16>
+void launch_stream_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k) {
+  decode_stream_kernel<G, APPEND, BF16><<<grid, 64, 0, stream>>>(
+      k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
+      APPEND ? k.append_slots : nullptr);
+}
+
+template <int G>
+void launch_stream(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k, bool append,
+                   bool bf16) {
+  if (bf16) {
+    if (append) {
+      launch_stream_variant<G, true, true>(grid, stream, k);
+    } else {
+      launch_stream_variant<G, false, true>(grid, stream, k);
+    }
+  } else if (append) {
+    launch_stream_variant<G, true, false>(grid, stream, k);
+  } else {
+    launch_stream_variant<G, false, false>(grid, stream, k);
+  }
+}
+
+}  // namespace
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   if (a.batch == 0) return hipSuccess;
   const bool streamed = a.pages_per_split == 0;
@@ -1652,6 +1797,7 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
       c.shared_pages = a.shared_pages;
       c.physical_blocks = a.physical_blocks;
       c.prefix_slot0 = static_cast<std::size_t>(k.prefix_slot0);
+      c.page_type = a.page_type;
       if (overlap) {
         hipError_t e = hipEventRecord(a.fork_event, stream);
         if (e == hipSuccess) e = hipStreamWaitEvent(a.side_stream, a.fork_event, 0);
@@ -1671,43 +1817,13 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     }
     k.stream_waves = static_cast<int>(waves);
     const dim3 grid(static_cast<unsigned>(waves));
+    const bool append = k.append_slots != nullptr;
+    const bool bf16 = a.page_type == PageType::kBF16;
     switch (group) {
-      case 1:
-        if (k.append_slots != nullptr) {
-          decode_stream_kernel<1, true><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
-        } else {
-          decode_stream_kernel<1, false><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
-        }
-        break;
-      case 2:
-        if (k.append_slots != nullptr) {
-          decode_stream_kernel<2, true><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
-        } else {
-          decode_stream_kernel<2, false><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
-        }
-        break;
-      case 4:
-        if (k.append_slots != nullptr) {
-          decode_stream_kernel<4, true><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
-        } else {
-          decode_stream_kernel<4, false><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
-        }
-        break;
-      case 8:
-        if (k.append_slots != nullptr) {
-          decode_stream_kernel<8, true><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, k.append_slots);
-        } else {
-          decode_stream_kernel<8, false><<<grid, 64, 0, stream>>>(
-              k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments, nullptr);
-        }
-        break;
+      case 1: launch_stream<1>(grid, stream, k, append, bf16); break;
+      case 2: launch_stream<2>(grid, stream, k, append, bf16); break;
+      case 4: launch_stream<4>(grid, stream, k, append, bf16); break;
+      case 8: launch_stream<8>(grid, stream, k, append, bf16); break;
       default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

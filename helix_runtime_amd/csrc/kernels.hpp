@@ -20,13 +20,20 @@ struct PageGeometry {
   std::size_t head_dim;
 };
 
+// Element type of the pages: fp32 (the reference's format) or bf16 (the
+// appended fp32 value rounded to nearest even; NaN stays NaN).  Pool
+// pointers are untyped where either may be passed; strides and offsets are
+// in elements.  Rows appended and gather outputs are fp32 either way.
+enum class PageType : int { kF32 = 0, kBF16 = 1 };
+constexpr std::size_t page_element_bytes(PageType t) { return t == PageType::kBF16 ? 2 : 4; }
+
 // One token for every layer.  src [layers, kv_heads, head_dim]; the token
 // lands at (block, offset) of every layer pool.  Layer l's key pool starts at
 // key_base + l * layer_stride (elements), values likewise.
-hipError_t launch_append_token(const float* keys, const float* values, float* key_base,
-                               float* value_base, std::size_t layer_stride, std::size_t layers,
+hipError_t launch_append_token(const float* keys, const float* values, void* key_base,
+                               void* value_base, std::size_t layer_stride, std::size_t layers,
                                const PageGeometry& g, std::uint32_t block, std::size_t offset,
-                               hipStream_t stream);
+                               hipStream_t stream, PageType type = PageType::kF32);
 
 // Bulk layer-major append of `tokens` tokens.  layer_keys/layer_values are
 // device arrays of `layers` device pointers, each [kv_heads, tokens, dim].
@@ -34,28 +41,32 @@ hipError_t launch_append_token(const float* keys, const float* values, float* ke
 // `vectorized` selects 128-bit accesses (every layer pointer 16-byte aligned
 // and head_dim % 4 == 0, checked by the caller on the host copies).
 hipError_t launch_append_bulk(const float* const* layer_keys, const float* const* layer_values,
-                              float* key_base, float* value_base, std::size_t layer_stride,
+                              void* key_base, void* value_base, std::size_t layer_stride,
                               std::size_t layers, const PageGeometry& g,
                               const std::uint32_t* blocks, std::size_t first_block,
                               std::size_t old_length, std::size_t tokens, hipStream_t stream,
-                              bool vectorized);
+                              bool vectorized, PageType type = PageType::kF32);
 
-// Batched append into one layer: src [count, kv_heads, dim]; slots[i] is the
-// flat slot block * block_tokens + offset of row i (negative rows skipped).
-hipError_t launch_append_slots(const float* keys, const float* values, float* key_pool,
-                               float* value_pool, const PageGeometry& g, const std::int64_t* slots,
-                               std::size_t count, hipStream_t stream, std::size_t tokens = 1);
+// Batched append into one layer: src [count, kv_heads, tokens, dim];
+// slots[i * tokens + t] is the flat slot block * block_tokens + offset of
+// row (i, t) (negative rows skipped).
+hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
+                               void* value_pool, const PageGeometry& g, const std::int64_t* slots,
+                               std::size_t count, hipStream_t stream, std::size_t tokens = 1,
+                               PageType type = PageType::kF32);
 
-// Gather one layer of one sequence into [kv_heads, dest_tokens, dim].
-hipError_t launch_gather(const float* key_pool, const float* value_pool, const PageGeometry& g,
+// Gather one layer of one sequence into fp32 [kv_heads, dest_tokens, dim].
+hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
-                         float* values_out, std::size_t dest_tokens, hipStream_t stream);
+                         float* values_out, std::size_t dest_tokens, hipStream_t stream,
+                         PageType type = PageType::kF32);
 
 // Copy the first `tokens` token rows of block `from` into block `to` for
 // every layer and head (copy-on-write of a partial shared page).
-hipError_t launch_page_copy(float* key_base, float* value_base, std::size_t layer_stride,
+hipError_t launch_page_copy(void* key_base, void* value_base, std::size_t layer_stride,
                             std::size_t layers, const PageGeometry& g, std::uint32_t from,
-                            std::uint32_t to, std::size_t tokens, hipStream_t stream);
+                            std::uint32_t to, std::size_t tokens, hipStream_t stream,
+                            PageType type = PageType::kF32);
 
 // Scatter (row, column, value) triples into a [rows, cols] uint32 table.
 hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
@@ -98,6 +109,10 @@ struct DecodeArgs {
   // once for all sequences on the matrix cores and the stream kernel covers
   // the rest.  0: off.
   std::size_t shared_pages = 0;
+  // Element type of key_pool / value_pool (and the append pools): bf16 pages
+  // are read through the same pointers, typed nominally as float.  Stream
+  // mode only.
+  PageType page_type = PageType::kF32;
   // Optional second stream for the cascade prefix pass: when set (with the
   // two events), the prefix runs on side_stream concurrently with the
   // stream kernel, which then takes one wavefront per SIMD and leaves the
@@ -173,6 +188,9 @@ struct PrefillArgs {
   // Optional launch order of the batch * kv_heads * ceil(tokens / positions
   // per block) work items, packed (b * kv_heads + kvh) * blocks + block.
   const std::uint32_t* order = nullptr;
+  // bf16 pages: history keys/values are widened from bf16 and the chunk rows
+  // rounded to bf16 (the values their pages hold once appended).
+  PageType page_type = PageType::kF32;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of
@@ -187,6 +205,7 @@ struct CascadePrefixArgs {
   float* part_o;
   float* part_ml;
   std::size_t batch, q_heads, kv_heads, shared_pages, physical_blocks, prefix_slot0;
+  PageType page_type = PageType::kF32;
 };
 hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream);
 // The shared prefix is split into key chunks (each leaving its own partial

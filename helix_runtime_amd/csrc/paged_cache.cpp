@@ -112,8 +112,9 @@ void synchronize_or_poison(CacheState& s, hipStream_t stream, const char* what) 
 
 }  // namespace
 
-CacheState::CacheState(const PagedConfig& config, int dev)
-    : manager(config), device((check_device(dev), dev)) {
+CacheState::CacheState(const PagedConfig& config, int dev, hip::PageType type)
+    : manager(config, hip::page_element_bytes(type)), device((check_device(dev), dev)),
+      page_type(type) {
   layer_elements = pool_elements(config);
   const std::size_t bytes = manager.stats().bytes_reserved;
   slab = DeviceBuffer(bytes, device);
@@ -142,8 +143,8 @@ void* CacheState::staging_bytes(std::size_t bytes) {
   return staging.data();
 }
 
-DevicePagedCache::DevicePagedCache(const PagedConfig& config, int device)
-    : state_(std::make_shared<CacheState>(config, device)) {}
+DevicePagedCache::DevicePagedCache(const PagedConfig& config, int device, hip::PageType page_type)
+    : state_(std::make_shared<CacheState>(config, device, page_type)) {}
 
 std::uint64_t DevicePagedCache::create_sequence() {
   std::scoped_lock lock(state_->mutex);
@@ -164,7 +165,7 @@ std::uint64_t DevicePagedCache::fork_sequence(std::uint64_t sequence, std::uint6
     const PagedConfig& c = s.manager.config();
     hip_check(hip::launch_page_copy(s.key_pool(0), s.value_pool(0), s.layer_stride(), c.layers,
                                     geometry(c), plan.cow_from, plan.cow_to, plan.cow_tokens,
-                                    stream),
+                                    stream, s.page_type),
               "fork_sequence copy-on-write launch");
     synchronize_or_poison(s, stream, "fork_sequence");
   }
@@ -189,7 +190,7 @@ void DevicePagedCache::append(std::uint64_t sequence, std::uint64_t cache_id, co
   hip_check(hip::launch_append_token(keys, values, s.key_pool(0), s.value_pool(0),
                                      s.layer_stride(), c.layers, geometry(c),
                                      static_cast<std::uint32_t>(slot / c.block_tokens),
-                                     slot % c.block_tokens, stream),
+                                     slot % c.block_tokens, stream, s.page_type),
             "append launch");
   synchronize_or_poison(s, stream, "append");
   s.manager.commit_append(plan);
@@ -235,7 +236,8 @@ void DevicePagedCache::append_layer_major(std::uint64_t sequence, std::uint64_t 
   const auto* dblocks = reinterpret_cast<const std::uint32_t*>(dev + 2 * c.layers * sizeof(void*));
   hip_check(hip::launch_append_bulk(dkeys, dvalues, s.key_pool(0), s.value_pool(0),
                                     s.layer_stride(), c.layers, geometry(c), dblocks,
-                                    plan.first_block, plan.old_length, tokens, stream, aligned),
+                                    plan.first_block, plan.old_length, tokens, stream, aligned,
+                                    s.page_type),
             "append_layer_major launch");
   synchronize_or_poison(s, stream, "append_layer_major");
   s.manager.commit_append(plan);
@@ -278,7 +280,7 @@ void DevicePagedCache::copy_layer_out(std::uint64_t sequence, std::uint64_t cach
                            hipMemcpyHostToDevice, stream),
             "copy_layer_out table upload");
   hip_check(hip::launch_gather(s.key_pool(layer), s.value_pool(layer), geometry(c), dev, length,
-                               keys_out, values_out, dest_tokens, stream),
+                               keys_out, values_out, dest_tokens, stream, s.page_type),
             "copy_layer_out launch");
   synchronize_or_poison(s, stream, "copy_layer_out");
 }
@@ -379,6 +381,8 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
   }
   static_cast<void>(total_pages);
   pages_per_split_ = pages_per_split != 0 ? pages_per_split : hip::kDefaultPagesPerSplit;
+  check(!s.bf16() || pages_per_split_ == 0, Status::kUnsupported,
+        "decode batch: bf16 pages decode in stream mode only (pages_per_split 0)");
   check(hip::decode_max_splits(max_blocks_, pages_per_split_) <= hip::kMaxDecodeSplits,
         Status::kUnsupported, "decode batch: max_tokens / pages_per_split above 4096 splits");
   host_lengths_.assign(batch, 0);
@@ -589,7 +593,7 @@ void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float
                                      state_->value_pool(layer),
                                      hip::PageGeometry{c.physical_blocks, c.kv_heads,
                                                        c.block_tokens, c.head_dimension},
-                                     slots(), batch(), stream, step_tokens_),
+                                     slots(), batch(), stream, step_tokens_, state_->page_type),
             "decode batch append launch");
 }
 
@@ -633,6 +637,7 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
   a.items = items_;
   a.between_event = between_event_;
   a.shared_pages = shared_pages_;
+  a.page_type = state_->page_type;
   a.side_stream = side_stream_;
   a.fork_event = fork_event_;
   a.join_event = join_event_;
@@ -667,6 +672,7 @@ void DecodeBatch::prefill_layer(std::size_t layer, const float* query, const flo
   a.tokens = step_tokens_;
   a.max_blocks = max_blocks_;
   a.physical_blocks = c.physical_blocks;
+  a.page_type = state_->page_type;
   if (step_tokens_ > 1) {
     a.order = reinterpret_cast<const std::uint32_t*>(
         static_cast<const unsigned char*>(step_.data()) + order_offset(step_tokens_));

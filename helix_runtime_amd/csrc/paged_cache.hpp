@@ -10,6 +10,7 @@
 #pragma once
 
 #include "block_manager.hpp"
+#include "kernels.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -68,22 +69,26 @@ private:
 void hip_check(hipError_t e, const char* what);
 
 struct CacheState {
-  CacheState(const PagedConfig& config, int device);
+  CacheState(const PagedConfig& config, int device, hip::PageType page_type = hip::PageType::kF32);
 
   BlockManager manager;
   int device;
+  hip::PageType page_type;
   DeviceBuffer slab;
   std::size_t layer_elements = 0;  // physical_blocks * kv_heads * block_tokens * head_dim
   std::mutex mutex;
   bool poisoned = false;
   DeviceBuffer staging;            // transient upload area (grown on demand)
 
-  [[nodiscard]] float* key_pool(std::size_t layer) const {
-    return static_cast<float*>(slab.data()) + (2 * layer) * layer_elements;
+  // Layer pools: fp32 elements, or bf16 bits for a bf16 cache (the pointer
+  // type is nominal then; page_type says which).
+  [[nodiscard]] float* key_pool(std::size_t layer) const { return pool_at(2 * layer); }
+  [[nodiscard]] float* value_pool(std::size_t layer) const { return pool_at(2 * layer + 1); }
+  [[nodiscard]] float* pool_at(std::size_t index) const {
+    return reinterpret_cast<float*>(static_cast<unsigned char*>(slab.data()) +
+                                    index * layer_elements * hip::page_element_bytes(page_type));
   }
-  [[nodiscard]] float* value_pool(std::size_t layer) const {
-    return static_cast<float*>(slab.data()) + (2 * layer + 1) * layer_elements;
-  }
+  [[nodiscard]] bool bf16() const noexcept { return page_type == hip::PageType::kBF16; }
   [[nodiscard]] std::size_t layer_stride() const noexcept { return 2 * layer_elements; }
   [[nodiscard]] bool overlaps_pool(const void* p, std::size_t bytes) const;
   void require_healthy(const char* op) const;
@@ -97,7 +102,8 @@ struct CacheState {
 // 557-611); a failed synchronisation poisons the cache.
 class DevicePagedCache {
 public:
-  DevicePagedCache(const PagedConfig& config, int device);
+  DevicePagedCache(const PagedConfig& config, int device,
+                   hip::PageType page_type = hip::PageType::kF32);
 
   [[nodiscard]] const std::shared_ptr<CacheState>& state() const noexcept { return state_; }
   [[nodiscard]] std::uint64_t cache_id() const noexcept { return state_->manager.cache_id(); }

@@ -31,6 +31,8 @@
 // masks, and such a block takes an exact per-key path for P.V.
 #include "kernels.hpp"
 
+#include "bf16.hpp"
+
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -110,7 +112,10 @@ __device__ __forceinline__ bool finite4(const float4& v) {
   return isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
 }
 
-template <int G, bool CASCADE>
+// BF16: history pages hold bf16; staging widens them and rounds the fp32
+// chunk rows to bf16 (the values their pages will hold), so the math is the
+// fp32 kernel's on bf16-exact operands.
+template <int G, bool CASCADE, bool BF16>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
                                                          const std::uint32_t* __restrict__ tables,
                                                          const std::uint32_t* __restrict__ order) {
@@ -206,17 +211,13 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
   auto stage_load = [&](int blk) {
     const int key0 = blk * kKeys;
     // Uniform bases: the history page of this block and the chunk rows.
-    const float* kpage = a.key_pool;
-    const float* vpage = a.value_pool;
+    std::size_t page_off = 0;  // element offset of this block's page in the layer pool
     bool page_ok = false;
     if (key0 < hist) {
       const std::uint32_t page = table[blk];
       page_ok = page < a.physical_blocks;
       bad = bad || !page_ok;
-      const std::size_t off =
-          page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
-      kpage += off;
-      vpage += off;
+      page_off = page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
     }
     const long long crow = static_cast<long long>(chunk_row0) + key0 - hist;
     const float* kchunk = a.chunk_key + crow * D;
@@ -227,10 +228,28 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
       const bool in_hist = key < hist;
       const bool valid = key < key_end && (!in_hist || page_ok);
       const int o = lane_off + 8 * r * D;
-      const float* kp = (in_hist ? kpage : kchunk) + o;
-      const float* vp = (in_hist ? vpage : vchunk) + o;
-      stk[r] = valid ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
-      stv[r] = valid ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (BF16) {
+        // History rows: 4 bf16 in the low two words; chunk rows: fp32.
+        stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        stv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (valid && in_hist) {
+          const std::size_t e = page_off + o;
+          const uint2 kw = *reinterpret_cast<const uint2*>(
+              reinterpret_cast<const unsigned short*>(a.key_pool) + e);
+          const uint2 vw = *reinterpret_cast<const uint2*>(
+              reinterpret_cast<const unsigned short*>(a.value_pool) + e);
+          stk[r] = make_float4(__uint_as_float(kw.x), __uint_as_float(kw.y), 0.f, 0.f);
+          stv[r] = make_float4(__uint_as_float(vw.x), __uint_as_float(vw.y), 0.f, 0.f);
+        } else if (valid) {
+          stk[r] = *reinterpret_cast<const float4*>(kchunk + o);
+          stv[r] = *reinterpret_cast<const float4*>(vchunk + o);
+        }
+      } else {
+        const float* kp = (in_hist ? a.key_pool + page_off : kchunk) + o;
+        const float* vp = (in_hist ? a.value_pool + page_off : vchunk) + o;
+        stk[r] = valid ? *reinterpret_cast<const float4*>(kp) : make_float4(0.f, 0.f, 0.f, 0.f);
+        stv[r] = valid ? *reinterpret_cast<const float4*>(vp) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
   };
   // Returns whether a staged value row is non-finite and some query row of
@@ -240,10 +259,21 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int kr = srow + 8 * r;
-      *reinterpret_cast<float4*>(&s_k[buf][kr * kKStride + scol * 4]) = stk[r];
-      *reinterpret_cast<float4*>(&s_v[buf][kr * D + scol * 4]) = stv[r];
       const int key = blk * kKeys + kr;
-      if (!CASCADE && key >= hist + pos0 + 1 && key < key_end && !finite4(stv[r])) {
+      float4 kv = stk[r];
+      float4 vv = stv[r];
+      if constexpr (BF16) {
+        if (key < hist) {
+          kv = bf16_widen(__float_as_uint(kv.x), __float_as_uint(kv.y));
+          vv = bf16_widen(__float_as_uint(vv.x), __float_as_uint(vv.y));
+        } else {
+          kv = bf16_rounded(kv);
+          vv = bf16_rounded(vv);
+        }
+      }
+      *reinterpret_cast<float4*>(&s_k[buf][kr * kKStride + scol * 4]) = kv;
+      *reinterpret_cast<float4*>(&s_v[buf][kr * D + scol * 4]) = vv;
+      if (!CASCADE && key >= hist + pos0 + 1 && key < key_end && !finite4(vv)) {
         nonfinite = true;
       }
     }
@@ -429,6 +459,16 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
   }
 }
 
+template <int G, bool CASCADE>
+void launch_variant(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
+                    const std::uint32_t* tables, const std::uint32_t* order, PageType type) {
+  if (type == PageType::kBF16) {
+    prefill_kernel<G, CASCADE, true><<<grid, 256, 0, stream>>>(k, tables, order);
+  } else {
+    prefill_kernel<G, CASCADE, false><<<grid, 256, 0, stream>>>(k, tables, order);
+  }
+}
+
 }  // namespace
 
 std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
@@ -475,10 +515,10 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.batch = static_cast<int>(a.batch);
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   switch (group) {
-    case 1: prefill_kernel<1, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
-    case 2: prefill_kernel<2, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
-    case 4: prefill_kernel<4, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
-    case 8: prefill_kernel<8, false><<<grid, 256, 0, stream>>>(k, a.tables, a.order); break;
+    case 1: launch_variant<1, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
+    case 2: launch_variant<2, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
+    case 4: launch_variant<4, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
+    case 8: launch_variant<8, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -509,10 +549,10 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
       (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * chunks));
   switch (group) {
-    case 1: prefill_kernel<1, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
-    case 2: prefill_kernel<2, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
-    case 4: prefill_kernel<4, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
-    case 8: prefill_kernel<8, true><<<grid, 256, 0, stream>>>(k, a.table, nullptr); break;
+    case 1: launch_variant<1, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 2: launch_variant<2, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 4: launch_variant<4, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 8: launch_variant<8, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -120,6 +120,18 @@ int helix_block_manager_geometry(const helix_block_manager* m, size_t* bytes_per
  * cuda_paged.cpp:454-697) plus the CPU cache's fork and bulk append. */
 int helix_paged_cache_create(const helix_paged_config* config, int device,
                              helix_paged_cache** out);
+/* Page element type (extension; the reference's pages are fp32 only,
+ * docs/KV_CACHE.md:531).  bf16 pages hold each appended fp32 value rounded to
+ * nearest even (NaN stays NaN); gathers widen them back to fp32 exactly, and
+ * attention over a bf16 cache computes in fp32 on the bf16 values, with the
+ * step's fp32 tail rows rounded the same way.  Byte statistics count 2-byte
+ * elements.  bf16 caches decode in stream mode only (pages_per_split 0), and
+ * the pools helix_paged_cache_layer_pools / helix_decode_view_layer_pools
+ * return then hold bf16 bits. */
+typedef enum helix_page_dtype { HELIX_PAGE_F32 = 0, HELIX_PAGE_BF16 = 1 } helix_page_dtype;
+int helix_paged_cache_create_typed(const helix_paged_config* config, int device, int page_dtype,
+                                   helix_paged_cache** out);
+int helix_paged_cache_page_dtype(helix_paged_cache* cache, int* out);
 void helix_paged_cache_destroy(helix_paged_cache* cache);
 int helix_paged_cache_create_sequence(helix_paged_cache* cache, helix_sequence* out);
 /* PagedKvCache::fork_sequence (paged.cpp:535-620); allow_cow != 0 copies a

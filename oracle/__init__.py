@@ -145,6 +145,27 @@ def random_normal(shape, seed):
     return out
 
 
+# ------------------------------------------------------------ bf16 pages --
+# Extension (no reference counterpart: the reference stores fp32 only,
+# docs/KV_CACHE.md:531).  The contract of bf16 pages: a page element is the
+# fp32 value rounded to nearest, ties to even (IEEE 754 roundTiesToEven onto
+# the 8-bit-mantissa grid); NaN stays NaN with the sign and top payload bits
+# kept and the quiet bit set; finite values that round past the largest bf16
+# become inf.  Attention over bf16 pages is the fp32 reference evaluated on
+# those rounded values.
+def bf16_bits(x):
+    """uint16 bf16 encodings of float32 values."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return np.where(nan, (u >> 16) | 0x40, rounded).astype(np.uint16)
+
+
+def round_bf16(x):
+    """float32 values moved onto the bf16 grid."""
+    return (bf16_bits(x).astype(np.uint32) << 16).view(np.float32)
+
+
 def mt19937_64_nth(seed, n):
     return int(lib().oracle_mt19937_64_nth(seed, n))
 

@@ -586,3 +586,49 @@ def test_batched_decode_equals_per_sequence_loop():
         o, _ = oracle.paged_attention(q[i][:, None], kp, vp, tables[i], int(lengths[i]),
                                       tk[i][:, None], tv[i][:, None])
         np.testing.assert_array_equal(out1[i], o[:, 0])
+
+
+# ------------------------------------------------------------ bf16 pages ----
+def test_bf16_rounding_known_answers():
+    """Round-to-nearest-even onto the bf16 grid, case by case."""
+    f = np.float32
+    cases = [
+        (1.0, 0x3F80), (-2.0, 0xC000), (0.0, 0x0000), (-0.0, 0x8000),
+        (np.inf, 0x7F80), (-np.inf, 0xFF80),
+        # exactly representable: unchanged
+        (1.0078125, 0x3F81),
+        # halfway between 0x3F80 and 0x3F81: ties to even (down)
+        (np.uint32(0x3F808000).view(np.float32), 0x3F80),
+        # halfway between 0x3F81 and 0x3F82: ties to even (up)
+        (np.uint32(0x3F818000).view(np.float32), 0x3F82),
+        # just above halfway: up; just below: down
+        (np.uint32(0x3F808001).view(np.float32), 0x3F81),
+        (np.uint32(0x3F807FFF).view(np.float32), 0x3F80),
+        # largest float32 rounds past the largest bf16: inf
+        (np.finfo(np.float32).max, 0x7F80),
+        # largest bf16 stays finite
+        (np.uint32(0x7F7F0000).view(np.float32), 0x7F7F),
+        # subnormals round on the same grid
+        (np.uint32(0x00018000).view(np.float32), 0x0002),
+        (np.uint32(0x00008000).view(np.float32), 0x0000),
+    ]
+    for x, want in cases:
+        got = int(oracle.bf16_bits(np.array([x], f))[0])
+        assert got == want, (x, hex(got), hex(want))
+    nan = oracle.bf16_bits(np.array([np.nan, -np.nan], f))
+    assert np.isnan(oracle.round_bf16(np.array([np.nan, -np.nan], f))).all()
+    assert (nan[0] & 0x8000) == 0 and (nan[1] & 0x8000) != 0  # sign kept
+
+
+def test_bf16_rounding_matches_torch():
+    """torch's CPU float32 -> bfloat16 conversion rounds to nearest even; it
+    must agree bit for bit on every non-NaN value, across magnitudes."""
+    import torch
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    x = np.concatenate([x, rng.standard_normal(50000).astype(np.float32) * 1e3])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.bf16_bits(x), want)
+    assert np.array_equal(oracle.round_bf16(x), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
