@@ -47,6 +47,11 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int D = 128;
 constexpr int P = 16;
 constexpr int kRows = 128;      // query rows per workgroup
+// 16-row tiles per wavefront: 2 (4 waves per workgroup, 256 VGPRs, two
+// workgroups per CU).  The kernel also builds with 1 (8 waves, 128 VGPRs,
+// four waves per SIMD): at config 5 that spills and measured 109 against
+// 112.5 TFLOP/s.
+constexpr int kTilesPerWave = 2;
 constexpr int kKeys = 16;       // keys per LDS stage (one page)
 constexpr int kKStride = D + 4; // padded K row: 8 consecutive rows hit distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
@@ -115,8 +120,11 @@ __device__ __forceinline__ bool finite4(const float4& v) {
 // BF16: history pages hold bf16; staging widens them and rounds the fp32
 // chunk rows to bf16 (the values their pages will hold), so the math is the
 // fp32 kernel's on bf16-exact operands.
-template <int G, bool CASCADE, bool BF16>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
+// RT: 16-row tiles per wavefront (1 or 2); the workgroup has 8 / RT waves
+// and each SIMD runs 6 - 2 * RT of them.
+template <int G, bool CASCADE, bool BF16, int RT>
+__global__ __launch_bounds__(512 / RT, 6 - 2 * RT)
+void prefill_kernel(PrefillKernelArgs a,
                                                          const std::uint32_t* __restrict__ tables,
                                                          const std::uint32_t* __restrict__ order) {
   constexpr int PW = kRows / G;  // chunk positions per workgroup
@@ -157,16 +165,16 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
   const std::uint32_t* __restrict__ table = tables + static_cast<std::size_t>(b) * a.max_blocks;
   const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
 
-  // Rows of this lane: tile t holds workgroup row wave * 32 + t * 16 + col.
+  // Rows of this lane: tile t holds workgroup row wave * 16 * RT + t * 16 + col.
   // Prefill: G heads x PW chunk positions of sequence b.  Cascade: row R of
   // the kv head is (sequence R / G, head R % G), one query token each.
-  int qpos[2];
-  bool qvalid[2];
-  std::size_t qrow[2];
-  float4 q[2][8];
+  int qpos[RT];
+  bool qvalid[RT];
+  std::size_t qrow[RT];
+  float4 q[RT][8];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int r = wave * 32 + t * 16 + col;
+  for (int t = 0; t < RT; ++t) {
+    const int r = wave * (16 * RT) + t * 16 + col;
     if constexpr (CASCADE) {
       const int row = pb * kRows + r;
       const int seq = row / G;
@@ -187,21 +195,26 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     }
   }
 
-  v4f o[2][2][4];  // [tile][dim half][component]: O^T tiles
+  v4f o[RT][2][4];  // [tile][dim half][component]: O^T tiles
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int c = 0; c < 4; ++c) o[t][h][c] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {-INFINITY, -INFINITY};
-  float l[2] = {0.f, 0.f};
+  float m[RT], l[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.f;
+  }
 
   // Staging: thread tid moves float4 column tid % 32 of key rows
-  // tid / 32 and tid / 32 + 8 of a 16-key block, for K and V.
+  // tid / 32 + RP * r (r < RT) of a 16-key block, for K and V.
+  constexpr int RP = 16 / RT;  // rows per staging pass
   const int srow = tid >> 5;
   const int scol = tid & 31;
-  float4 stk[2], stv[2];
+  float4 stk[RT], stv[RT];
   // A 16-key block is exactly one page, so a history block needs one
   // (uniform) table entry.  The non-finite check runs at store time, when
   // the values have arrived, so the loads stay in flight across the block's
@@ -223,11 +236,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     const float* kchunk = a.chunk_key + crow * D;
     const float* vchunk = a.chunk_value + crow * D;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int key = key0 + srow + 8 * r;
+    for (int r = 0; r < RT; ++r) {
+      const int key = key0 + srow + RP * r;
       const bool in_hist = key < hist;
       const bool valid = key < key_end && (!in_hist || page_ok);
-      const int o = lane_off + 8 * r * D;
+      const int o = lane_off + RP * r * D;
       if constexpr (BF16) {
         // History rows: 4 bf16 in the low two words; chunk rows: fp32.
         stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -257,8 +270,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
   auto stage_store = [&](int buf, int blk) {
     bool nonfinite = false;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int kr = srow + 8 * r;
+    for (int r = 0; r < RT; ++r) {
+      const int kr = srow + RP * r;
       const int key = blk * kKeys + kr;
       float4 kv = stk[r];
       float4 vv = stv[r];
@@ -303,9 +316,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
 
     // S^T = K Q^T: st[t] holds keys 4*grp + i (i = vector component) of
     // query row t*16 + col.
-    v4f st[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    v4f st[RT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < RT; ++t) {
+      st[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKStride + 16 * c + 4 * grp]);
@@ -320,12 +334,12 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     // Online softmax (exp2 domain), lane-local rescale of O.  A block whose
     // keys every row of the workgroup sees (all but the last blocks) skips
     // the mask.
-    float p[2][4];
+    float p[RT][4];
     const bool full = (n + 1) * kKeys <= min(key_end, hist + pos0 + 1);
     auto softmax = [&](auto full_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < RT; ++t) {
         float x[4];
         bool vis[4];
 #pragma unroll
@@ -367,7 +381,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < RT; ++t) {
               o[t][h][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(comp(vv, c), p[t][i], o[t][h][c],
                                                                 0, 0, 0);
             }
@@ -382,10 +396,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
         const int i = kk & 3;
         const int src = col + 16 * (kk >> 2);
         const int key = n * kKeys + kk;
-        float pk[2];
-        bool vis[2];
+        float pk[RT];
+        bool vis[RT];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < RT; ++t) {
           const float sel = i == 0 ? p[t][0] : i == 1 ? p[t][1] : i == 2 ? p[t][2] : p[t][3];
           pk[t] = __shfl(sel, src, 64);
           vis[t] = key < key_end && (key < hist || key - hist <= qpos[t]);
@@ -397,7 +411,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
             const float4 vv =
                 *reinterpret_cast<const float4*>(&V[kk * D + 64 * h + 16 * grp + 4 * ii]);
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < RT; ++t) {
               if (vis[t]) {
                 o[t][h][0][ii] += pk[t] * vv.x;
                 o[t][h][1][ii] += pk[t] * vv.y;
@@ -419,9 +433,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     // Partial (m, l, o) per row; lanes of the four k groups hold the row's
     // 128 dims, the (m, l) pair is written by group 0.
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < RT; ++t) {
       if (!qvalid[t]) continue;
-      const int row = pb * kRows + wave * 32 + t * 16 + col;
+      const int row = pb * kRows + wave * (16 * RT) + t * 16 + col;
       const long long units = static_cast<long long>(a.kv_heads) * a.batch;
       const std::size_t slot = static_cast<std::size_t>(
           a.prefix_slot0 + chunk * units + static_cast<long long>(kvh) * a.batch + row / G);
@@ -442,7 +456,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
     return;
   }
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RT; ++t) {
     if (qpos[t] >= T) continue;
     const bool nan_row = any_bad || m[t] == -INFINITY;
     const float inv = nan_row ? NAN : 1.0f / l[t];
@@ -462,10 +476,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKernelArgs a,
 template <int G, bool CASCADE>
 void launch_variant(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
                     const std::uint32_t* tables, const std::uint32_t* order, PageType type) {
+  constexpr int RT = kTilesPerWave;
   if (type == PageType::kBF16) {
-    prefill_kernel<G, CASCADE, true><<<grid, 256, 0, stream>>>(k, tables, order);
+    prefill_kernel<G, CASCADE, true, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
   } else {
-    prefill_kernel<G, CASCADE, false><<<grid, 256, 0, stream>>>(k, tables, order);
+    prefill_kernel<G, CASCADE, false, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
   }
 }
 
