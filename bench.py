@@ -254,6 +254,47 @@ def copy_probe(nbytes=1 << 30, reps=10):
                       "read_probe_gbps": round(4 * nbytes / ms_read / 1e6, 1)}), flush=True)
 
 
+def page_probe(seed, reps=10):
+    """Reads the config-3 decode's pages in the stream kernel's order (kv-head
+    major, each wavefront a contiguous range of the page list, two K/V page
+    pairs in flight) with loads only: the attainable rate for this access
+    pattern, with default and with non-temporal (streaming) loads."""
+    rng = np.random.default_rng(seed)
+    lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=BATCH)).astype(np.int64)
+    pages = (lengths + P - 1) // P
+    n_phys = int(pages.sum() + 64)
+    perm = rng.permutation(n_phys).astype(np.int64)
+    tables, at = [], 0
+    for n in pages:
+        tables.append(perm[at: at + n])
+        at += n
+    kv = [(ph * HKV + h, n_phys * HKV + ph * HKV + h)
+          for h in range(HKV) for t in tables for ph in t]
+    props = torch.cuda.get_device_properties(0)
+    waves = props.multi_processor_count * 8
+    steps = len(kv) // waves
+    pairs = np.array(kv[: waves * steps], np.uint32).reshape(-1)
+    pool = torch.zeros(2 * n_phys * HKV * P * D, device="cuda:0")
+    dpairs = torch.from_numpy(pairs.view(np.int32)).to("cuda:0")
+    sink = torch.empty(waves * 64, device="cuda:0")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {"page_probe_pairs": waves * steps, "page_probe_bytes": waves * steps * 2 * P * D * 4}
+    for nt in (0, 1):
+        args = (ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(dpairs.data_ptr()), steps, waves,
+                nt, ctypes.c_void_p(sink.data_ptr()),
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        hx.check(hx.load().helix_probe_page_read(*args))
+        e0.record()
+        for _ in range(reps):
+            hx.check(hx.load().helix_probe_page_read(*args))
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out["page_probe_gbps" + ("_nontemporal" if nt else "")] = round(
+            out["page_probe_bytes"] / ms / 1e6, 1)
+    print(json.dumps(out), flush=True)
+
+
 MFMA_F32_PEAK_TFLOPS = 157.3
 CHUNK_BATCH, CHUNK_TOKENS = 16, 512
 
@@ -442,6 +483,9 @@ def main():
     ap.add_argument("--page-dtype", default="f32", choices=("f32", "bf16"),
                     help="page element type (bf16: the reduced-precision extension; the CPU "
                          "baseline is reported for f32 pages only)")
+    ap.add_argument("--page-probe", action="store_true",
+                    help="only read the config-3 pages in the decode order with loads only "
+                         "(the attainable rate for the access pattern)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM probe / counter calibration)")
     args = ap.parse_args()
@@ -457,6 +501,9 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_probe:
         copy_probe()
+        return
+    if args.page_probe:
+        page_probe(args.seed)
         return
     if args.config == 5:
         run_prefill(args)

@@ -160,6 +160,7 @@ SIGNATURES = {
     "helix_decode_batch_shared_pages": (c_int, [vp, P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
     "helix_probe_stream_read": (c_int, [vp, c_size, vp, ctypes.c_uint, vp]),
+    "helix_probe_page_read": (c_int, [vp, vp, c_size, ctypes.c_uint, c_int, vp, vp]),
     "helix_paged_cache_create_typed": (c_int, [P(Config), c_int, c_int, P(vp)]),
     "helix_paged_cache_page_dtype": (c_int, [vp, P(c_int)]),
     # prefix cache

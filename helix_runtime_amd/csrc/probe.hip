@@ -6,6 +6,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
+
 namespace {
 
 template <int UNROLL>
@@ -28,7 +30,62 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const float4* __restri
   out[blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x] = acc;
 }
 
+constexpr int kProbeWord3 = 0x00020000;
+typedef unsigned probe_u32x4 __attribute__((ext_vector_type(4)));
+
+// One wavefront per work list; each step reads a K and a V chunk of 8 KiB
+// with 1 KiB-per-instruction buffer loads, two steps in flight.
+template <int AUX>
+__global__ __launch_bounds__(64) void page_read_kernel(const float* __restrict__ pool,
+                                                       const std::uint32_t* __restrict__ pairs,
+                                                       int steps, float* out) {
+  const int lane = threadIdx.x;
+  const std::uint32_t* my = pairs + static_cast<std::size_t>(blockIdx.x) * steps * 2;
+  float acc = 0.0f;
+  probe_u32x4 ka[8], va[8], kb[8], vb[8];
+  auto load = [&](int c, probe_u32x4 (&k)[8], probe_u32x4 (&v)[8]) {
+    c = c < steps ? c : steps - 1;
+    const std::uint32_t ck = __builtin_amdgcn_readfirstlane(my[2 * c]);
+    const std::uint32_t cv = __builtin_amdgcn_readfirstlane(my[2 * c + 1]);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(pool + static_cast<std::size_t>(ck) * 2048), 0, 8192, kProbeWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(pool + static_cast<std::size_t>(cv) * 2048), 0, 8192, kProbeWord3);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) k[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, u * 1024, AUX);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, u * 1024, AUX);
+  };
+  load(0, ka, va);
+  load(1, kb, vb);
+  for (int c = 0; c < steps; c += 2) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += __uint_as_float(ka[u][0]) + __uint_as_float(va[u][3]);
+    load(c + 2, ka, va);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += __uint_as_float(kb[u][1]) + __uint_as_float(vb[u][2]);
+    load(c + 3, kb, vb);
+  }
+  out[blockIdx.x * 64 + lane] = acc;
+}
+
 }  // namespace
+
+extern "C" int helix_probe_page_read(const float* pool, const uint32_t* pairs, size_t steps,
+                                     unsigned waves, int nontemporal, float* out,
+                                     helix_stream stream) {
+  if (pool == nullptr || pairs == nullptr || out == nullptr || steps == 0 || waves == 0 ||
+      steps > 0x7fffffff) {
+    return HELIX_INVALID_ARGUMENT;
+  }
+  const auto s = static_cast<hipStream_t>(stream);
+  if (nontemporal != 0) {
+    page_read_kernel<2><<<waves, 64, 0, s>>>(pool, pairs, static_cast<int>(steps), out);
+  } else {
+    page_read_kernel<0><<<waves, 64, 0, s>>>(pool, pairs, static_cast<int>(steps), out);
+  }
+  return hipGetLastError() == hipSuccess ? HELIX_OK : HELIX_RUNTIME;
+}
 
 extern "C" int helix_probe_stream_read(const float* data, size_t n_floats, float* out,
                                        unsigned blocks, helix_stream stream) {

@@ -413,6 +413,13 @@ int helix_prefix_cache_block_tokens(helix_prefix_cache* prefixes, size_t* out);
  * measure the attainable HBM read bandwidth. */
 int helix_probe_stream_read(const float* data, size_t n_floats, float* out, unsigned blocks,
                             helix_stream stream);
+/* Page-pair read probe (no reference counterpart): `waves` wavefronts each
+ * read `steps` (key chunk, value chunk) pairs of 8 KiB chunks of `pool`,
+ * two pairs in flight, as the stream decode kernel does; pairs holds
+ * waves * steps * 2 chunk indices (wave-major).  nontemporal != 0 uses the
+ * decode kernel's streaming cache policy.  out: waves * 64 floats. */
+int helix_probe_page_read(const float* pool, const uint32_t* pairs, size_t steps, unsigned waves,
+                          int nontemporal, float* out, helix_stream stream);
 
 #ifdef __cplusplus
 }
