@@ -52,6 +52,11 @@ constexpr int kRows = 128;      // query rows per workgroup
 // four waves per SIMD): at config 5 that spills and measured 109 against
 // 112.5 TFLOP/s.
 constexpr int kTilesPerWave = 2;
+// The cascade prefix pass has few keys per work item and runs beside the
+// stream decode kernel: 8 waves of one tile (108 VGPRs, no spills) fit two
+// waves per SIMD next to a stream wavefront (107.0 against 108.1 us per
+// layer back to back at config 4).
+constexpr int kCascadeTilesPerWave = 1;
 constexpr int kKeys = 16;       // keys per LDS stage (one page)
 constexpr int kKStride = D + 4; // padded K row: 8 consecutive rows hit distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
@@ -473,10 +478,9 @@ void prefill_kernel(PrefillKernelArgs a,
   }
 }
 
-template <int G, bool CASCADE>
+template <int G, bool CASCADE, int RT = kTilesPerWave>
 void launch_variant(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
                     const std::uint32_t* tables, const std::uint32_t* order, PageType type) {
-  constexpr int RT = kTilesPerWave;
   if (type == PageType::kBF16) {
     prefill_kernel<G, CASCADE, true, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
   } else {
@@ -564,10 +568,10 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
       (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * chunks));
   switch (group) {
-    case 1: launch_variant<1, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 2: launch_variant<2, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 4: launch_variant<4, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 8: launch_variant<8, true>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 1: launch_variant<1, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 2: launch_variant<2, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 4: launch_variant<4, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 8: launch_variant<8, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
