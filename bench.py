@@ -472,7 +472,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
-                    help="launch the per-layer append separately instead of fused into decode")
+                    help="the reference's flow: attention over the uncommitted tail for every "
+                         "layer, then one launch appending the token for all layers (instead "
+                         "of the append fused into each layer's decode launch)")
     ap.add_argument("--no-shuffle", action="store_true",
                     help="allocate pages in pool order instead of scattering them")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
@@ -508,7 +510,8 @@ def main():
     if args.config == 5:
         run_prefill(args)
         return
-    steps_total = args.warmup + args.steps + 2
+    # warmup, the timed steps, then as many instrumented steps (per-kernel events)
+    steps_total = args.warmup + 2 * args.steps + 2
     t_setup = time.perf_counter()
     if args.config == 4:
         cache, seqs, lengths0 = build_prefix_workload(args.seed, args.layers, steps_total)
@@ -545,9 +548,6 @@ def main():
         for l in range(L):
             if events is not None:
                 events[l][0].record(stream)
-            if not fused:
-                batch.append_layer(l, k[l], v[l], stream)
-            if events is not None:
                 events[l][1].record(stream)
                 batch.set_timing_event(events[l][3])
             if fused:
@@ -556,53 +556,69 @@ def main():
                 batch.attention_layer(l, q[l], k[l], v[l], out[l], stream)
             if events is not None:
                 events[l][2].record(stream)
-        batch.set_timing_event(None)
+        if events is not None:
+            batch.set_timing_event(None)
+        if not fused:
+            # The reference's flow: the token is committed for every layer
+            # after the forward pass has attended to it as the tail.
+            batch.append_all_layers(k, v, stream)
 
     for _ in range(args.warmup):
         step(None)
+    # Timed steps: no per-layer events (event records between launches add
+    # their own gaps); `value` and ms_per_step come from these.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(ev[i])
+        step(None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    if fused:
-        # The step's appends ran inside the decode kernel; time the standalone
-        # append kernel separately (it rewrites the same slots with the same
-        # rows) for the append rate.
-        aev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L * 3)]
-        for r in range(3 * L):
-            aev[r][0].record(stream)
-            batch.append_layer(r % L, k[r % L], v[r % L], stream)
-            aev[r][1].record(stream)
-        torch.cuda.synchronize()
-        append_ms = [e[0].elapsed_time(e[1]) for e in aev]
-    else:
-        append_ms = [ev[i][l][0].elapsed_time(ev[i][l][1]) for i in range(args.steps)
-                     for l in range(L)]
+    # Instrumented steps (same work, the next K steps): per-launch events for
+    # the kernel breakdown and the roofline.
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    # Append rates, timed separately: the all-layer commit (one launch moves
+    # the step's token for all layers) and the single-layer append.
+    reps = 3 * L
+    aev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(reps)]
+    lev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(reps)]
+    for r in range(reps):
+        aev[r][0].record(stream)
+        batch.append_all_layers(k, v, stream)
+        aev[r][1].record(stream)
+    for r in range(reps):
+        lev[r][0].record(stream)
+        batch.append_layer(r % L, k[r % L], v[r % L], stream)
+        lev[r][1].record(stream)
+    torch.cuda.synchronize()
+    append_ms = [e[0].elapsed_time(e[1]) for e in aev]
+    append_layer_ms = [e[0].elapsed_time(e[1]) for e in lev]
     attn_ms = [ev[i][l][1].elapsed_time(ev[i][l][2]) for i in range(args.steps) for l in range(L)]
     kern_ms = [ev[i][l][1].elapsed_time(ev[i][l][3]) for i in range(args.steps) for l in range(L)]
     merge_ms = [ev[i][l][3].elapsed_time(ev[i][l][2]) for i in range(args.steps) for l in range(L)]
 
     # History of timed step i is the initial length plus the tokens of the
-    # warmup and earlier timed steps.
-    per_step_decode = [decode_bytes(lengths0 + args.warmup + i) for i in range(args.steps)]
-    launch_bytes = float(np.mean(per_step_decode))
-    if args.config == 4:
-        # Roofline on unique HBM bytes: shared prefix pages are read from HBM
-        # once per launch and served from cache to the other sequences.
-        roof_bytes = float(np.mean([unique_decode_bytes(lengths0 + args.warmup + i)
-                                    for i in range(args.steps)]))
-    else:
-        roof_bytes = launch_bytes
+    # warmup and earlier timed steps; the instrumented steps follow them.
+    timed_hist = [lengths0 + args.warmup + i for i in range(args.steps)]
+    inst_hist = [lengths0 + args.warmup + args.steps + i for i in range(args.steps)]
+    # Config 4's roofline is on unique HBM bytes: shared prefix pages are
+    # read from HBM once per launch and served from cache to the other
+    # sequences.
+    roof_fn = unique_decode_bytes if args.config == 4 else decode_bytes
+    step_roof_bytes = float(np.mean([roof_fn(h) for h in timed_hist]))
+    roof_bytes = float(np.mean([roof_fn(h) for h in inst_hist]))
+    launch_bytes = float(np.mean([decode_bytes(h) for h in inst_hist]))
     if fused:
         # The decode kernel also writes the new token rows into their pages.
+        step_roof_bytes += append_write_bytes(nseq)
         roof_bytes += append_write_bytes(nseq)
         launch_bytes += append_write_bytes(nseq)
-    step_decode = roof_bytes * L
-    # Fused: the append's writes are in roof_bytes and its source rows are the
-    # attention tail, already counted there.
+    step_decode = step_roof_bytes * L
+    # Fused: the append's writes are counted with the decode and its source
+    # rows are the attention tail, already counted there.  Otherwise the
+    # all-layer commit reads the rows and writes the pages.
     step_append = 0 if fused else append_bytes(nseq) * L
     value = (step_decode + step_append) / (ms_per_step * 1e-3) / 1e9
     attn_avg_ms = float(np.mean(attn_ms))
@@ -617,7 +633,9 @@ def main():
     achieved = roof_bytes / (roof_ms * 1e-3) / 1e9
     pair_gbps = roof_bytes / (attn_avg_ms * 1e-3) / 1e9
     logical_gbps = launch_bytes / (attn_avg_ms * 1e-3) / 1e9
-    append_gbps = append_bytes(nseq) / (append_avg_ms * 1e-3) / 1e9
+    # The all-layer commit moves every layer's row of the step's token.
+    append_gbps = append_bytes(nseq) * L / (append_avg_ms * 1e-3) / 1e9
+    append_layer_avg_ms = float(np.mean(append_layer_ms))
 
     traffic = None
     suffix = "" if PAGE_DTYPE == "f32" else f"_{PAGE_DTYPE}"
@@ -680,8 +698,12 @@ def main():
         "decode_attn_logical_gbps": round(logical_gbps, 2),
         "append_gbps": round(append_gbps, 2),
         "append_avg_us": round(append_avg_ms * 1e3, 2),
-        "append_mode": ("fused into the decode kernel; append_gbps is the standalone append "
-                        "kernel, timed separately" if fused else "separate append kernel"),
+        "append_layer_avg_us": round(append_layer_avg_ms * 1e3, 2),
+        "append_mode": ("fused into each layer's decode launch; append_gbps is the all-layer "
+                        "commit (one launch writes the step's token for all layers, the "
+                        "batched CudaPagedKvCache::append), timed separately"
+                        if fused else "attention over the uncommitted tail for every layer, "
+                                      "then one all-layer commit launch per step"),
         "decode_avg_us": round(attn_avg_ms * 1e3, 2),
         "decode_median_us": round(float(np.median(attn_ms)) * 1e3, 2),
         "decode_kernel_avg_us": round(kern_avg_ms * 1e3, 2),

@@ -590,6 +590,14 @@ class DecodeBatch:
         check(_lib().helix_decode_batch_append_layer(self._h, layer, _ptr(keys), _ptr(values),
                                                      _stream(stream)))
 
+    def append_all_layers(self, keys, values, stream=None):
+        """append_layer for every layer in one launch: rows [layers, batch,
+        kv_heads, tokens, head_dim] (the step's token committed after the
+        forward pass, as CudaPagedKvCache::append commits [layers, kv_heads,
+        head_dim] for one sequence)."""
+        check(_lib().helix_decode_batch_append_all_layers(self._h, _ptr(keys), _ptr(values),
+                                                          _stream(stream)))
+
     def attention_layer(self, layer, query, tail_key, tail_value, output, stream=None):
         check(_lib().helix_decode_batch_attention_layer(self._h, layer, _ptr(query),
                                                         _ptr(tail_key), _ptr(tail_value),

@@ -1024,6 +1024,14 @@ int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const f
   });
 }
 
+int helix_decode_batch_append_all_layers(helix_decode_batch* b, const float* keys,
+                                         const float* values, helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    b->batch->append_all_layers(keys, values, as_stream(stream));
+  });
+}
+
 int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
                                        const float* tail_key, const float* tail_value,
                                        float* output, helix_stream stream) {

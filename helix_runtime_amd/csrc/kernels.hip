@@ -136,33 +136,44 @@ __global__ void append_bulk_kernel(LayerPointers src, S* key_base, S* value_base
   }
 }
 
-// Batched per-layer append through a slot mapping.  Source rows are
-// [batch, heads, tokens, dim] (tokens = 1 for a decode step, the chunk
-// length for chunked prefill); token t of sequence b goes to physical slot
-// slots[b * tokens + t] = block * block_tokens + offset (negative: skipped).
-template <typename S, int W>
+// Batched append through a slot mapping, for one layer or for every layer
+// of a step at once.  Source rows are [layers, batch, heads, tokens, dim]
+// (tokens = 1 for a decode step, the chunk length for chunked prefill);
+// token t of sequence b goes to physical slot slots[b * tokens + t] =
+// block * block_tokens + offset (negative: skipped) of every layer, whose
+// pools lie layer_stride page elements apart.  The all-layer form is the
+// batched CudaPagedKvCache::append (src/kv_cache/cuda_paged.cpp:491-611),
+// which commits one token's [layers, kv_heads, dim] rows after the forward
+// pass.  I is the index type: 32-bit whenever the element count fits, so
+// the row decomposition costs 32-bit divisions.
+template <typename S, int W, typename I>
 __global__ void append_slots_kernel(const float* __restrict__ keys,
                                     const float* __restrict__ values, S* key_pool, S* value_pool,
-                                    std::size_t heads, std::size_t block_tokens, std::size_t dim,
-                                    const std::int64_t* __restrict__ slots, std::size_t count,
-                                    std::size_t tokens) {
-  const std::size_t dv = dim / W;
-  const std::size_t total = count * heads * tokens * dv;
+                                    std::size_t layer_stride, I layers, I heads, I block_tokens,
+                                    I dim, const std::int64_t* __restrict__ slots, I count,
+                                    I tokens) {
+  const I dv = dim / W;
+  const I per_layer = count * heads * tokens * dv;
+  const I total = layers * per_layer;
   const float* src = blockIdx.y == 0 ? keys : values;
   S* pool = blockIdx.y == 0 ? key_pool : value_pool;
-  for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
-       e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
-    const std::size_t c = e % dv;
-    const std::size_t ht = e / dv;
-    const std::size_t t = ht % tokens;
-    const std::size_t bh = ht / tokens;
-    const std::size_t h = bh % heads;
-    const std::size_t b = bh / heads;
+  for (I e = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; e < total;
+       e += static_cast<I>(gridDim.x) * blockDim.x) {
+    const I l = e / per_layer;
+    const I r = e - l * per_layer;
+    const I c = r % dv;
+    const I ht = r / dv;
+    const I t = ht % tokens;
+    const I bh = ht / tokens;
+    const I h = bh % heads;
+    const I b = bh / heads;
     const std::int64_t slot = slots[b * tokens + t];
     if (slot < 0) continue;
     const std::size_t block = static_cast<std::size_t>(slot) / block_tokens;
     const std::size_t off = static_cast<std::size_t>(slot) % block_tokens;
-    Elems<S, W>::put(pool + ((block * heads + h) * block_tokens + off) * dim + c * W, src + e * W);
+    Elems<S, W>::put(pool + l * layer_stride +
+                         ((block * heads + h) * block_tokens + off) * dim + c * W,
+                     src + static_cast<std::size_t>(e) * W);
   }
 }
 
@@ -1568,16 +1579,27 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
 hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
                                void* value_pool, const PageGeometry& g, const std::int64_t* slots,
                                std::size_t count, hipStream_t stream, std::size_t tokens,
-                               PageType type) {
-  if (count == 0 || tokens == 0) return hipSuccess;
+                               PageType type, std::size_t layers, std::size_t layer_stride) {
+  if (count == 0 || tokens == 0 || layers == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
-  const std::size_t work = count * tokens * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
+  const std::size_t work = layers * count * tokens * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
   const dim3 grid(grid_for(work, kThreads), 2);
+  const bool narrow = work + static_cast<std::size_t>(grid.x) * kThreads < (std::size_t{1} << 32);
   return with_page_type(type, vec, [&](auto s, auto w) {
     using S = decltype(s);
-    append_slots_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
-        keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), g.kv_heads, g.block_tokens,
-        g.head_dim, slots, count, tokens);
+    constexpr int W = decltype(w)::value;
+    auto launch = [&](auto index) {
+      using I = decltype(index);
+      append_slots_kernel<S, W, I><<<grid, kThreads, 0, stream>>>(
+          keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), layer_stride,
+          static_cast<I>(layers), static_cast<I>(g.kv_heads), static_cast<I>(g.block_tokens),
+          static_cast<I>(g.head_dim), slots, static_cast<I>(count), static_cast<I>(tokens));
+    };
+    if (narrow) {
+      launch(0u);
+    } else {
+      launch(std::size_t{0});
+    }
   });
 }
 

@@ -47,13 +47,15 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
                               std::size_t old_length, std::size_t tokens, hipStream_t stream,
                               bool vectorized, PageType type = PageType::kF32);
 
-// Batched append into one layer: src [count, kv_heads, tokens, dim];
+// Batched append: src [layers, count, kv_heads, tokens, dim];
 // slots[i * tokens + t] is the flat slot block * block_tokens + offset of
-// row (i, t) (negative rows skipped).
+// row (i, t) (negative rows skipped) in each of `layers` layer pools that
+// start layer_stride page elements apart from key_pool / value_pool.
 hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
                                void* value_pool, const PageGeometry& g, const std::int64_t* slots,
                                std::size_t count, hipStream_t stream, std::size_t tokens = 1,
-                               PageType type = PageType::kF32);
+                               PageType type = PageType::kF32, std::size_t layers = 1,
+                               std::size_t layer_stride = 0);
 
 // Gather one layer of one sequence into fp32 [kv_heads, dest_tokens, dim].
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,

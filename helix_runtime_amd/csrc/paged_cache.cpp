@@ -597,6 +597,21 @@ void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float
             "decode batch append launch");
 }
 
+void DecodeBatch::append_all_layers(const float* keys, const float* values,
+                                    hipStream_t stream) const {
+  const PagedConfig& c = state_->manager.config();
+  check(prepared_, Status::kInvalidArgument, "decode batch append before prepare");
+  check(keys != nullptr && values != nullptr, Status::kInvalidArgument,
+        "decode batch append needs key and value rows");
+  DeviceGuard guard(state_->device);
+  hip_check(hip::launch_append_slots(keys, values, state_->key_pool(0), state_->value_pool(0),
+                                     hip::PageGeometry{c.physical_blocks, c.kv_heads,
+                                                       c.block_tokens, c.head_dimension},
+                                     slots(), batch(), stream, step_tokens_, state_->page_type,
+                                     c.layers, state_->layer_stride()),
+            "decode batch append launch");
+}
+
 void DecodeBatch::append_attention_layer(std::size_t layer, const float* query,
                                          const float* keys, const float* values, float* out,
                                          hipStream_t stream) const {

@@ -169,6 +169,10 @@ public:
   void prepare(hipStream_t stream, std::size_t tokens = 1);
   void append_layer(std::size_t layer, const float* keys, const float* values,
                     hipStream_t stream) const;
+  // append_layer() for every layer in one launch: rows [layers, batch,
+  // kv_heads, tokens, head_dim] (the step's K/V committed after the forward
+  // pass, as CudaPagedKvCache::append commits [layers, kv_heads, dim]).
+  void append_all_layers(const float* keys, const float* values, hipStream_t stream) const;
   void attention_layer(std::size_t layer, const float* query, const float* tail_key,
                        const float* tail_value, float* out, hipStream_t stream,
                        bool fused_append = false) const;

@@ -324,6 +324,15 @@ int helix_decode_batch_append_attention_layer(helix_decode_batch* b, size_t laye
 int helix_decode_batch_prepare_chunk(helix_decode_batch* b, size_t tokens, helix_stream stream);
 int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const float* keys,
                                     const float* values, helix_stream stream);
+/* append_layer() for every layer of the cache in one launch: keys/values
+ * [layers, batch, kv_heads, tokens, head_dim].  The batched form of
+ * CudaPagedKvCache::append (include/helix/kv_cache/cuda_paged.hpp:47-120,
+ * src/kv_cache/cuda_paged.cpp:491-611), which commits one token's
+ * [layers, kv_heads, head_dim] K/V after the forward pass has attended to it
+ * as the uncommitted tail; the reference issues 2 * layers * kv_heads
+ * device copies per sequence for it. */
+int helix_decode_batch_append_all_layers(helix_decode_batch* b, const float* keys,
+                                         const float* values, helix_stream stream);
 int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
                                        const float* tail_key, const float* tail_value,
                                        float* output, helix_stream stream);

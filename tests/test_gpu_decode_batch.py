@@ -25,9 +25,13 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("mode", ["separate", "fused", "commit"])
 @pytest.mark.parametrize("hq", [8, 32])
-def test_decode_batch_steps_match_oracle(device, hq, fused):
+def test_decode_batch_steps_match_oracle(device, hq, mode):
+    """separate: append_layer then attention_layer per layer; fused: one
+    launch per layer; commit: attention over the uncommitted tail for every
+    layer, then one append_all_layers launch (the reference's flow: the
+    token is appended for all layers after the forward pass)."""
     L, H, D, P = 2, 8, 128, 16
     rng = np.random.default_rng(hq)
     lengths = [1, 15, 16, 31, 47, 200]
@@ -60,11 +64,13 @@ def test_decode_batch_steps_match_oracle(device, hq, fused):
         for layer in range(L):
             q = rng.standard_normal((B, hq, D), dtype=np.float32)
             out = torch.empty(B, hq, D, device=device)
-            if fused:
+            if mode == "fused":
                 batch.append_attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]),
                                              out)
-            else:
+            elif mode == "separate":
                 batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+                batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            else:
                 batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
             torch.cuda.synchronize()
             kp, vp = pool.layer_pages(layer)
@@ -74,9 +80,54 @@ def test_decode_batch_steps_match_oracle(device, hq, fused):
             ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
                                         threads=8)
             np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+        if mode == "commit":
+            batch.append_all_layers(dev(keys), dev(values))
         for b, (_, so) in enumerate(seqs):
             pool.append(so, keys[:, b], values[:, b])
         assert cache.stats() == pool.stats()
+    for s, so in seqs:
+        assert cache.block_table(s) == pool.block_table(so).tolist()
+        for layer in range(L):
+            gk, gv = cache.retrieve_layer(s, layer)
+            ok, ov = pool.copy_layer(so, layer)
+            np.testing.assert_array_equal(host(gk), ok)
+            np.testing.assert_array_equal(host(gv), ov)
+    batch.close()
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 16, 37])
+def test_append_all_layers_chunk_bit_exact(device, tokens):
+    """One append_all_layers launch writes a step of `tokens` tokens for every
+    layer (rows [layers, batch, kv_heads, tokens, dim]) exactly as the oracle's
+    layer-major append does, across page boundaries and mid-page starts."""
+    L, H = 3, 4
+    rng = np.random.default_rng(tokens)
+    lengths = [0, 7, 16, 33]
+    N = sum((n + tokens) // P + 2 for n in lengths) + 4
+    cache = hx.PagedKvCache(L, H, D, P, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for n in lengths:
+        s, so = cache.create_sequence(), pool.create_sequence()
+        if n:
+            k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            cache.append_layer_major(s, [dev(k[l]) for l in range(L)],
+                                     [dev(v[l]) for l in range(L)])
+            pool.append_layer_major(so, k, v)
+        seqs.append((s, so))
+    B = len(seqs)
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], H, max_tokens=128)
+    if tokens == 1:
+        batch.prepare()
+    else:
+        batch.prepare_chunk(tokens)
+    keys = rng.standard_normal((L, B, H, tokens, D), dtype=np.float32)
+    values = rng.standard_normal((L, B, H, tokens, D), dtype=np.float32)
+    batch.append_all_layers(dev(keys), dev(values))
+    torch.cuda.synchronize()
+    for b, (_, so) in enumerate(seqs):
+        pool.append_layer_major(so, keys[:, b], values[:, b])
     for s, so in seqs:
         assert cache.block_table(s) == pool.block_table(so).tolist()
         for layer in range(L):
@@ -178,9 +229,9 @@ def test_prefix_sharing_decode_with_cow_forks(device):
     batch.close()
 
 
-@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("mode", ["separate", "fused", "commit"])
 @pytest.mark.parametrize("hq", [8, 32])
-def test_cascade_shared_prefix_decode(device, hq, fused):
+def test_cascade_shared_prefix_decode(device, hq, mode):
     """Sequences forked from one root share its full leading pages; the decode
     step attends them once for the batch (cascade) and the per-sequence rest
     through the stream kernel.  Outputs match the oracle over several steps,
@@ -224,17 +275,21 @@ def test_cascade_shared_prefix_decode(device, hq, fused):
         for layer in range(L):
             q = rng.standard_normal((B, hq, D), dtype=np.float32)
             out = torch.empty(B, hq, D, device=device)
-            if fused:
+            if mode == "fused":
                 batch.append_attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]),
                                              out)
-            else:
+            elif mode == "separate":
                 batch.append_layer(layer, dev(keys[layer]), dev(values[layer]))
+                batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
+            else:
                 batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out)
             torch.cuda.synchronize()
             kp, vp = pool.layer_pages(layer)
             ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
                                         threads=8)
             np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+        if mode == "commit":
+            batch.append_all_layers(dev(keys), dev(values))
         for b, (_, so) in enumerate(seqs):
             pool.append(so, keys[:, b], values[:, b])
     assert cache.stats() == pool.stats()
