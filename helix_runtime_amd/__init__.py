@@ -12,6 +12,7 @@ kernels of ``libhelix_paged.so``.
 from __future__ import annotations
 
 import ctypes
+import sys
 import os
 import subprocess
 
@@ -77,7 +78,9 @@ class BlockManager:
         self.block_tokens = block_tokens
         self.physical_blocks = physical_blocks
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         h = getattr(self, "_h", None)
         if h:
             _lib().helix_block_manager_destroy(h)
@@ -179,7 +182,9 @@ class PagedPrefixCache:
             _lib().helix_prefix_cache_destroy(h)
             self._h = None
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         self.close()
 
     def insert(self, namespace_id, tokens, source):
@@ -260,7 +265,9 @@ class PagedKvCache:
             _lib().helix_paged_cache_destroy(h)
             self._h = None
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         self.close()
 
     def create_sequence(self) -> Sequence:
@@ -398,7 +405,9 @@ class DecodeView:
     def __exit__(self, *exc):
         self.release()
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         self.release()
 
     def length(self):
@@ -441,7 +450,9 @@ class PagedBlockTable:
     def data(self):
         return _lib().helix_block_table_data(self._h)
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         h = getattr(self, "_h", None)
         if h:
             _lib().helix_block_table_destroy(h)
@@ -564,7 +575,9 @@ class DecodeBatch:
             _lib().helix_decode_batch_destroy(h)
             self._h = None
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return  # the process is exiting; the driver reclaims device memory
         self.close()
 
     def prepare(self, stream=None):

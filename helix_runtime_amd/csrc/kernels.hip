@@ -784,12 +784,11 @@ __device__ __forceinline__ long long wave_sum(long long v) {
   return v;
 }
 
-// Pages of sequences [0, upto) for one kv head: sum of unit_pages.  The
-// decode and the merge kernel compute it identically.
-__device__ __forceinline__ long long stream_pages_before(const DecodeKernelArgs& a, int upto,
-                                                         int lane) {
+// Pages of sequences [from, upto) for one kv head: sum of unit_pages.
+__device__ __forceinline__ long long stream_pages_between(const DecodeKernelArgs& a, int from,
+                                                          int upto, int lane) {
   long long sum = 0;
-  for (int c0 = 0; c0 < upto; c0 += 64) {
+  for (int c0 = from; c0 < upto; c0 += 64) {
     const int bb = c0 + lane;
     const int w = bb < upto ? unit_pages(clamp_length(a.lengths[bb], a.max_blocks), a.first_page) : 0;
     sum += wave_sum(w);
@@ -851,12 +850,27 @@ void decode_stream_kernel(
   const int j = lane & 31;
   const int wave = blockIdx.x;
 
-  // One pass over the lengths when the batch fits a wavefront (lane b holds
-  // sequence b), a second one only for larger batches.
-  const int hist0 = lane < a.batch ? clamp_length(a.lengths[lane], a.max_blocks) : -1;
-  const int np0 = lane < a.batch ? unit_pages(hist0, a.first_page) : 0;
-  long long per_head = wave_sum(np0);
-  if (a.batch > 64) per_head += stream_pages_before(a, a.batch, lane) - per_head;
+  // The lengths of the first kScanChunks * 64 sequences are loaded at once
+  // (lane l holds sequences l, l + 64, ...), so finding the first unit costs
+  // one load latency; only larger batches load further chunks in turn.
+  constexpr int kScanChunks = 4;
+  int histc[kScanChunks];
+  int npc[kScanChunks];
+#pragma unroll
+  for (int c = 0; c < kScanChunks; ++c) {
+    const int bb = c * 64 + lane;
+    histc[c] = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
+  }
+  long long lane_pages = 0;
+#pragma unroll
+  for (int c = 0; c < kScanChunks; ++c) {
+    npc[c] = c * 64 + lane < a.batch ? unit_pages(histc[c], a.first_page) : 0;
+    lane_pages += npc[c];
+  }
+  long long per_head = wave_sum(lane_pages);
+  if (a.batch > kScanChunks * 64) {
+    per_head += stream_pages_between(a, kScanChunks * 64, a.batch, lane);
+  }
   per_head = uniform64(per_head);
   const long long total = per_head * a.kv_heads;
   const long long C = uniform64((total + a.stream_waves - 1) / a.stream_waves);
@@ -872,9 +886,22 @@ void decode_stream_kernel(
     long long base = 0;
     for (int c0 = 0; c0 < a.batch; c0 += 64) {
       const int bb = c0 + lane;
-      const int hist =
-          c0 == 0 ? hist0 : (bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1);
-      const int np = c0 == 0 ? np0 : (bb < a.batch ? unit_pages(hist, a.first_page) : 0);
+      int hist, np;
+      if (c0 < kScanChunks * 64) {
+        // Select the preloaded chunk (wave-uniform index into registers).
+        hist = histc[0];
+        np = npc[0];
+#pragma unroll
+        for (int c = 1; c < kScanChunks; ++c) {
+          if (c0 == c * 64) {
+            hist = histc[c];
+            np = npc[c];
+          }
+        }
+      } else {
+        hist = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
+        np = bb < a.batch ? unit_pages(hist, a.first_page) : 0;
+      }
       long long incl = np;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -970,11 +997,15 @@ void decode_stream_kernel(
     if (p == 0 || d.g == g0) {
       const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<float*>(a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D),
-          0, G * D * 4, kBufferWord3);
+          0, d.skip ? 0 : G * D * 4, kBufferWord3);
 #pragma unroll
       for (int h = 0; h < G; ++h) q[h] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(qr, row_off, h * D * 4, 0));
     }
-    const int bytes = BF16 ? (tail ? D * 4 : P * D * 2) : P * D * 4;
+    // A skip descriptor (past the end of the range) gets an empty buffer
+    // range: its loads return zeros without touching memory, and the step
+    // that consumes them does nothing.  The instruction stream is the same
+    // either way, so the prefetch waits stay static.
+    const int bytes = d.skip ? 0 : (BF16 ? (tail ? D * 4 : P * D * 2) : P * D * 4);
     const __amdgpu_buffer_rsrc_t kr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kb), 0, bytes, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vr =

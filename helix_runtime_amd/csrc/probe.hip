@@ -44,13 +44,16 @@ __global__ __launch_bounds__(64) void page_read_kernel(const float* __restrict__
   float acc = 0.0f;
   probe_u32x4 ka[8], va[8], kb[8], vb[8];
   auto load = [&](int c, probe_u32x4 (&k)[8], probe_u32x4 (&v)[8]) {
+    // Past the end: an empty buffer range, so the loads return zeros
+    // without touching memory (the instruction stream stays the same).
+    const int range = c < steps ? 8192 : 0;
     c = c < steps ? c : steps - 1;
     const std::uint32_t ck = __builtin_amdgcn_readfirstlane(my[2 * c]);
     const std::uint32_t cv = __builtin_amdgcn_readfirstlane(my[2 * c + 1]);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(pool + static_cast<std::size_t>(ck) * 2048), 0, 8192, kProbeWord3);
+        const_cast<float*>(pool + static_cast<std::size_t>(ck) * 2048), 0, range, kProbeWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(pool + static_cast<std::size_t>(cv) * 2048), 0, 8192, kProbeWord3);
+        const_cast<float*>(pool + static_cast<std::size_t>(cv) * 2048), 0, range, kProbeWord3);
 #pragma unroll
     for (int u = 0; u < 8; ++u) k[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, u * 1024, AUX);
 #pragma unroll
