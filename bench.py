@@ -295,6 +295,150 @@ def page_probe(seed, reps=10):
     print(json.dumps(out), flush=True)
 
 
+# Llama-3-8B decoder shapes for --model-step.
+MODEL_HIDDEN, MODEL_INTER, MODEL_VOCAB, ROPE_THETA = 4096, 14336, 128256, 500000.0
+
+
+class _DevicePointer:
+    """A raw device address passed where the wrappers take a tensor."""
+
+    def __init__(self, address):
+        self.address = address
+
+    def data_ptr(self):
+        return self.address
+
+
+def run_model_step(args):
+    """A whole Llama-3-8B-shaped decode step (batch 64, config-3 contexts, 32
+    layers, random fp32 weights): the model's dense work (RMSNorm,
+    projections, SwiGLU, LM head) in torch (hipBLASLt GEMMs), the KV path in
+    the library.  Two flows over the same pages, alternating step by step:
+
+    * reference: the order of CudaLlamaModel::decode_one_paged_device
+      (src/model/cuda_llama.cpp:311-400) -- per layer two RoPE launches,
+      attention over the uncommitted tail, copies of the token's K/V into
+      the step's [L, B, Hkv, D] buffers and a stream synchronisation; the
+      token committed for all layers after the forward pass;
+    * integrated: one RoPE launch for query and key, K/V projected straight
+      into the step buffers, the append fused into each decode launch, no
+      synchronisation inside the step.
+
+    value = tokens per second of the integrated flow."""
+    steps_total = args.warmup + 2 * args.steps + 2
+    cache, seqs, lengths0 = build_workload(args.seed, BATCH, LAYERS, steps_total)
+    nseq = len(seqs)
+    batch = hx.DecodeBatch(cache, seqs, HQ, max_tokens=int(lengths0.max()) + steps_total + P)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(args.seed + 7)
+
+    def w(*shape):
+        return torch.randn(*shape, device="cuda:0", generator=gen) * 0.02
+
+    layers = [{"an": 1 + w(MODEL_HIDDEN), "q": w(MODEL_HIDDEN, HQ * D),
+               "k": w(MODEL_HIDDEN, HKV * D), "v": w(MODEL_HIDDEN, HKV * D),
+               "o": w(HQ * D, MODEL_HIDDEN), "fn": 1 + w(MODEL_HIDDEN),
+               "g": w(MODEL_HIDDEN, MODEL_INTER), "u": w(MODEL_HIDDEN, MODEL_INTER),
+               "d": w(MODEL_INTER, MODEL_HIDDEN)} for _ in range(LAYERS)]
+    emb = w(MODEL_VOCAB, MODEL_HIDDEN)
+    final = 1 + w(MODEL_HIDDEN)
+    head = w(MODEL_HIDDEN, MODEL_VOCAB)
+    weight_bytes = sum(t.numel() for lw in layers for t in lw.values()) * 4 + head.numel() * 4
+    positions = int(lengths0.max()) + steps_total + 1
+    pair = torch.arange(D // 2, dtype=torch.float64)
+    ang = torch.arange(positions, dtype=torch.float64)[:, None] * (
+        ROPE_THETA ** (-2.0 * pair / D))[None, :]
+    cos = torch.cos(ang).float().to("cuda:0")
+    sin = torch.sin(ang).float().to("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    stream = torch.cuda.current_stream()
+    k_all = torch.empty(LAYERS, nseq, HKV, D, device="cuda:0")
+    v_all = torch.empty_like(k_all)
+    ctx = torch.empty(nseq, HQ, D, device="cuda:0")
+    token_ids = torch.randint(0, MODEL_VOCAB, (nseq,), device="cuda:0", generator=gen)
+    step_lengths = _DevicePointer(batch.device_state()["lengths"])
+
+    def norm(x, g):
+        return x * torch.rsqrt(torch.mean(x * x, dim=-1, keepdim=True) + 1e-5) * g
+
+    def step(integrated):
+        batch.prepare(stream)
+        hidden = emb[token_ids]
+        for l, lw in enumerate(layers):
+            x = norm(hidden, lw["an"])
+            q = (x @ lw["q"]).view(nseq, HQ, D)
+            if integrated:
+                torch.matmul(x, lw["k"], out=k_all[l].view(nseq, HKV * D))
+                torch.matmul(x, lw["v"], out=v_all[l].view(nseq, HKV * D))
+                batch.rope(q, k_all[l], cos, sin, stream)
+                batch.append_attention_layer(l, q, k_all[l], v_all[l], ctx, stream)
+            else:
+                k = (x @ lw["k"]).view(nseq, HKV, D)
+                v = (x @ lw["v"]).view(nseq, HKV, D)
+                hx.rope_out(q, cos, sin, q, positions=step_lengths, stream=stream)
+                hx.rope_out(k, cos, sin, k, positions=step_lengths, stream=stream)
+                batch.attention_layer(l, q, k, v, ctx, stream)
+                k_all[l].copy_(k)
+                v_all[l].copy_(v)
+            hidden = hidden + ctx.view(nseq, HQ * D) @ lw["o"]
+            f = norm(hidden, lw["fn"])
+            hidden = hidden + (torch.nn.functional.silu(f @ lw["g"]) * (f @ lw["u"])) @ lw["d"]
+            if not integrated:
+                stream.synchronize()
+        if not integrated:
+            batch.append_all_layers(k_all, v_all, stream)
+        return norm(hidden, final) @ head
+
+    times = {True: [], False: []}
+    for i in range(2 * (args.warmup + args.steps)):
+        integrated = i % 2 == 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step(integrated)
+        torch.cuda.synchronize()
+        if i >= 2 * args.warmup:
+            times[integrated].append(time.perf_counter() - t0)
+    ms = {k: float(np.mean(v)) * 1e3 for k, v in times.items()}
+    # Attention alone in the same state: the decode launches of one step.
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    batch.prepare(stream)
+    q = torch.randn(nseq, HQ, D, device="cuda:0", generator=gen)
+    ev[0].record(stream)
+    for l in range(LAYERS):
+        batch.append_attention_layer(l, q, k_all[l], v_all[l], ctx, stream)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    attn_ms = ev[0].elapsed_time(ev[1])
+    line = {
+        "metric": "Llama-3-8B-shaped decode step tokens/s (dense ops in torch, paged KV path "
+                  "in the library), batch 64",
+        "value": round(nseq / (ms[True] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms[True], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random fp32 weights, N(0,1) cache contents, seeded",
+        "config": {"workload": "config3 contexts under a Llama-3-8B-shaped decoder: 32 layers, "
+                               "hidden 4096, 32q/8kv heads, intermediate 14336, vocab 128256",
+                   "batch": nseq, "mean_context": float(lengths0.mean())},
+        "reference_flow_ms_per_step": round(ms[False], 3),
+        "reference_flow_tokens_per_s": round(nseq / (ms[False] * 1e-3), 1),
+        "attention_ms_per_step": round(attn_ms, 3),
+        "attention_share": round(attn_ms / ms[True], 4),
+        "dense_weight_bytes": weight_bytes,
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    batch.close()
+    cache.close()
+
+
 MFMA_F32_PEAK_TFLOPS = 157.3
 CHUNK_BATCH, CHUNK_TOKENS = 16, 512
 
@@ -488,6 +632,9 @@ def main():
     ap.add_argument("--page-probe", action="store_true",
                     help="only read the config-3 pages in the decode order with loads only "
                          "(the attainable rate for the access pattern)")
+    ap.add_argument("--model-step", action="store_true",
+                    help="a whole Llama-3-8B-shaped decode step (torch dense ops, library KV "
+                         "path): the integrated flow against the reference's per-layer order")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM probe / counter calibration)")
     args = ap.parse_args()
@@ -506,6 +653,9 @@ def main():
         return
     if args.page_probe:
         page_probe(args.seed)
+        return
+    if args.model_step:
+        run_model_step(args)
         return
     if args.config == 5:
         run_prefill(args)

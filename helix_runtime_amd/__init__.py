@@ -460,6 +460,25 @@ class PagedBlockTable:
 
 
 # ------------------------------------------------------------- attention ----
+def rope_out(input, cosine, sine, output, positions=None, stream=None):
+    """kernels::rope / cpu::rope_out (src/kernels/cpu/reference.cpp:490-533) on
+    device tensors: input/output [tokens, ..., head_dim] float32 (output may
+    be input), cosine/sine [rows, head_dim / 2].  Without positions token t
+    uses row t (rows must equal tokens); with int32 positions [tokens] it uses
+    row positions[t]."""
+    tokens, head_dim = input.shape[0], input.shape[-1]
+    vectors = input.numel() // (tokens * head_dim) if tokens and head_dim else 0
+    check(_lib().helix_rope(_ptr(input), _ptr(output), tokens, vectors, head_dim, _ptr(cosine),
+                            _ptr(sine), cosine.shape[0],
+                            None if positions is None else _ptr(positions), _stream(stream)))
+    return output
+
+
+def rope(input, cosine, sine, positions=None, stream=None):
+    import torch
+    return rope_out(input, cosine, sine, torch.empty_like(input), positions, stream)
+
+
 def paged_attention_out(query, key_blocks, value_blocks, block_table, kv_tokens,
                         query_position_offset, output, score_workspace, stream=None):
     """paged_scaled_dot_product_attention_out; block_table: device uint32 pointer or tensor."""
@@ -610,6 +629,13 @@ class DecodeBatch:
         head_dim] for one sequence)."""
         check(_lib().helix_decode_batch_append_all_layers(self._h, _ptr(keys), _ptr(values),
                                                           _stream(stream)))
+
+    def rope(self, query, key, cosine, sine, stream=None):
+        """Rotary embedding of the step's query [batch, q_heads, dim] and key
+        [batch, kv_heads, dim] in place, each sequence at its position (its
+        length before the step); cosine/sine [rows, dim / 2]."""
+        check(_lib().helix_decode_batch_rope(self._h, _ptr(query), _ptr(key), _ptr(cosine),
+                                             _ptr(sine), cosine.shape[0], _stream(stream)))
 
     def attention_layer(self, layer, query, tail_key, tail_value, output, stream=None):
         check(_lib().helix_decode_batch_attention_layer(self._h, layer, _ptr(query),

@@ -155,6 +155,8 @@ SIGNATURES = {
     "helix_decode_batch_prepare": (c_int, [vp, vp]),
     "helix_decode_batch_append_layer": (c_int, [vp, c_size, vp, vp, vp]),
     "helix_decode_batch_append_all_layers": (c_int, [vp, vp, vp, vp]),
+    "helix_decode_batch_rope": (c_int, [vp, vp, vp, vp, vp, c_size, vp]),
+    "helix_rope": (c_int, [vp, vp, c_size, c_size, c_size, vp, vp, c_size, vp, vp]),
     "helix_decode_batch_attention_layer": (c_int, [vp, c_size, vp, vp, vp, vp, vp]),
     "helix_decode_batch_tables": (c_int, [vp, P(vp), P(vp), P(vp), P(c_size), P(c_size)]),
     "helix_decode_batch_set_timing_event": (c_int, [vp, vp]),

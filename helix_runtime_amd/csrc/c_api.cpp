@@ -891,6 +891,37 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
   });
 }
 
+int helix_rope(const float* input, float* output, size_t tokens, size_t vectors,
+               size_t head_dim, const float* cosine, const float* sine, size_t cache_rows,
+               const int32_t* positions, helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "rope";
+    check(head_dim != 0 && head_dim % 2 == 0, Status::kInvalidArgument,
+          std::string(op) + ": head dimension must be positive and even");
+    if (tokens == 0 || vectors == 0) return;
+    check(input && output && cosine && sine, Status::kInvalidArgument,
+          std::string(op) + ": device pointers must be non-null");
+    check(positions != nullptr || cache_rows == tokens, Status::kInvalidArgument,
+          std::string(op) + ": without positions the tables need one row per token");
+    check(cache_rows != 0, Status::kInvalidArgument, std::string(op) + ": tables have no rows");
+    const std::size_t elems = mul(mul(tokens, vectors), head_dim);
+    check(elems / 2 < (std::size_t{1} << 31), Status::kOutOfRange,
+          std::string(op) + ": too many elements for one launch");
+    check(((reinterpret_cast<std::uintptr_t>(input) | reinterpret_cast<std::uintptr_t>(output)) & 7u) == 0,
+          Status::kInvalidArgument, std::string(op) + ": input and output must be 8-byte aligned");
+    const std::size_t bytes = elems * sizeof(float);
+    check(input == output || !overlap(input, bytes, output, bytes), Status::kInvalidArgument,
+          std::string(op) + ": output must be the input itself or not overlap it");
+    const std::size_t tb = mul(cache_rows, head_dim / 2) * sizeof(float);
+    check(!overlap(cosine, tb, output, bytes) && !overlap(sine, tb, output, bytes),
+          Status::kInvalidArgument, std::string(op) + ": output must not alias the tables");
+    helix::hip_check(helix::hip::launch_rope(helix::hip::RopeTensor{input, output, vectors},
+                                             helix::hip::RopeTensor{}, tokens, head_dim, cosine,
+                                             sine, cache_rows, positions, as_stream(stream)),
+                     op);
+  });
+}
+
 int helix_paged_append_slots(const float* keys, const float* values, float* key_blocks,
                              float* value_blocks, size_t physical_blocks, size_t kv_heads,
                              size_t block_tokens, size_t head_dim, const int64_t* slots,
@@ -1029,6 +1060,17 @@ int helix_decode_batch_append_all_layers(helix_decode_batch* b, const float* key
   return guarded([&] {
     check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
     b->batch->append_all_layers(keys, values, as_stream(stream));
+  });
+}
+
+int helix_decode_batch_rope(helix_decode_batch* b, float* query, float* key,
+                            const float* cosine, const float* sine, size_t cache_rows,
+                            helix_stream stream) {
+  return guarded([&] {
+    check(b != nullptr, Status::kInvalidArgument, "decode batch must not be NULL");
+    check(((reinterpret_cast<std::uintptr_t>(query) | reinterpret_cast<std::uintptr_t>(key)) & 7u) == 0,
+          Status::kInvalidArgument, "decode batch rope: query and key must be 8-byte aligned");
+    b->batch->rope(query, key, cosine, sine, cache_rows, as_stream(stream));
   });
 }
 

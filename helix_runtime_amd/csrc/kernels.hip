@@ -177,6 +177,55 @@ __global__ void append_slots_kernel(const float* __restrict__ keys,
   }
 }
 
+// ---------------------------------------------------------------- rope ----
+// Rotary embedding of adjacent pairs (2i, 2i+1) of head vectors, as
+// cpu::rope_out (src/kernels/cpu/reference.cpp:490-533): out[2i] =
+// x[2i]*cos - x[2i+1]*sin, out[2i+1] = x[2i]*sin + x[2i+1]*cos, every
+// product and sum rounded to fp32 on its own (no fused multiply-add), so the
+// result is bit-identical to the reference's CPU path.  Up to two tensors
+// [rows, vectors, dim] that share the rows' positions go in one launch (a
+// decode step's query and key); row r uses cache row positions[r] (or r), and
+// a position outside [0, cache_rows) yields a NaN row.  One thread per pair;
+// in place is allowed.
+struct RopeSegment {
+  const float* in;
+  float* out;
+  unsigned vectors;
+};
+
+__global__ void rope_kernel(RopeSegment s0, RopeSegment s1, unsigned rows, unsigned pairs,
+                            const float* __restrict__ cosine, const float* __restrict__ sine,
+                            const std::int32_t* __restrict__ positions, long long cache_rows) {
+  // Products and sums stay separately rounded: no contraction into fma.
+#pragma clang fp contract(off)
+  const unsigned per_row0 = s0.vectors * pairs;
+  const unsigned per_row1 = s1.vectors * pairs;
+  const unsigned total0 = rows * per_row0;
+  const unsigned total = total0 + rows * per_row1;
+  for (unsigned e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const bool second = e >= total0;
+    const unsigned f = second ? e - total0 : e;
+    const unsigned per_row = second ? per_row1 : per_row0;
+    const unsigned r = f / per_row;
+    const unsigned rem = f - r * per_row;  // vector * pairs + pair
+    const unsigned pair = rem % pairs;
+    const long long pos = positions != nullptr ? positions[r] : static_cast<long long>(r);
+    const std::size_t off = (static_cast<std::size_t>(r) * per_row + rem) * 2;
+    const float2 x = *reinterpret_cast<const float2*>((second ? s1.in : s0.in) + off);
+    float2 y;
+    if (pos < 0 || pos >= cache_rows) {
+      y = make_float2(NAN, NAN);
+    } else {
+      const std::size_t c_off = static_cast<std::size_t>(pos) * pairs + pair;
+      const float c = cosine[c_off];
+      const float sn = sine[c_off];
+      y.x = x.x * c - x.y * sn;
+      y.y = x.x * sn + x.y * c;
+    }
+    *reinterpret_cast<float2*>((second ? s1.out : s0.out) + off) = y;
+  }
+}
+
 // Reference: PagedKvCache copy_layer / copy_layer_prefix_out
 // (src/kv_cache/paged.cpp:242-280, 895-950).
 template <typename S, int W>
@@ -1632,6 +1681,20 @@ hipError_t launch_append_slots(const float* keys, const float* values, void* key
       launch(std::size_t{0});
     }
   });
+}
+
+hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t rows,
+                       std::size_t head_dim, const float* cosine, const float* sine,
+                       std::size_t cache_rows, const std::int32_t* positions, hipStream_t stream) {
+  const std::size_t pairs = head_dim / 2;
+  const std::size_t work = rows * (a.vectors + b.vectors) * pairs;
+  if (work == 0) return hipSuccess;
+  const RopeSegment s0{a.input, a.output, static_cast<unsigned>(a.vectors)};
+  const RopeSegment s1{b.input, b.output, static_cast<unsigned>(b.vectors)};
+  rope_kernel<<<grid_for(work, kThreads), kThreads, 0, stream>>>(
+      s0, s1, static_cast<unsigned>(rows), static_cast<unsigned>(pairs), cosine, sine, positions,
+      static_cast<long long>(cache_rows));
+  return hipGetLastError();
 }
 
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,

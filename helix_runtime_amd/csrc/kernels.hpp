@@ -57,6 +57,19 @@ hipError_t launch_append_slots(const float* keys, const float* values, void* key
                                PageType type = PageType::kF32, std::size_t layers = 1,
                                std::size_t layer_stride = 0);
 
+// Rotary embedding (cpu::rope_out, bit-exact) of up to two tensors
+// [rows, vectors, head_dim] whose rows share positions; row r uses cache row
+// positions[r] (positions == nullptr: row r).  rows * vectors * head_dim / 2
+// summed over both must stay below 2^32.
+struct RopeTensor {
+  const float* input = nullptr;
+  float* output = nullptr;
+  std::size_t vectors = 0;
+};
+hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t rows,
+                       std::size_t head_dim, const float* cosine, const float* sine,
+                       std::size_t cache_rows, const std::int32_t* positions, hipStream_t stream);
+
 // Gather one layer of one sequence into fp32 [kv_heads, dest_tokens, dim].
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,

@@ -612,6 +612,22 @@ void DecodeBatch::append_all_layers(const float* keys, const float* values,
             "decode batch append launch");
 }
 
+void DecodeBatch::rope(float* query, float* key, const float* cosine, const float* sine,
+                       std::size_t cache_rows, hipStream_t stream) const {
+  const PagedConfig& c = state_->manager.config();
+  check(prepared_, Status::kInvalidArgument, "decode batch rope before prepare");
+  check(step_tokens_ == 1, Status::kInvalidArgument,
+        "decode batch rope needs a one-token step (positions of chunk rows differ)");
+  check(query != nullptr && key != nullptr && cosine != nullptr && sine != nullptr,
+        Status::kInvalidArgument, "decode batch rope needs query, key and the rope tables");
+  check(cache_rows != 0, Status::kInvalidArgument, "decode batch rope tables have no rows");
+  DeviceGuard guard(state_->device);
+  hip_check(hip::launch_rope(hip::RopeTensor{query, query, q_heads_},
+                             hip::RopeTensor{key, key, c.kv_heads}, batch(), c.head_dimension,
+                             cosine, sine, cache_rows, lengths(), stream),
+            "decode batch rope launch");
+}
+
 void DecodeBatch::append_attention_layer(std::size_t layer, const float* query,
                                          const float* keys, const float* values, float* out,
                                          hipStream_t stream) const {

@@ -173,6 +173,12 @@ public:
   // kv_heads, tokens, head_dim] (the step's K/V committed after the forward
   // pass, as CudaPagedKvCache::append commits [layers, kv_heads, dim]).
   void append_all_layers(const float* keys, const float* values, hipStream_t stream) const;
+  // Rotary embedding of a one-token step's query [batch, q_heads, dim] and
+  // key [batch, kv_heads, dim] rows in place, in one launch, each sequence
+  // at its position (its length before the step): cosine/sine are
+  // [cache_rows, dim / 2] tables as the model's rope cache holds them.
+  void rope(float* query, float* key, const float* cosine, const float* sine,
+            std::size_t cache_rows, hipStream_t stream) const;
   void attention_layer(std::size_t layer, const float* query, const float* tail_key,
                        const float* tail_value, float* out, hipStream_t stream,
                        bool fused_append = false) const;

@@ -272,6 +272,18 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
                                  helix_stream stream);
+/* kernels::rope / cpu::rope_out (src/kernels/cpu/reference.cpp:490-533):
+ * rotates the adjacent pairs (2i, 2i+1) of every head vector, out[2i] =
+ * x[2i]*cos - x[2i+1]*sin, out[2i+1] = x[2i]*sin + x[2i+1]*cos, each product
+ * and sum rounded to fp32 separately (bit-identical to the reference's CPU
+ * path).  input, output [tokens, vectors, head_dim] (output == input allowed,
+ * 8-byte aligned); cosine, sine [cache_rows, head_dim / 2].  positions NULL:
+ * token t uses table row t (cache_rows must equal tokens, as the reference
+ * requires); else row positions[t] (int32, device), and a position outside
+ * [0, cache_rows) yields a NaN vector. */
+int helix_rope(const float* input, float* output, size_t tokens, size_t vectors,
+               size_t head_dim, const float* cosine, const float* sine, size_t cache_rows,
+               const int32_t* positions, helix_stream stream);
 /* Writes rows [count, kv_heads, head_dim] of keys/values into one layer's
  * pools at slots[i] = block * block_tokens + offset (negative: skipped). */
 int helix_paged_append_slots(const float* keys, const float* values, float* key_blocks,
@@ -333,6 +345,16 @@ int helix_decode_batch_append_layer(helix_decode_batch* b, size_t layer, const f
  * device copies per sequence for it. */
 int helix_decode_batch_append_all_layers(helix_decode_batch* b, const float* keys,
                                          const float* values, helix_stream stream);
+/* Rotary embedding of a one-token step's query [batch, q_heads, head_dim]
+ * and key [batch, kv_heads, head_dim] rows, in place and in one launch, each
+ * sequence at its own position (its length before the step).  Replaces the
+ * model's two kernels::rope launches per layer (src/model/cuda_llama.cpp:
+ * 353-354); same arithmetic as helix_rope.  cosine/sine [cache_rows,
+ * head_dim / 2] as detail::make_rope_cache builds them
+ * (src/model/llama_common.cpp:22-47) for positions 0..cache_rows-1. */
+int helix_decode_batch_rope(helix_decode_batch* b, float* query, float* key,
+                            const float* cosine, const float* sine, size_t cache_rows,
+                            helix_stream stream);
 int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
                                        const float* tail_key, const float* tail_value,
                                        float* output, helix_stream stream);
