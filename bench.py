@@ -774,12 +774,11 @@ def main():
     attn_avg_ms = float(np.mean(attn_ms))
     kern_avg_ms = float(np.mean(kern_ms))
     append_avg_ms = float(np.mean(append_ms))
-    # The roofline is the dominant kernel's (the main decode kernel, timed
-    # alone); decode_attn_gbps is the whole attention launch incl. the merge.
-    # Config 4 runs the cascade prefix pass on a second stream beside the
-    # stream kernel, so no single kernel carries the launch: its roofline
-    # takes the whole launch (prefix || stream, then merge).
-    roof_ms = attn_avg_ms if args.config == 4 else kern_avg_ms
+    # The roofline is the dominant kernel's (timed alone): the stream decode
+    # kernel, or at config 4 the fused cascade kernel (prefix pass and
+    # stream in one launch); decode_attn_gbps is the whole attention launch
+    # including the merge.
+    roof_ms = kern_avg_ms
     achieved = roof_bytes / (roof_ms * 1e-3) / 1e9
     pair_gbps = roof_bytes / (attn_avg_ms * 1e-3) / 1e9
     logical_gbps = launch_bytes / (attn_avg_ms * 1e-3) / 1e9
@@ -858,7 +857,9 @@ def main():
         "decode_median_us": round(float(np.median(attn_ms)) * 1e3, 2),
         "decode_kernel_avg_us": round(kern_avg_ms * 1e3, 2),
         "decode_merge_avg_us": round(float(np.mean(merge_ms)) * 1e3, 2),
-        "decode_kernel": "decode_stream_kernel" if split == 0 else "decode_split_kernel",
+        "decode_kernel": ("decode_split_kernel" if split != 0 else
+                          "cascade_decode_kernel" if batch.shared_pages() > 0 else
+                          "decode_stream_kernel"),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic},

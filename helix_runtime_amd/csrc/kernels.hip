@@ -9,6 +9,7 @@
 #include "kernels.hpp"
 
 #include "bf16.hpp"
+#include "prefill_body.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -854,13 +855,73 @@ struct PageDesc {
 // BF16: pages hold bf16 (4 per 64-bit lane load) and are widened to fp32 in
 // registers.  The fp32 tail row is rounded to bf16 as it is read (it is the
 // value the page will hold once appended).
-template <int G, bool APPEND, bool BF16>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
-void decode_stream_kernel(
+// LDS of one stream wavefront.  Results are staged until the wavefront's
+// last page: on this architecture a store counts in the same in-order
+// counter as the loads, so a store issued between prefetches would make the
+// next page's wait also wait for the store to complete; staging keeps every
+// global store after the last load.  A full stage is flushed early (many
+// short units per wavefront).
+constexpr int kStreamStage = 4;
+template <int G>
+struct StreamShared {
+  __align__(16) float p[2][8 * G];
+  __align__(16) float head[3][G];
+  __align__(16) float4 res_o[kStreamStage][G][32];
+  float res_ml[kStreamStage][G][2];
+  long long res_dst[kStreamStage];  // >= 0: first output row; < 0: -1 - partial slot
+  int2 seg[kStreamStage];
+  int seg_unit[kStreamStage];
+  __align__(16) float4 app_k[kStreamStage][32];
+  __align__(16) float4 app_v[kStreamStage][32];
+  long long app_dst[kStreamStage];  // element offset of the row, < 0: none
+};
+
+// References to one stream wavefront's LDS arrays.  The stream kernel binds
+// them to separate __shared__ arrays: as distinct objects they are known not
+// to overlap, which the dynamically indexed fields of one struct are not
+// (the struct form cost 70 extra LDS reads and spills in the loop).
+template <int G>
+struct StreamLds {
+  float (&p)[2][8 * G];
+  float (&head)[3][G];
+  float4 (&res_o)[kStreamStage][G][32];
+  float (&res_ml)[kStreamStage][G][2];
+  long long (&res_dst)[kStreamStage];
+  int2 (&seg)[kStreamStage];
+  int (&seg_unit)[kStreamStage];
+  float4 (&app_k)[kStreamStage][32];
+  float4 (&app_v)[kStreamStage][32];
+  long long (&app_dst)[kStreamStage];
+};
+template <int G>
+__device__ __forceinline__ StreamLds<G> stream_lds(StreamShared<G>& s) {
+  return StreamLds<G>{s.p, s.head, s.res_o, s.res_ml, s.res_dst,
+                      s.seg, s.seg_unit, s.app_k, s.app_v, s.app_dst};
+}
+
+// LDS hand-off inside one wavefront.  In the stream kernel a workgroup is a
+// single wavefront, so a workgroup barrier is that; when several independent
+// stream wavefronts share a workgroup (the fused cascade launch) each orders
+// only its own LDS accesses, which execute in order within a wavefront.
+template <bool SHARED_BLOCK>
+__device__ __forceinline__ void stream_sync() {
+  if constexpr (SHARED_BLOCK) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();
+  }
+}
+
+// The body of one stream wavefront: `wave` is its index among
+// a.stream_waves, `lane` its lane, `sh` its LDS.
+template <int G, bool APPEND, bool BF16, bool SHARED_BLOCK>
+__device__ __forceinline__ void decode_stream_body(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
-    const std::int64_t* __restrict__ append_slots) {
+    const std::int64_t* __restrict__ append_slots, int wave, int lane, StreamLds<G> sh) {
   // The block table and lengths are read-only here and do not alias the
   // outputs; with the restrict-qualified parameters their uniform reads
   // become scalar loads.
@@ -876,28 +937,20 @@ void decode_stream_kernel(
   constexpr int R = G >= 4 ? G / 4 : 1;
   constexpr int DUPB = G >= 4 ? 0 : (G == 2 ? 1 : 2);
   constexpr int NV = 8 * G;
+  constexpr int kStage = kStreamStage;
+  auto& s_p = sh.p;
+  auto& s_head = sh.head;
+  auto& s_res_o = sh.res_o;
+  auto& s_res_ml = sh.res_ml;
+  auto& s_res_dst = sh.res_dst;
+  auto& s_seg = sh.seg;
+  auto& s_seg_unit = sh.seg_unit;
+  auto& s_app_k = sh.app_k;
+  auto& s_app_v = sh.app_v;
+  auto& s_app_dst = sh.app_dst;
 
-  __shared__ __align__(16) float s_p[2][NV];
-  __shared__ __align__(16) float s_head[3][G];
-  // Results staged until the wavefront's last page.  On this architecture a
-  // store counts in the same in-order counter as the loads, so a store
-  // issued between prefetches would make the next page's wait also wait for
-  // the store to complete; staging keeps every global store after the last
-  // load.  A full stage is flushed early (many short units per wavefront).
-  constexpr int kStage = 4;
-  __shared__ __align__(16) float4 s_res_o[kStage][G][32];
-  __shared__ float s_res_ml[kStage][G][2];
-  __shared__ long long s_res_dst[kStage];  // >= 0: first output row; < 0: -1 - partial slot
-  __shared__ int2 s_seg[kStage];
-  __shared__ int s_seg_unit[kStage];
-  __shared__ __align__(16) float4 s_app_k[kStage][32];
-  __shared__ __align__(16) float4 s_app_v[kStage][32];
-  __shared__ long long s_app_dst[kStage];  // element offset of the row, < 0: none
-
-  const int lane = threadIdx.x;
   const int parity = lane >> 5;
   const int j = lane & 31;
-  const int wave = blockIdx.x;
 
   // The lengths of the first kScanChunks * 64 sequences are loaded at once
   // (lane l holds sequences l, l + 64, ...), so finding the first unit costs
@@ -1149,7 +1202,7 @@ void decode_stream_kernel(
       if ((j & ((1 << DUPB) - 1)) == 0) s_p[parity][vi] = pr;
       if (parity == 0 && vi < G && (j & ((1 << DUPB) - 1)) == 0) s_head[0][vi] = alpha;
     }
-    __syncthreads();
+    stream_sync<SHARED_BLOCK>();
     float pp[NV];
 #pragma unroll
     for (int i = 0; i < NV / 4; ++i) {
@@ -1162,7 +1215,7 @@ void decode_stream_kernel(
     float al[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) al[h] = s_head[0][h];
-    __syncthreads();
+    stream_sync<SHARED_BLOCK>();
     if (valid < P) {  // wave-uniform: only partial pages and the tail
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -1247,7 +1300,7 @@ void decode_stream_kernel(
     nres = 0;
     nseg = 0;
     napp = 0;
-    __syncthreads();
+    stream_sync<SHARED_BLOCK>();
   };
 
   // Publishes the unit's result: the output itself when this wavefront saw
@@ -1267,7 +1320,7 @@ void decode_stream_kernel(
       }
     }
     if (nres == kStage) flush();
-    __syncthreads();
+    stream_sync<SHARED_BLOCK>();
     const std::size_t unit = static_cast<std::size_t>(d.kvh) * a.batch + d.b;
     // With a cascade prefix every unit also has a prefix partial to merge.
     const bool complete = a.first_page == 0 && d.p == d.np - 1 && d.g - d.p >= g0;
@@ -1299,7 +1352,7 @@ void decode_stream_kernel(
                             : -1 - static_cast<long long>(unit + wave);
     }
     ++nres;
-    __syncthreads();
+    stream_sync<SHARED_BLOCK>();
     reset();
   };
 
@@ -1339,7 +1392,7 @@ void decode_stream_kernel(
                        : ((slot / P * static_cast<long long>(a.kv_heads) + d.kvh) * P + slot % P) * D;
         }
         ++napp;
-        __syncthreads();
+        stream_sync<SHARED_BLOCK>();
       }
     }
     process(k, v, qc, valid);
@@ -1375,6 +1428,64 @@ void decode_stream_kernel(
     load_page(db, kb, vb, qb, badb);
   }
   flush();
+}
+
+template <int G, bool APPEND, bool BF16>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
+void decode_stream_kernel(
+    DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
+    const std::int32_t* __restrict__ lengths, float* __restrict__ out,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
+    const std::int64_t* __restrict__ append_slots) {
+  __shared__ __align__(16) float s_p[2][8 * G];
+  __shared__ __align__(16) float s_head[3][G];
+  __shared__ __align__(16) float4 s_res_o[kStreamStage][G][32];
+  __shared__ float s_res_ml[kStreamStage][G][2];
+  __shared__ long long s_res_dst[kStreamStage];
+  __shared__ int2 s_seg[kStreamStage];
+  __shared__ int s_seg_unit[kStreamStage];
+  __shared__ __align__(16) float4 s_app_k[kStreamStage][32];
+  __shared__ __align__(16) float4 s_app_v[kStreamStage][32];
+  __shared__ long long s_app_dst[kStreamStage];
+  decode_stream_body<G, APPEND, BF16, false>(
+      a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
+      StreamLds<G>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k, s_app_v,
+                   s_app_dst});
+}
+
+// Cascade decode in one launch.  Blocks [0, prefix_blocks) are the cascade
+// prefix pass's workgroups (4 wavefronts, the prefill kernel's two-tile
+// shape) and every later block is 4 independent stream wavefronts, so a CU
+// holds one of each (256 VGPRs per wavefront, two wavefronts per SIMD) and
+// the matrix-core prefix work runs beside the HBM-bound stream without a
+// second stream and the fork and join between them.  LDS is one buffer
+// carved either way.
+template <int G>
+union CascadeShared {
+  StreamShared<G> stream[4];
+  prefill_detail::PrefillShared prefill;
+};
+
+template <int G, bool APPEND, bool BF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void cascade_decode_kernel(
+    DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
+    const std::int32_t* __restrict__ lengths, float* __restrict__ out,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
+    const std::int64_t* __restrict__ append_slots, prefill_detail::PrefillKernelArgs prefix,
+    unsigned prefix_blocks) {
+  __shared__ __align__(16) unsigned char lds[sizeof(CascadeShared<G>)];
+  auto& sh = *reinterpret_cast<CascadeShared<G>*>(lds);
+  if (blockIdx.x < prefix_blocks) {
+    prefill_detail::prefill_body<G, true, BF16, 2>(prefix, tables, nullptr, blockIdx.x,
+                                                   sh.prefill);
+    return;
+  }
+  const int w = static_cast<int>(threadIdx.x >> 6);
+  decode_stream_body<G, APPEND, BF16, true>(
+      a, tables, lengths, out, part_o, part_ml, segments, append_slots,
+      static_cast<int>(blockIdx.x - prefix_blocks) * 4 + w, static_cast<int>(threadIdx.x & 63),
+      stream_lds(sh.stream[w]));
 }
 
 // Combines the partials of units that span several stream wavefronts.  One
@@ -1848,6 +1959,32 @@ void launch_stream_variant(const dim3& grid, hipStream_t stream, const DecodeKer
       APPEND ? k.append_slots : nullptr);
 }
 
+template <int G, bool APPEND, bool BF16>
+void launch_cascade_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k,
+                            const prefill_detail::PrefillKernelArgs& prefix,
+                            unsigned prefix_blocks) {
+  cascade_decode_kernel<G, APPEND, BF16><<<grid, 256, 0, stream>>>(
+      k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
+      APPEND ? k.append_slots : nullptr, prefix, prefix_blocks);
+}
+
+template <int G>
+void launch_cascade(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k,
+                    const prefill_detail::PrefillKernelArgs& prefix, unsigned prefix_blocks,
+                    bool append, bool bf16) {
+  if (bf16) {
+    if (append) {
+      launch_cascade_variant<G, true, true>(grid, stream, k, prefix, prefix_blocks);
+    } else {
+      launch_cascade_variant<G, false, true>(grid, stream, k, prefix, prefix_blocks);
+    }
+  } else if (append) {
+    launch_cascade_variant<G, true, false>(grid, stream, k, prefix, prefix_blocks);
+  } else {
+    launch_cascade_variant<G, false, false>(grid, stream, k, prefix, prefix_blocks);
+  }
+}
+
 template <int G>
 void launch_stream(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k, bool append,
                    bool bf16) {
@@ -1890,9 +2027,14 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
   if (streamed) {
-    const bool overlap = a.shared_pages > 0 && a.side_stream != nullptr &&
+    // Cascade in one launch for groups up to kCascadeFusedMaxGroup (the
+    // stream LDS of four wavefronts then fits beside a prefix workgroup's,
+    // two blocks per CU); larger groups run the prefix pass on the side
+    // stream when the caller provides one.
+    const bool fused = a.shared_pages > 0 && group <= kCascadeFusedMaxGroup;
+    const bool overlap = !fused && a.shared_pages > 0 && a.side_stream != nullptr &&
                          a.fork_event != nullptr && a.join_event != nullptr;
-    const std::size_t waves = stream_waves(group, overlap);
+    const std::size_t waves = stream_waves(group, overlap || fused);
     const WorkspaceLayout lay = stream_layout_for(a.batch, a.q_heads, a.kv_heads);
     k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
@@ -1919,6 +2061,35 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
       c.physical_blocks = a.physical_blocks;
       c.prefix_slot0 = static_cast<std::size_t>(k.prefix_slot0);
       c.page_type = a.page_type;
+      if (fused) {
+        std::size_t items = 0;
+        const prefill_detail::PrefillKernelArgs pk = prefill_detail::cascade_prefix_args(c, &items);
+        k.stream_waves = static_cast<int>(waves);
+        const dim3 grid(static_cast<unsigned>(items + waves / 4));
+        const bool append = k.append_slots != nullptr;
+        const bool bf16 = a.page_type == PageType::kBF16;
+        const auto pb = static_cast<unsigned>(items);
+        switch (group) {
+          case 1: launch_cascade<1>(grid, stream, k, pk, pb, append, bf16); break;
+          case 2: launch_cascade<2>(grid, stream, k, pk, pb, append, bf16); break;
+          case 4: launch_cascade<4>(grid, stream, k, pk, pb, append, bf16); break;
+          default: return hipErrorInvalidValue;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        if (a.between_event != nullptr) {
+          e = hipEventRecord(a.between_event, stream);
+          if (e != hipSuccess) return e;
+        }
+        const dim3 mgrid(static_cast<unsigned>(a.batch * a.kv_heads));
+        switch (group) {
+          case 1: decode_stream_merge_kernel<1><<<mgrid, 1 * 32, 0, stream>>>(k); break;
+          case 2: decode_stream_merge_kernel<2><<<mgrid, 2 * 32, 0, stream>>>(k); break;
+          case 4: decode_stream_merge_kernel<4><<<mgrid, 4 * 32, 0, stream>>>(k); break;
+          default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+      }
       if (overlap) {
         hipError_t e = hipEventRecord(a.fork_event, stream);
         if (e == hipSuccess) e = hipStreamWaitEvent(a.side_stream, a.fork_event, 0);

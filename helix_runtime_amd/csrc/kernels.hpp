@@ -226,6 +226,10 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
 // The shared prefix is split into key chunks (each leaving its own partial
 // per unit, at slot prefix_slot0 + chunk * units + unit).
 constexpr std::size_t kMaxCascadeChunks = 16;
+// Query groups up to this size run the cascade prefix pass and the stream
+// kernel as one launch; larger groups put the prefix pass on a side stream
+// (DecodeArgs::side_stream).
+constexpr std::size_t kCascadeFusedMaxGroup = 4;
 std::size_t cascade_chunk_pages(std::size_t shared_pages, std::size_t batch, std::size_t group,
                                 std::size_t kv_heads);
 

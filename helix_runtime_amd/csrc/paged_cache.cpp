@@ -571,8 +571,10 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
     }
     if (shared >= kMinCascadePages) shared_pages_ = shared;
   }
-  if (shared_pages_ > 0 && side_stream_ == nullptr) {
-    // The cascade prefix pass runs on this stream beside the stream kernel.
+  if (shared_pages_ > 0 && side_stream_ == nullptr &&
+      q_heads_ / c.kv_heads > hip::kCascadeFusedMaxGroup) {
+    // Large query groups run the cascade prefix pass on this stream beside
+    // the stream kernel (smaller ones launch both as one kernel).
     hip_check(hipStreamCreateWithFlags(&side_stream_, hipStreamNonBlocking), "hipStreamCreate");
     hip_check(hipEventCreateWithFlags(&fork_event_, hipEventDisableTiming), "hipEventCreate");
     hip_check(hipEventCreateWithFlags(&join_event_, hipEventDisableTiming), "hipEventCreate");
