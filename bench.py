@@ -450,6 +450,17 @@ def prefill_flops(hists, t=CHUNK_TOKENS, hq=HQ, d=D):
     return float(np.sum(4.0 * hq * d * (t * hists + t * (t + 1) / 2.0)))
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch of a workload's dominant kernel(s), measured with
+    the FETCH_SIZE / WRITE_SIZE counters and recorded under profiles/ (the
+    counters cannot be read from inside this process); None when absent."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def run_prefill(args):
     """Config 5: 16 sequences each append a 512-token chunk onto a paged
     history of uniform [0, 4096] tokens, then attend causally (MFMA path).
@@ -592,7 +603,8 @@ def run_prefill(args):
         "append_avg_us": round(float(np.mean(append_ms)) * 1e3, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": MFMA_F32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("prefill_config5" + (
+                         "" if PAGE_DTYPE == "f32" else f"_{PAGE_DTYPE}"))},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -786,12 +798,8 @@ def main():
     append_gbps = append_bytes(nseq) * L / (append_avg_ms * 1e-3) / 1e9
     append_layer_avg_ms = float(np.mean(append_layer_ms))
 
-    traffic = None
     suffix = "" if PAGE_DTYPE == "f32" else f"_{PAGE_DTYPE}"
-    tpath = os.path.join(ROOT, "profiles", f"decode_config{args.config}{suffix}_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = measured_traffic(f"decode_config{args.config}{suffix}")
 
     cpu = None
     if not args.no_cpu and PAGE_DTYPE == "f32":
