@@ -41,7 +41,13 @@ std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
 // parallelism gains (128 sequences x 32 heads: 8 chunks beat both 16 and 4).
 std::size_t cascade_chunk_pages(std::size_t shared_pages, std::size_t batch, std::size_t group,
                                 std::size_t kv_heads) {
-  constexpr std::size_t kCascadeTarget = 256;
+  // Work items the key chunks aim for.  Beside a side-stream stream kernel:
+  // one prefix workgroup per CU.  In the fused launch, where every CU also
+  // holds stream wavefronts, fewer and longer prefix items do better: they
+  // reload fewer query tiles and leave fewer partials to merge (config 4,
+  // 32-layer step: 4 chunks 2.65 ms, 5 chunks 2.62 ms, 6 chunks 2.67 ms,
+  // 8 chunks 2.84 ms, 16 chunks 3.38 ms).
+  const std::size_t kCascadeTarget = group <= kCascadeFusedMaxGroup ? 160 : 256;
   const std::size_t items = ((batch * group + kRows - 1) / kRows) * kv_heads;
   std::size_t chunks = (kCascadeTarget + items - 1) / items;
   if (chunks > kMaxCascadeChunks) chunks = kMaxCascadeChunks;
