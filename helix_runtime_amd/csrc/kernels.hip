@@ -1481,7 +1481,7 @@ void cascade_decode_kernel(
                                                    sh.prefill);
     return;
   }
-  const int w = static_cast<int>(threadIdx.x >> 6);
+  const int w = static_cast<int>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
   decode_stream_body<G, APPEND, BF16, true>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots,
       static_cast<int>(blockIdx.x - prefix_blocks) * 4 + w, static_cast<int>(threadIdx.x & 63),
