@@ -1463,7 +1463,7 @@ void decode_stream_kernel(
 template <int G>
 union CascadeShared {
   StreamShared<G> stream[4];
-  prefill_detail::PrefillShared prefill;
+  prefill_detail::CascadePrefixShared prefill;
 };
 
 template <int G, bool APPEND, bool BF16>

@@ -14,8 +14,10 @@
 // kv head times 128 / G consecutive chunk positions, so every K/V byte
 // staged in LDS feeds all G heads.  Each wavefront holds 32 of those rows
 // (two 16-row tiles) and keeps its Q rows in registers.  Keys stream through
-// a double-buffered LDS stage one page (16 keys) at a time: history pages
-// through the block table, then the chunk rows.
+// LDS one page (16 keys) at a time: history pages through the block table,
+// then the chunk rows.  With fp32 pages the stages are filled by direct
+// global -> LDS loads three blocks ahead; bf16 pages and the cascade
+// prefix pass stage through registers into two stages.
 //
 // Layout trick.  Scores are computed transposed, S^T = K Q^T, so the MFMA
 // result leaves each lane holding 4 keys of one query row; the row's max and
@@ -130,23 +132,68 @@ __device__ __forceinline__ bool finite4(const float4& v) {
 // fp32 kernel's on bf16-exact operands.
 // RT: 16-row tiles per wavefront (1 or 2); the workgroup has 8 / RT waves
 // and each SIMD runs 6 - 2 * RT of them.
-// LDS of one prefill workgroup: the double-buffered K (padded rows) and V
-// stages.
-struct PrefillShared {
+// LDS of one prefill workgroup.  fp32 pages: three K and three V stages
+// filled by direct global -> LDS loads; K rows unpadded with their 16-byte
+// chunks XOR-swizzled by row (chunk j of row r at j ^ (r & 15)), so the
+// MFMA operand reads (16 rows, one chunk) hit distinct banks.  bf16 pages:
+// two register-staged stages (the widening happens on the way), K rows
+// padded to kKStride floats.
+constexpr int kDmaStages = 4;
+struct PrefillRegStages {
   __align__(16) float k[2][kKeys * kKStride];
   __align__(16) float v[2][kKeys * D];
 };
+struct PrefillDmaStages {
+  __align__(16) float k[kDmaStages][kKeys * D];
+  __align__(16) float v[kDmaStages][kKeys * D];
+};
+// The standalone prefill kernel holds either layout; the cascade prefix
+// pass (register staging only) holds just the smaller one.
+struct PrefillShared {
+  union {
+    PrefillDmaStages dma;
+    PrefillRegStages reg;
+  };
+};
+struct CascadePrefixShared {
+  PrefillRegStages reg;
+};
+__device__ __forceinline__ PrefillDmaStages* dma_stages(PrefillShared& s) { return &s.dma; }
+__device__ __forceinline__ PrefillDmaStages* dma_stages(CascadePrefixShared&) { return nullptr; }
+
+// 64 zero float4: the source of the direct loads of rows past the key range.
+__device__ const float4 kZeroRows[64] = {};
+
+// One direct global -> LDS load of 16 bytes per lane: lane i's bytes land at
+// LDS byte address lds + 16 i.  Issued from inline assembly so that the
+// compiler does not order its own LDS reads behind every pending load; the
+// caller waits with an explicit vmcnt before reading the stage and joins
+// the workgroup at a barrier.
+__device__ __forceinline__ void lds_load16(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<std::uintptr_t>(p)));
+}
 
 // The body of one prefill (or cascade prefix) workgroup; `block` is its
 // work-item index (the block index of the standalone kernel).
-template <int G, bool CASCADE, bool BF16, int RT>
+template <int G, bool CASCADE, bool BF16, int RT, class Shared>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
                                              const std::uint32_t* __restrict__ tables,
                                              const std::uint32_t* __restrict__ order,
-                                             std::uint32_t block, PrefillShared& sh) {
+                                             std::uint32_t block, Shared& sh) {
   constexpr int PW = kRows / G;  // chunk positions per workgroup
-  float (&s_k)[2][kKeys * kKStride] = sh.k;
-  float (&s_v)[2][kKeys * D] = sh.v;
+  constexpr bool DMA = !BF16 && !CASCADE;
+  constexpr int kKRow = DMA ? D : kKStride;  // K row stride in LDS
+  PrefillDmaStages* const ds = dma_stages(sh);  // null where DMA is off
+  float (&s_k)[2][kKeys * kKStride] = sh.reg.k;
+  float (&s_v)[2][kKeys * D] = sh.reg.v;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -318,18 +365,113 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
     __syncthreads();
     return 0;
   };
+  // Direct-load staging (fp32 pages).  A block's 8 KiB of K (and of V) is
+  // 8 wave loads of 1 KiB = 2 rows; wave w issues loads w * IPW .. + IPW - 1
+  // of each, lane i covering row 2 c + i / 32, LDS chunk i % 32.
+  constexpr int kWaves = 8 / RT;
+  constexpr int IPW = 8 / kWaves;
+  auto dma_issue = [&](int blk) {
+    const int sbuf = blk % kDmaStages;
+    const int key0 = blk * kKeys;
+    std::size_t page_off = 0;
+    bool page_ok = false;
+    if (key0 < hist) {
+      const std::uint32_t page = table[blk];
+      page_ok = page < a.physical_blocks;
+      bad = bad || !page_ok;
+      page_off = page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
+    }
+    const long long crow = static_cast<long long>(chunk_row0) + key0 - hist;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int c = wave * IPW + i;
+      const int row = 2 * c + (lane >> 5);
+      const int phys = lane & 31;
+      const int key = key0 + row;
+      const bool in_hist = key < hist;
+      const bool valid = key < key_end && (!in_hist || page_ok);
+      const std::size_t rk = in_hist ? page_off + static_cast<std::size_t>(row) * D : 0;
+      const float* kr = in_hist ? a.key_pool + rk : a.chunk_key + (crow + row) * D;
+      const float* vr = in_hist ? a.value_pool + rk : a.chunk_value + (crow + row) * D;
+      const float* ks = valid ? kr + 4 * (phys ^ (row & 15)) : &kZeroRows[lane].x;
+      const float* vs = valid ? vr + 4 * phys : &kZeroRows[lane].x;
+      lds_load16(ks, lds_address(&ds->k[sbuf][c * 256]));
+      lds_load16(vs, lds_address(&ds->v[sbuf][c * 256]));
+    }
+  };
+  // After a block's stage has landed: does a value row that some query row
+  // of the workgroup masks hold a non-finite value?
+  auto dma_nonfinite = [&](int blk) {
+    bool nf = false;
+    const int sbuf = blk % kDmaStages;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int c = wave * IPW + i;
+      const int key = blk * kKeys + 2 * c + (lane >> 5);
+      if (key >= hist + pos0 + 1 && key < key_end) {
+        nf = nf || !finite4(*reinterpret_cast<const float4*>(&ds->v[sbuf][c * 256 + 4 * lane]));
+      }
+    }
+    return nf;
+  };
+  // Wait for this wavefront's loads of block n (those of block n + 1 may
+  // stay in flight), then meet the workgroup; LDS writes of this wave are
+  // complete too.
+  static_assert(kDmaStages == 4, "the waits below keep up to two later blocks in flight");
+  auto dma_wait = [&](int later_in_flight) {
+    if (later_in_flight >= 2) {
+      if constexpr (IPW == 2) {
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    } else if (later_in_flight == 1) {
+      if constexpr (IPW == 2) {
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    } else {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+  };
+
   const int nblocks = (key_end + kKeys - 1) / kKeys;
   const int nfirst = key_begin / kKeys;
   int exact_pv = 0;
-  if (nblocks > nfirst) {
-    stage_load(nfirst);
-    exact_pv = staged_barrier(stage_store(nfirst & 1, nfirst), nfirst);
+  if constexpr (DMA) {
+#pragma unroll
+    for (int i = 0; i < kDmaStages - 1; ++i) {
+      if (nblocks > nfirst + i) dma_issue(nfirst + i);
+    }
+  } else {
+    if (nblocks > nfirst) {
+      stage_load(nfirst);
+      exact_pv = staged_barrier(stage_store(nfirst & 1, nfirst), nfirst);
+    }
   }
   for (int n = nfirst; n < nblocks; ++n) {
-    const int buf = n & 1;
-    if (n + 1 < nblocks) stage_load(n + 1);
-    const float* K = s_k[buf];
-    const float* V = s_v[buf];
+    const float* K;
+    const float* V;
+    if constexpr (DMA) {
+      const int sbuf = n % kDmaStages;
+      dma_wait(min(nblocks - 1 - n, kDmaStages - 2));
+      // Only a block holding chunk rows past the workgroup's first
+      // position can carry a masked value row.
+      exact_pv = 0;
+      if (!CASCADE && n * kKeys + kKeys > hist + pos0 + 1) {
+        exact_pv = __syncthreads_or(dma_nonfinite(n));
+      }
+      // The stage of block n - 1 is free: every wave has passed the barrier.
+      if (n + kDmaStages - 1 < nblocks) dma_issue(n + kDmaStages - 1);
+      K = ds->k[sbuf];
+      V = ds->v[sbuf];
+    } else {
+      const int buf = n & 1;
+      if (n + 1 < nblocks) stage_load(n + 1);
+      K = s_k[buf];
+      V = s_v[buf];
+    }
 
     // S^T = K Q^T: st[t] holds keys 4*grp + i (i = vector component) of
     // query row t*16 + col.
@@ -339,7 +481,8 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       st[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKStride + 16 * c + 4 * grp]);
+        const int kc = DMA ? ((4 * c + grp) ^ (col & 15)) : 4 * c + grp;
+        const float4 kk = *reinterpret_cast<const float4*>(&K[col * kKRow + 4 * kc]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(comp(kk, e), comp(q[t][c], e), st[t], 0,
@@ -441,8 +584,10 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       }
     }
 
-    const bool nonfinite = n + 1 < nblocks && stage_store(buf ^ 1, n + 1);
-    exact_pv = staged_barrier(nonfinite, n + 1);
+    if constexpr (!DMA) {
+      const bool nonfinite = n + 1 < nblocks && stage_store((n & 1) ^ 1, n + 1);
+      exact_pv = staged_barrier(nonfinite, n + 1);
+    }
   }
 
   const int any_bad = __syncthreads_or(bad);
