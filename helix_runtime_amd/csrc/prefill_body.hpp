@@ -170,10 +170,9 @@ __device__ const float4 kZeroRows[64] = {};
 // caller waits with an explicit vmcnt before reading the stage and joins
 // the workgroup at a barrier.
 __device__ __forceinline__ void lds_load16(const void* src, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds)
-               : "memory", "m0");
+  // M0 (the LDS base of the load) is an operand the compiler sets; the
+  // nop is the wait state a write of M0 needs before an LDS-DMA load.
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds) : "memory");
 }
 
 __device__ __forceinline__ unsigned lds_address(const void* p) {
