@@ -7,8 +7,8 @@
 // such as 8'101 give the reference tests' values.
 //
 // Built by tests/cpp/Makefile; run by tests/test_gpu_cpp_api.py on a GPU.
-// Without a GPU every case reports SKIPPED (the CPU suite uses that to check
-// that the binary links and starts).
+// Without a GPU the host-contract cases run and every GPU case reports
+// SKIPPED (the CPU suite runs the binary that way).
 
 #include "helix_paged.hpp"
 #include "mini_test.hpp"
@@ -66,6 +66,9 @@ struct GpuFixture {
     helix_amd::hip::set_device(0);
   }
 };
+struct HostContractTest {
+  void SetUp() {}
+};
 struct HipPagedKvCacheTest : GpuFixture {};
 struct HipAttentionTest : GpuFixture {};
 struct HipDecodeBatchTest : GpuFixture {};
@@ -90,6 +93,43 @@ void expect_error_code(const std::function<void()>& operation, ErrorCode code) {
   } catch (const Error& error) {
     EXPECT_EQ(static_cast<int>(error.code()), static_cast<int>(code));
   }
+}
+
+// ------------------------------------------ host contracts (no GPU needed) ----
+// Validation that happens before any device work, and the status -> Error
+// mapping (include/helix/core/error.hpp:10-17: status = code + 1).
+TEST_F(HostContractTest, InvalidTablesAndConfigsThrowTheReferenceErrorCodes) {
+  constexpr std::array<std::uint32_t, 1> kOutOfRange{3};
+  expect_error_code([] { PagedBlockTable t(std::span<const std::uint32_t>{}, 0, 0); },
+                    ErrorCode::kInvalidArgument);
+  expect_error_code([&] { PagedBlockTable t(kOutOfRange, 3, 0); }, ErrorCode::kOutOfRange);
+  expect_error_code([&] { PagedBlockTable t(kOutOfRange, 4, -1); }, ErrorCode::kInvalidArgument);
+  expect_error_code([] { HipPagedKvCache c(PagedKvCacheConfig{0, 1, 1, 1, 1}); },
+                    ErrorCode::kInvalidArgument);
+  expect_error_code([] { HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, -1); },
+                    ErrorCode::kInvalidArgument);
+  EXPECT_TRUE(error_code_name(ErrorCode::kResourceExhausted) == "ResourceExhausted");
+  try {
+    helix_amd::detail::check(HELIX_OUT_OF_RANGE);
+    FAIL("check() must throw on a non-zero status");
+  } catch (const Error& e) {
+    EXPECT_TRUE(e.code() == ErrorCode::kOutOfRange);
+  }
+}
+
+TEST_F(HostContractTest, HostTensorsReshapeShareStorageAndCheckCounts) {
+  const Tensor t = Tensor::from_values({2, 3}, std::array{1.F, 2.F, 3.F, 4.F, 5.F, 6.F});
+  const Tensor r = t.reshape({3, 2});
+  EXPECT_TRUE(r.data_as<float>() == t.data_as<float>());
+  EXPECT_EQ(r.numel(), 6U);
+  EXPECT_EQ(r.nbytes(), 24U);
+  EXPECT_THROW(static_cast<void>(t.reshape({4, 2})), Error);
+  EXPECT_THROW(static_cast<void>(Tensor::from_values({2, 2}, std::array{1.F, 2.F, 3.F})), Error);
+  const Tensor z = Tensor::zeros({0, 5});
+  EXPECT_EQ(z.numel(), 0U);
+  const HipPagedSequenceHandle empty;
+  EXPECT_FALSE(static_cast<bool>(empty));
+  EXPECT_EQ(empty.native().id, 0U);
 }
 
 // ------------------------------------------------ paged KV cache (device) ----

@@ -1,6 +1,8 @@
 """The C++ mirror (include/helix_paged.hpp) on the CPU: the header compiles
-on its own as C++20, and the C++ API test binary links against the library
-and the oracle and starts (every case reports SKIPPED without a GPU)."""
+on its own as C++20; the C++ API test binary links against the library and
+the oracle, runs its host-contract cases (validation before any device work,
+the status -> helix_amd::Error mapping, host tensors) and skips the GPU
+cases."""
 
 import os
 import subprocess
@@ -21,11 +23,10 @@ def test_header_compiles_standalone(tmp_path):
                     "-I", "/opt/rocm/include", str(src)], check=True)
 
 
-def test_api_binary_links_and_skips_without_gpu():
+def test_api_binary_runs_host_cases_and_skips_gpu_cases():
     if not os.path.exists(BINARY):
         pytest.skip("tests/cpp/paged_api_test is not built (run __graft_entry__.build())")
     env = dict(os.environ, HIP_VISIBLE_DEVICES="")  # no device here; make it explicit
     r = subprocess.run([BINARY], capture_output=True, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "0 ran" in r.stdout and "0 failed" in r.stdout
-    assert r.stdout.count("[  SKIPPED ]") >= 16
+    assert "2 ran, 16 skipped, 0 failed" in r.stdout, r.stdout[-2000:]
