@@ -653,7 +653,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the paged-KV "
-              "hot path shards by KV head or by sequence with no exchange; see DESIGN.md). "
+              "hot path shards by KV head or by sequence with no exchange). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
