@@ -145,36 +145,35 @@ __global__ void append_bulk_kernel(LayerPointers src, S* key_base, S* value_base
 // pools lie layer_stride page elements apart.  The all-layer form is the
 // batched CudaPagedKvCache::append (src/kv_cache/cuda_paged.cpp:491-611),
 // which commits one token's [layers, kv_heads, dim] rows after the forward
-// pass.  I is the index type: 32-bit whenever the element count fits, so
-// the row decomposition costs 32-bit divisions.
-template <typename S, int W, typename I>
-__global__ void append_slots_kernel(const float* __restrict__ keys,
-                                    const float* __restrict__ values, S* key_pool, S* value_pool,
-                                    std::size_t layer_stride, I layers, I heads, I block_tokens,
-                                    I dim, const std::int64_t* __restrict__ slots, I count,
-                                    I tokens) {
-  const I dv = dim / W;
-  const I per_layer = count * heads * tokens * dv;
-  const I total = layers * per_layer;
-  const float* src = blockIdx.y == 0 ? keys : values;
-  S* pool = blockIdx.y == 0 ? key_pool : value_pool;
-  for (I e = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; e < total;
-       e += static_cast<I>(gridDim.x) * blockDim.x) {
-    const I l = e / per_layer;
-    const I r = e - l * per_layer;
-    const I c = r % dv;
-    const I ht = r / dv;
-    const I t = ht % tokens;
-    const I bh = ht / tokens;
-    const I h = bh % heads;
-    const I b = bh / heads;
-    const std::int64_t slot = slots[b * tokens + t];
+// pass.  The (layer, sequence, token) row comes from the workgroup index,
+// so each lane divides only for its (head, vector) pair.
+template <typename S, int W>
+__global__ __launch_bounds__(256) void append_slots_kernel(
+    const float* __restrict__ keys, const float* __restrict__ values, S* key_pool, S* value_pool,
+    std::size_t layer_stride, unsigned heads, unsigned block_tokens, unsigned dim,
+    const std::int64_t* __restrict__ slots, unsigned count, unsigned tokens) {
+  // Grid: x covers one row group's heads * dim / W vectors, y walks the
+  // (sequence, token) rows, z = 2 * layer + (0: K, 1: V).  Everything but
+  // the lane's (head, vector) pair is uniform across the workgroup.
+  const unsigned dv = dim / W;
+  const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= heads * dv) return;
+  const unsigned h = i / dv;
+  const unsigned c = i - h * dv;
+  const bool is_value = (blockIdx.z & 1u) != 0;
+  const std::size_t l = blockIdx.z >> 1;
+  const float* src = is_value ? values : keys;
+  S* pool = (is_value ? value_pool : key_pool) + l * layer_stride;
+  const unsigned rows = count * tokens;
+  for (unsigned bt = blockIdx.y; bt < rows; bt += gridDim.y) {
+    const std::int64_t slot = slots[bt];
     if (slot < 0) continue;
+    const unsigned b = bt / tokens;
+    const unsigned t = bt - b * tokens;
     const std::size_t block = static_cast<std::size_t>(slot) / block_tokens;
     const std::size_t off = static_cast<std::size_t>(slot) % block_tokens;
-    Elems<S, W>::put(pool + l * layer_stride +
-                         ((block * heads + h) * block_tokens + off) * dim + c * W,
-                     src + static_cast<std::size_t>(e) * W);
+    const std::size_t e = (((l * count + b) * heads + h) * tokens + t) * dv + c;
+    Elems<S, W>::put(pool + ((block * heads + h) * block_tokens + off) * dim + c * W, src + e * W);
   }
 }
 
@@ -1773,24 +1772,22 @@ hipError_t launch_append_slots(const float* keys, const float* values, void* key
                                PageType type, std::size_t layers, std::size_t layer_stride) {
   if (count == 0 || tokens == 0 || layers == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
-  const std::size_t work = layers * count * tokens * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
-  const dim3 grid(grid_for(work, kThreads), 2);
-  const bool narrow = work + static_cast<std::size_t>(grid.x) * kThreads < (std::size_t{1} << 32);
+  const std::size_t per_row = g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
+  const std::size_t rows = count * tokens;
+  if (rows > 0xffffffffu || layers * 2 > 65535 || per_row > 0xffffffffu) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid(static_cast<unsigned>((per_row + kThreads - 1) / kThreads),
+                  static_cast<unsigned>(rows < 65535 ? rows : 65535),
+                  static_cast<unsigned>(layers * 2));
   return with_page_type(type, vec, [&](auto s, auto w) {
     using S = decltype(s);
     constexpr int W = decltype(w)::value;
-    auto launch = [&](auto index) {
-      using I = decltype(index);
-      append_slots_kernel<S, W, I><<<grid, kThreads, 0, stream>>>(
-          keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), layer_stride,
-          static_cast<I>(layers), static_cast<I>(g.kv_heads), static_cast<I>(g.block_tokens),
-          static_cast<I>(g.head_dim), slots, static_cast<I>(count), static_cast<I>(tokens));
-    };
-    if (narrow) {
-      launch(0u);
-    } else {
-      launch(std::size_t{0});
-    }
+    append_slots_kernel<S, W><<<grid, kThreads, 0, stream>>>(
+        keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), layer_stride,
+        static_cast<unsigned>(g.kv_heads), static_cast<unsigned>(g.block_tokens),
+        static_cast<unsigned>(g.head_dim), slots, static_cast<unsigned>(count),
+        static_cast<unsigned>(tokens));
   });
 }
 
