@@ -1481,6 +1481,9 @@ void cascade_decode_kernel(
     return;
   }
   const int w = static_cast<int>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+  // The stream wavefronts issue ahead of the prefix wavefronts that share
+  // their SIMDs (the prefix work is short and not on the critical path).
+  __builtin_amdgcn_s_setprio(3);
   decode_stream_body<G, APPEND, BF16, true>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots,
       static_cast<int>(blockIdx.x - prefix_blocks) * 4 + w, static_cast<int>(threadIdx.x & 63),
