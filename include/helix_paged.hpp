@@ -949,6 +949,7 @@ class DecodeBatch final {
 
   void prepare(const hip::Stream& stream) {
     detail::check(helix_decode_batch_prepare(batch_handle_, stream.native()));
+    chunk_ = 0;
   }
   void prepare_chunk(std::size_t tokens, const hip::Stream& stream) {
     detail::check(helix_decode_batch_prepare_chunk(batch_handle_, tokens, stream.native()));
@@ -986,20 +987,32 @@ class DecodeBatch final {
         batch_handle_, layer, query.data_as<float>(), keys.data_as<float>(),
         values.data_as<float>(), output.data<float>(), stream.native()));
   }
+  /// The step's rows of one layer: [B, kv_heads, D] after prepare(),
+  /// [B, kv_heads, T, D] after prepare_chunk(T).
   void append_layer(std::size_t layer, const Tensor& keys, const Tensor& values,
                     const hip::Stream& stream) {
-    rows(keys, "keys", kv_heads_);
-    rows(values, "values", kv_heads_);
+    if (chunk_ == 0) {
+      rows(keys, "keys", kv_heads_);
+      rows(values, "values", kv_heads_);
+    } else {
+      chunk_rows(keys, "chunk keys", kv_heads_);
+      chunk_rows(values, "chunk values", kv_heads_);
+    }
     detail::check(helix_decode_batch_append_layer(batch_handle_, layer, keys.data_as<float>(),
                                                   values.data_as<float>(), stream.native()));
   }
+  /// Every layer's rows: [layers, B, kv_heads, D] after prepare(),
+  /// [layers, B, kv_heads, T, D] after prepare_chunk(T).
   void append_all_layers(const Tensor& keys, const Tensor& values, const hip::Stream& stream) {
     for (const Tensor* t : {&keys, &values}) {
-      detail::require_float_on(*t, device_, 4, "append_all_layers");
+      const std::size_t rank = chunk_ == 0 ? 4 : 5;
+      detail::require_float_on(*t, device_, rank, "append_all_layers");
       detail::require(detail::dim(*t, 0) == layers_ && detail::dim(*t, 1) == batch_ &&
-                          detail::dim(*t, 2) == kv_heads_ && detail::dim(*t, 3) == head_dim_,
+                          detail::dim(*t, 2) == kv_heads_ &&
+                          (chunk_ == 0 || detail::dim(*t, 3) == chunk_) &&
+                          detail::dim(*t, rank - 1) == head_dim_,
                       ErrorCode::kInvalidArgument,
-                      "append_all_layers: rows must be [layers, batch, kv_heads, head_dim]");
+                      "append_all_layers: rows must be [layers, batch, kv_heads, (tokens,) head_dim]");
     }
     detail::check(helix_decode_batch_append_all_layers(batch_handle_, keys.data_as<float>(),
                                                        values.data_as<float>(), stream.native()));

@@ -33,6 +33,13 @@ int oracle_batched_decode(const float* query, std::size_t batch, std::size_t q_h
                           const float* tail_value, float* output, int threads);
 void oracle_random_uniform(std::uint64_t seed, float lower, float upper, float* out,
                            std::size_t n);
+int oracle_paged_attention(const float* query, std::size_t q_heads, std::size_t kv_heads,
+                           std::size_t query_tokens, std::size_t head_dim, std::size_t value_dim,
+                           const float* key_blocks, const float* value_blocks,
+                           std::size_t block_tokens, const std::uint32_t* block_table,
+                           std::size_t history, const float* tail_key, const float* tail_value,
+                           std::size_t tail, std::size_t offset, float* output,
+                           float* workspace);
 }
 
 namespace {
@@ -957,6 +964,128 @@ TEST_F(HipDecodeBatchTest, GqaDecodeStepsMatchOracleAndCommitBitExactly) {
   EXPECT_THROW(batch.append_layer(0, wrong, wrong, stream), Error);
   Tensor rows = Tensor::empty({B, H, D}, DType::kFloat32, kGpu);
   EXPECT_THROW(batch.attention_layer(L, wrong, rows, rows, wrong, stream), Error);
+}
+
+// Extension: a chunked-prefill step through DecodeBatch (prepare_chunk, the
+// chunk rows appended per layer, prefill attention over the pages plus the
+// causal chunk) against the oracle's paged attention with a T-token tail,
+// the chunk gathered back bit-exactly, then a decode step's RoPE at each
+// sequence's position (bit-exact against fp32 arithmetic with every product
+// and sum rounded on its own, cpu::rope_out, src/kernels/cpu/reference.cpp:490-533).
+TEST_F(HipDecodeBatchTest, ChunkStepMatchesOracleAndDecodeRopeUsesPositions) {
+  constexpr std::size_t L = 2, H = 2, HQ = 8, D = 128, P = 16, B = 3, T = 24;
+  const PagedKvCacheConfig config{L, H, D, P, 48};
+  HipPagedKvCache cache(config);
+  Stream stream;
+  const std::array<std::size_t, B> hist{0, 5, 37};
+  std::vector<HipPagedSequenceHandle> seqs;
+  std::vector<std::vector<std::vector<float>>> hk(B), hv(B);  // [b][l] -> [H, n, D]
+  for (std::size_t b = 0; b < B; ++b) {
+    seqs.push_back(cache.create_sequence());
+    const auto n = static_cast<Dimension>(hist[b]);
+    std::vector<Tensor> lk, lv;
+    for (std::size_t l = 0; l < L; ++l) {
+      const Tensor k = random_uniform({H, n, D}, 300 + 10 * b + l, -1, 1);
+      const Tensor v = random_uniform({H, n, D}, 400 + 10 * b + l, -1, 1);
+      hk[b].emplace_back(k.data_as<float>(), k.data_as<float>() + k.numel());
+      hv[b].emplace_back(v.data_as<float>(), v.data_as<float>() + v.numel());
+      lk.push_back(k.to(kGpu));
+      lv.push_back(v.to(kGpu));
+    }
+    if (n != 0) cache.append_layer_major(seqs.back(), lk, lv, stream);
+  }
+  DecodeBatch batch(cache, seqs, HQ, 96);
+  batch.prepare_chunk(T, stream);
+  for (std::size_t l = 0; l < L; ++l) {
+    const Tensor q = random_uniform({B, HQ, T, D}, 500 + l, -1, 1);
+    const Tensor ck = random_uniform({B, H, T, D}, 600 + l, -1, 1);
+    const Tensor cv = random_uniform({B, H, T, D}, 700 + l, -1, 1);
+    const Tensor dk = ck.to(kGpu), dv = cv.to(kGpu);
+    Tensor out = Tensor::empty({B, HQ, T, D}, DType::kFloat32, kGpu);
+    EXPECT_THROW(batch.append_layer(l, random_uniform({B, H, D}, 1, -1, 1).to(kGpu),
+                                    random_uniform({B, H, D}, 2, -1, 1).to(kGpu), stream),
+                 Error);  // decode-step rows after prepare_chunk
+    batch.append_layer(l, dk, dv, stream);
+    batch.prefill_layer(l, q.to(kGpu), dk, dv, out, stream);
+    stream.synchronize();
+    const auto got = host_values(out);
+    for (std::size_t b = 0; b < B; ++b) {
+      const std::size_t n = hist[b];
+      const std::size_t pages = std::max<std::size_t>(1, (n + P - 1) / P);
+      std::vector<float> kb(pages * H * P * D, 0.0F), vb(pages * H * P * D, 0.0F);
+      for (std::size_t h = 0; h < H; ++h)
+        for (std::size_t t = 0; t < n; ++t)
+          for (std::size_t d = 0; d < D; ++d) {
+            const std::size_t dst = (((t / P) * H + h) * P + t % P) * D + d;
+            kb[dst] = hk[b][l][(h * n + t) * D + d];
+            vb[dst] = hv[b][l][(h * n + t) * D + d];
+          }
+      std::vector<std::uint32_t> table(pages);
+      std::iota(table.begin(), table.end(), 0U);
+      std::vector<float> want(HQ * T * D), ws(HQ * T * (n + T));
+      ASSERT_EQ(oracle_paged_attention(q.data_as<float>() + b * HQ * T * D, HQ, H, T, D, D,
+                                       kb.data(), vb.data(), P, table.data(), n,
+                                       ck.data_as<float>() + b * H * T * D,
+                                       cv.data_as<float>() + b * H * T * D, T, n, want.data(),
+                                       ws.data()),
+                0);
+      for (std::size_t i = 0; i < want.size(); ++i) {
+        const float a = got[b * HQ * T * D + i], e = want[i];
+        EXPECT_TRUE(std::fabs(a - e) <= 2.0e-5F + 1.0e-4F * std::fabs(e));
+      }
+      // Fold the chunk into the host history of this layer.
+      for (auto* pair : {&hk, &hv}) {
+        const float* rows = (pair == &hk ? ck : cv).data_as<float>() + b * H * T * D;
+        std::vector<float> grown(H * (n + T) * D);
+        for (std::size_t h = 0; h < H; ++h) {
+          std::copy_n((*pair)[b][l].data() + h * n * D, n * D, grown.data() + h * (n + T) * D);
+          std::copy_n(rows + h * T * D, T * D, grown.data() + (h * (n + T) + n) * D);
+        }
+        (*pair)[b][l] = std::move(grown);
+      }
+    }
+  }
+  for (std::size_t b = 0; b < B; ++b) {
+    const std::size_t n = hist[b] + T;
+    EXPECT_EQ(cache.length(seqs[b]), n);
+    for (std::size_t l = 0; l < L; ++l) {
+      Tensor gk = Tensor::empty({H, static_cast<Dimension>(n), D}, DType::kFloat32, kGpu);
+      Tensor gv = Tensor::empty({H, static_cast<Dimension>(n), D}, DType::kFloat32, kGpu);
+      cache.copy_layer_out(seqs[b], l, gk, gv, stream);
+      stream.synchronize();
+      EXPECT_TRUE(host_values(gk) == hk[b][l]);
+      EXPECT_TRUE(host_values(gv) == hv[b][l]);
+    }
+  }
+
+  // Decode step: RoPE of the step's query and key at each sequence's length.
+  batch.prepare(stream);
+  constexpr std::size_t kRows = 96;
+  const Tensor cosine = random_uniform({kRows, D / 2}, 801, -1, 1);
+  const Tensor sine = random_uniform({kRows, D / 2}, 802, -1, 1);
+  const Tensor qh = random_uniform({B, HQ, D}, 803, -2, 2);
+  const Tensor kh = random_uniform({B, H, D}, 804, -2, 2);
+  Tensor qd = qh.to(kGpu), kd = kh.to(kGpu);
+  batch.rope(qd, kd, cosine.to(kGpu), sine.to(kGpu), stream);
+  stream.synchronize();
+  const auto gq = host_values(qd), gk = host_values(kd);
+  auto check_rope = [&](const Tensor& x, const std::vector<float>& got, std::size_t heads) {
+    for (std::size_t b = 0; b < B; ++b) {
+      const std::size_t pos = hist[b] + T;
+      for (std::size_t h = 0; h < heads; ++h)
+        for (std::size_t i = 0; i < D / 2; ++i) {
+          const std::size_t o = (b * heads + h) * D + 2 * i;
+          const float x0 = x.data_as<float>()[o], x1 = x.data_as<float>()[o + 1];
+          const float c = cosine.data_as<float>()[pos * (D / 2) + i];
+          const float sn = sine.data_as<float>()[pos * (D / 2) + i];
+          const float a = x0 * c, bb = x1 * sn, cc = x0 * sn, dd = x1 * c;
+          EXPECT_EQ(got[o], a - bb);
+          EXPECT_EQ(got[o + 1], cc + dd);
+        }
+    }
+  };
+  check_rope(qh, gq, HQ);
+  check_rope(kh, gk, H);
 }
 
 }  // namespace
