@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <array>
 #include <chrono>
+#include <cstring>
 #include <future>
 #include <limits>
 #include <numeric>
@@ -453,6 +454,65 @@ TEST_F(HipPagedKvCacheTest, ForkBulkAppendAndGatherAreBitExact) {
   cache.release_sequence(child);
   cache.release_sequence(source);
   EXPECT_EQ(cache.stats().used_blocks, 0U);
+}
+
+// Extension: bf16 pages.  An appended fp32 value is stored rounded to the
+// nearest bf16 (ties to even); the gather widens it back exactly, and the
+// read view hands out bf16 pools.
+float bf16_round(float x) {
+  std::uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu) != 0) {
+    u |= 0x00400000u;  // NaN stays (quiet) NaN
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+  }
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+TEST_F(HipPagedKvCacheTest, Bf16PagesRoundOnAppendAndWidenOnGather) {
+  const PagedKvCacheConfig config{2, 2, 8, 4, 8};
+  HipPagedKvCache cache(config, 0, PageDType::kBFloat16);
+  Stream stream;
+  const auto seq = cache.create_sequence();
+  std::vector<std::vector<float>> keys, values;  // per token [L, H, D]
+  for (std::size_t t = 0; t < 6; ++t) {
+    const Tensor k = random_uniform({2, 2, 8}, 900 + t, -3, 3);
+    const Tensor v = random_uniform({2, 2, 8}, 950 + t, -3, 3);
+    keys.emplace_back(k.data_as<float>(), k.data_as<float>() + k.numel());
+    values.emplace_back(v.data_as<float>(), v.data_as<float>() + v.numel());
+    cache.append(seq, k.to(kGpu), v.to(kGpu), stream);
+  }
+  // 1.00390625 = 1 + 2^-8 lies halfway between bf16 1 and 1 + 2^-7: ties to even.
+  const std::vector<float> special(32, 1.00390625F);
+  cache.append(seq, Tensor::from_values({2, 2, 8}, special, kGpu),
+               Tensor::from_values({2, 2, 8}, special, kGpu), stream);
+  keys.push_back(special);
+  values.push_back(special);
+  stream.synchronize();
+  EXPECT_EQ(bf16_round(1.00390625F), 1.0F);
+  {
+    auto view = cache.read_sequence(seq);
+    EXPECT_TRUE(view.layer_key_blocks()[0].dtype() == DType::kBFloat16);
+    EXPECT_EQ(view.length(), 7U);
+  }
+  for (std::size_t l = 0; l < 2; ++l) {
+    Tensor gk = Tensor::empty({2, 7, 8}, DType::kFloat32, kGpu);
+    Tensor gv = Tensor::empty({2, 7, 8}, DType::kFloat32, kGpu);
+    cache.copy_layer_out(seq, l, gk, gv, stream);
+    stream.synchronize();
+    const auto hk = host_values(gk), hv = host_values(gv);
+    for (std::size_t h = 0; h < 2; ++h)
+      for (std::size_t t = 0; t < 7; ++t)
+        for (std::size_t d = 0; d < 8; ++d) {
+          const std::size_t src = (l * 2 + h) * 8 + d;
+          EXPECT_EQ(hk[(h * 7 + t) * 8 + d], bf16_round(keys[t][src]));
+          EXPECT_EQ(hv[(h * 7 + t) * 8 + d], bf16_round(values[t][src]));
+        }
+  }
 }
 
 // Extension: the prefix index over the device cache (prefix.hpp:77-113).
