@@ -164,6 +164,33 @@ def unique_decode_bytes(lengths, shared_tokens=PREFIX_TOKENS, hq=HQ, hkv=HKV, d=
                                ((lengths + p - 1) // p) * 4))
 
 
+# Worker threads of the CPU baseline: one per host core this process may use,
+# at most the GPU box's CPU share per GPU (16; the box may report more cores
+# than one job is given).
+CPU_SHARE = 16
+
+
+def host_cpu():
+    """The host the CPU baseline runs on: logical CPUs, the CPUs this process
+    may run on, the CPU model, and the thread count the baseline uses."""
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        usable = nproc
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:  # pragma: no cover
+        pass
+    return {"nproc": nproc, "usable_cpus": usable, "cpu_model": model,
+            "threads": min(CPU_SHARE, usable)}
+
+
 def cpu_baseline(cache, seqs, layers_multi, layers_single, threads, seed):
     """Times the CPU oracle (C++ restatement of the reference CPU paged
     attention, fp64 accumulation, GQA as replicated MHA) on the bench's own
@@ -214,6 +241,28 @@ def cpu_baseline(cache, seqs, layers_multi, layers_single, threads, seed):
     return rate, max_err
 
 
+_probe_lib = None
+
+
+def probe_lib():
+    """The bench-only probe kernels (libhelix_probe.so, built beside the
+    product library but not part of it)."""
+    global _probe_lib
+    if _probe_lib is None:
+        path = os.path.join(ROOT, "helix_runtime_amd", "libhelix_probe.so")
+        if not os.path.exists(path):
+            raise SystemExit(f"{path} is missing: run `make -C helix_runtime_amd libhelix_probe.so`")
+        _probe_lib = ctypes.CDLL(path)
+        for name in ("helix_probe_stream_read", "helix_probe_page_read"):
+            getattr(_probe_lib, name).restype = ctypes.c_int
+    return _probe_lib
+
+
+def probe_check(rc):
+    if rc != 0:
+        raise SystemExit(f"probe kernel failed with status {rc}")
+
+
 def copy_probe(nbytes=1 << 30, reps=10):
     """Streaming copy of a known size: reads nbytes and writes nbytes per launch."""
     src = torch.randn(nbytes // 4, device="cuda:0")
@@ -234,12 +283,13 @@ def copy_probe(nbytes=1 << 30, reps=10):
     for per_cu in (2, 4, 8, 16, 32):
         blocks = props.multi_processor_count * per_cu
         sink = torch.empty(blocks * 256, device="cuda:0")
-        args = (ctypes.c_void_p(big.data_ptr()), big.numel(), ctypes.c_void_p(sink.data_ptr()),
-                blocks, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        hx.check(hx.load().helix_probe_stream_read(*args))
+        args = (ctypes.c_void_p(big.data_ptr()), ctypes.c_size_t(big.numel()),
+                ctypes.c_void_p(sink.data_ptr()), ctypes.c_uint(blocks),
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        probe_check(probe_lib().helix_probe_stream_read(*args))
         e0.record()
         for _ in range(reps):
-            hx.check(hx.load().helix_probe_stream_read(*args))
+            probe_check(probe_lib().helix_probe_stream_read(*args))
         e1.record()
         torch.cuda.synchronize()
         ms_r = e0.elapsed_time(e1) / reps
@@ -280,13 +330,14 @@ def page_probe(seed, reps=10):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = {"page_probe_pairs": waves * steps, "page_probe_bytes": waves * steps * 2 * P * D * 4}
     for nt in (0, 1):
-        args = (ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(dpairs.data_ptr()), steps, waves,
-                nt, ctypes.c_void_p(sink.data_ptr()),
+        args = (ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(dpairs.data_ptr()),
+                ctypes.c_size_t(steps), ctypes.c_uint(waves), ctypes.c_int(nt),
+                ctypes.c_void_p(sink.data_ptr()),
                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-        hx.check(hx.load().helix_probe_page_read(*args))
+        probe_check(probe_lib().helix_probe_page_read(*args))
         e0.record()
         for _ in range(reps):
-            hx.check(hx.load().helix_probe_page_read(*args))
+            probe_check(probe_lib().helix_probe_page_read(*args))
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
@@ -570,11 +621,15 @@ def run_prefill(args):
                 raise SystemExit(f"prefill parity failure on sequence {b}: max {diff.max()}")
             err = max(err, float(diff.max()))
         cpu_flops = prefill_flops(hists[:nseq])
+        hostinfo = host_cpu()
         cpu = {"value": round(cpu_flops / secs / 1e12, 5), "unit": "TFLOP/s", "cores": nseq,
-               "kind": "port",
-               "sample": f"CPU oracle (fp64 accumulation, GQA as replicated MHA) on layer 0 of "
-                         f"{nseq} of {CHUNK_BATCH} sequences, one thread each, {secs:.1f} s; "
-                         f"GPU matched it to max abs err {err:.2e}"}
+               "kind": "port", "threads": nseq, "nproc": hostinfo["nproc"],
+               "usable_cpus": hostinfo["usable_cpus"], "cpu_model": hostinfo["cpu_model"],
+               "sample": f"CPU oracle (fp64 accumulation) on layer 0 of {nseq} of "
+                         f"{CHUNK_BATCH} sequences, one thread each, {secs:.1f} s; the reference "
+                         f"has no GQA, so the CPU runs GQA as MHA with replicated KV heads (the "
+                         f"FLOP count is the same, each K/V byte is read {HQ // HKV}x); GPU "
+                         f"matched it to max abs err {err:.2e}"}
         del kp, vp, mb
     metric = "chunked-prefill attention TFLOP/s (fp32 MFMA), 8B-GQA 16 x 512-token chunks"
     if PAGE_DTYPE != "f32":
@@ -803,18 +858,26 @@ def main():
 
     cpu = None
     if not args.no_cpu and PAGE_DTYPE == "f32":
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        hostinfo = host_cpu()
+        threads = args.cpu_threads or hostinfo["threads"]
         rate, err = cpu_baseline(cache, seqs, args.cpu_layers, args.cpu_single_layers, threads,
                                  args.seed)
         (gbps, secs), (gbps1, secs1) = rate[threads], rate[1]
         cpu = {"value": round(gbps, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "threads": threads, "nproc": hostinfo["nproc"],
+               "usable_cpus": hostinfo["usable_cpus"], "cpu_model": hostinfo["cpu_model"],
                "single_thread_value": None if gbps1 is None else round(gbps1, 3),
                "sample": f"CPU oracle (C++ restatement of the reference CPU paged attention, "
-                         f"fp64 accumulation, GQA as replicated MHA), {threads} threads over "
-                         f"{args.cpu_layers} layers x all {nseq} sequences ({secs:.1f} s wall), "
-                         f"plus 1 thread over {args.cpu_single_layers} layer(s) ({secs1:.1f} s); "
-                         f"same decode-bytes formula as the GPU; GPU kernel matched it on every "
-                         f"sampled layer, max abs err {err:.2e}"}
+                         f"fp64 accumulation), {threads} threads (one per usable host CPU, "
+                         f"capped at the GPU box's {CPU_SHARE}-CPU share per GPU; host has "
+                         f"{hostinfo['nproc']} logical CPUs, {hostinfo['usable_cpus']} usable) "
+                         f"over {args.cpu_layers} layers x all {nseq} sequences "
+                         f"({secs:.1f} s wall), plus 1 thread (the reference's own mode) over "
+                         f"{args.cpu_single_layers} layer(s) ({secs1:.1f} s). The reference has "
+                         f"no GQA, so the CPU runs GQA as MHA with each KV head replicated for "
+                         f"its {HQ // HKV} query heads: it does {HQ // HKV}x the work per counted "
+                         f"byte, whose formula (each K/V byte once per KV head) is the GPU's. "
+                         f"GPU kernel matched it on every sampled layer, max abs err {err:.2e}"}
 
     if args.config == 4:
         metric = ("prefix-sharing paged decode attn GB/s on unique HBM bytes + append GB/s, "

@@ -533,10 +533,10 @@ def paged_decode_attention(query, key_pool, value_pool, tables, lengths, tail_ke
     if pool_shape is None:
         pool_shape = tuple(key_pool.shape)
         key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
-    n, hkv, _, _ = pool_shape
+    n, hkv, p, d = pool_shape
     check(_lib().helix_paged_decode_attention(
-        _ptr(query), b, hq, hkv, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
-        _ptr(tables),
+        _ptr(query), b, hq, hkv, d, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
+        p, _ptr(tables),
         tables.shape[1], _ptr(lengths), _ptr(tail_key), _ptr(tail_value), _ptr(output),
         _ptr(workspace), workspace.numel() * workspace.element_size(), pages_per_split,
         _stream(stream)))
@@ -560,10 +560,10 @@ def paged_prefill_attention(query, key_pool, value_pool, tables, lengths, chunk_
     if pool_shape is None:
         pool_shape = tuple(key_pool.shape)
         key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
-    n, hkv, _, _ = pool_shape
+    n, hkv, p, d = pool_shape
     check(_lib().helix_paged_prefill_attention(
-        _ptr(query), b, hq, hkv, t, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
-        _ptr(tables), tables.shape[1], _ptr(lengths), _ptr(chunk_key), _ptr(chunk_value),
+        _ptr(query), b, hq, hkv, t, d, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool),
+        n, p, _ptr(tables), tables.shape[1], _ptr(lengths), _ptr(chunk_key), _ptr(chunk_value),
         _ptr(output), _stream(stream)))
 
 

@@ -139,13 +139,13 @@ SIGNATURES = {
     "helix_paged_decode_workspace_bytes": (c_int, [c_size] * 5 + [P(c_size)]),
     "helix_paged_decode_workspace_init": (c_int, [vp, c_size, vp]),
     "helix_paged_decode_attention": (
-        c_int, [vp, c_size, c_size, c_size, vp, vp, c_size, vp, c_size, vp, vp, vp, vp, vp,
-                c_size, c_size, vp]),
+        c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size, vp, vp,
+                vp, vp, vp, c_size, c_size, vp]),
     "helix_paged_append_slots": (
         c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, vp]),
     "helix_paged_prefill_attention": (
-        c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, vp, c_size, vp, vp, vp, vp,
-                vp]),
+        c_int, [vp, c_size, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size,
+                vp, vp, vp, vp, vp]),
     "helix_paged_append_chunk": (
         c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, c_size, vp]),
     "helix_decode_batch_prepare_chunk": (c_int, [vp, c_size, vp]),
@@ -162,8 +162,6 @@ SIGNATURES = {
     "helix_decode_batch_set_timing_event": (c_int, [vp, vp]),
     "helix_decode_batch_shared_pages": (c_int, [vp, P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
-    "helix_probe_stream_read": (c_int, [vp, c_size, vp, ctypes.c_uint, vp]),
-    "helix_probe_page_read": (c_int, [vp, vp, c_size, ctypes.c_uint, c_int, vp, vp]),
     "helix_paged_cache_create_typed": (c_int, [P(Config), c_int, c_int, P(vp)]),
     "helix_paged_cache_page_dtype": (c_int, [vp, P(c_int)]),
     # prefix cache

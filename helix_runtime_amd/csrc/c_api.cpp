@@ -806,6 +806,14 @@ std::size_t resolve_split(std::size_t pages_per_split) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
+// The batched kernels are compiled for one page geometry.
+void require_kernel_geometry(std::size_t head_dim, std::size_t block_tokens, const char* op) {
+  check(head_dim == helix::hip::kDecodeHeadDim && block_tokens == helix::hip::kDecodeBlockTokens,
+        Status::kUnsupported,
+        std::string(op) + ": pools must have head_dim 128 and 16-token pages (got head_dim " +
+            std::to_string(head_dim) + ", " + std::to_string(block_tokens) + "-token pages)");
+}
+
 }  // namespace
 
 int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t kv_heads,
@@ -831,15 +839,16 @@ int helix_paged_decode_workspace_init(void* workspace, size_t workspace_bytes,
 }
 
 int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
-                                 size_t kv_heads, const float* key_blocks,
+                                 size_t kv_heads, size_t head_dim, const float* key_blocks,
                                  const float* value_blocks, size_t physical_blocks,
-                                 const uint32_t* tables, size_t max_blocks,
+                                 size_t block_tokens, const uint32_t* tables, size_t max_blocks,
                                  const int32_t* lengths, const float* tail_key,
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
                                  helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_decode_attention";
+    require_kernel_geometry(head_dim, block_tokens, op);
     check(kv_heads != 0 && q_heads % kv_heads == 0 &&
               helix::hip::decode_group_supported(q_heads / kv_heads),
           Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");
@@ -961,13 +970,15 @@ int helix_paged_append_chunk(const float* keys, const float* values, float* key_
 }
 
 int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_heads,
-                                  size_t kv_heads, size_t tokens, const float* key_blocks,
-                                  const float* value_blocks, size_t physical_blocks,
+                                  size_t kv_heads, size_t tokens, size_t head_dim,
+                                  const float* key_blocks, const float* value_blocks,
+                                  size_t physical_blocks, size_t block_tokens,
                                   const uint32_t* tables, size_t max_blocks,
                                   const int32_t* lengths, const float* chunk_key,
                                   const float* chunk_value, float* output, helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_prefill_attention";
+    require_kernel_geometry(head_dim, block_tokens, op);
     check(kv_heads != 0 && q_heads % kv_heads == 0 &&
               helix::hip::prefill_group_supported(q_heads / kv_heads),
           Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");

@@ -247,6 +247,7 @@ void DevicePagedCache::release(std::uint64_t sequence, std::uint64_t cache_id) {
   std::scoped_lock lock(state_->mutex);
   state_->require_sequence(sequence, cache_id, "release_sequence");
   state_->manager.release(sequence);
+  state_->releases.fetch_add(1, std::memory_order_release);
 }
 
 void DevicePagedCache::copy_layer_out(std::uint64_t sequence, std::uint64_t cache_id,
@@ -396,6 +397,9 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
   tables_ = DeviceBuffer(host.size() * sizeof(std::uint32_t), s.device);
   hip_check(hipMemcpy(tables_.data(), host.data(), tables_.size(), hipMemcpyHostToDevice),
             "decode batch table upload");
+  mirrored_.resize(batch);
+  for (std::size_t i = 0; i < batch; ++i) mirrored_[i] = s.manager.blocks(sequences[i]).size();
+  mirror_ = std::move(host);
   workspace_ = DeviceBuffer(
       hip::decode_workspace_bytes(batch, q_heads, c.kv_heads, max_blocks_, pages_per_split_),
       s.device);
@@ -405,6 +409,7 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
   for (int i = 0; i < 2; ++i) {
     hip_check(hipEventCreateWithFlags(&uploaded_[i], hipEventDisableTiming), "hipEventCreate");
   }
+  hip_check(hipEventCreateWithFlags(&order_event_, hipEventDisableTiming), "hipEventCreate");
   reserve_step(1);
 }
 
@@ -423,7 +428,7 @@ DecodeBatch::~DecodeBatch() {
     (void)hipStreamSynchronize(side_stream_);
     (void)hipStreamDestroy(side_stream_);
   }
-  for (hipEvent_t e : {fork_event_, join_event_}) {
+  for (hipEvent_t e : {fork_event_, join_event_, order_event_}) {
     if (e != nullptr) (void)hipEventDestroy(e);
   }
   if (switched) (void)hipSetDevice(previous);
@@ -441,12 +446,13 @@ const std::int64_t* DecodeBatch::slots() const {
 }
 
 // Step buffers for `tokens` slots per sequence: lengths [B] int32, slots
-// [B, tokens] int64, up to B * (tokens / block_tokens + 1) table updates of
-// 3 words, and for chunks the prefill work-item order, in one device buffer
-// and two pinned staging copies.
+// [B, tokens] int64, up to B * max_blocks table updates of 3 words (a step
+// uploads the entries a member gained since the previous step, inside or
+// outside the batch), and for chunks the prefill work-item order, in one
+// device buffer and two pinned staging copies.
 std::size_t DecodeBatch::order_offset(std::size_t tokens) const {
   const std::size_t B = batch();
-  const std::size_t max_updates = B * (tokens / state_->manager.config().block_tokens + 1);
+  const std::size_t max_updates = B * max_blocks_;
   return align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
          3 * max_updates * sizeof(std::uint32_t);
 }
@@ -472,6 +478,8 @@ void DecodeBatch::reserve_step(std::size_t tokens) {
 void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   CacheState& s = *state_;
   std::scoped_lock lock(s.mutex);
+  prepared_ = false;
+  step_tokens_ = 0;
   s.require_healthy("decode batch prepare");
   const PagedConfig& c = s.manager.config();
   const std::size_t B = batch();
@@ -483,6 +491,8 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
     check(s.manager.contains(sequences_[i]), Status::kInvalidArgument,
           "decode batch sequence was released");
     const std::size_t len = s.manager.length(sequences_[i]);
+    check(s.manager.blocks(sequences_[i]).size() >= mirrored_[i], Status::kInternal,
+          "decode batch table row shrank while the sequence lived");
     check(len + tokens <= max_blocks_ * c.block_tokens, Status::kOutOfRange,
           "decode batch sequence reached the batch's max_tokens");
     new_blocks += (len + tokens + c.block_tokens - 1) / c.block_tokens -
@@ -491,6 +501,13 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   check(new_blocks <= s.manager.free_block_count(), Status::kResourceExhausted,
         "decode batch prepare: the pool has too few free blocks for the step");
   reserve_step(tokens);
+  DeviceGuard guard(s.device);
+  if (any_call_ && last_stream_ != stream) {
+    // The previous step's last call may still read the step buffers and
+    // tables this step rewrites.
+    hip_check(hipEventRecord(order_event_, last_stream_), "decode batch order event");
+    hip_check(hipStreamWaitEvent(stream, order_event_, 0), "decode batch order wait");
+  }
 
   const int which = next_pinned_;
   next_pinned_ ^= 1;
@@ -508,16 +525,18 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
     for (std::size_t t = 0; t < tokens; ++t) {
       slots[i * tokens + t] = static_cast<std::int64_t>(plan.slot(t, c.block_tokens));
     }
-    // Newly allocated blocks are the last new_blocks entries of plan.blocks.
-    const std::size_t first_new = plan.blocks.size() - plan.new_blocks;
-    for (std::size_t k = first_new; k < plan.blocks.size(); ++k) {
+    // Every entry the device row lacks: the pages this step allocated and
+    // any the sequence gained outside the batch since the last step.
+    const std::vector<std::uint32_t>& row = s.manager.blocks(sequences_[i]);
+    for (std::size_t k = mirrored_[i]; k < row.size(); ++k) {
       updates[3 * n_updates] = static_cast<std::uint32_t>(i);
-      updates[3 * n_updates + 1] = static_cast<std::uint32_t>(plan.first_block + k);
-      updates[3 * n_updates + 2] = plan.blocks[k];
+      updates[3 * n_updates + 1] = static_cast<std::uint32_t>(k);
+      updates[3 * n_updates + 2] = row[k];
+      mirror_[i * max_blocks_ + k] = row[k];
       ++n_updates;
     }
+    mirrored_[i] = row.size();
   }
-  DeviceGuard guard(s.device);
   const std::size_t used = align8(B * sizeof(std::int32_t)) + B * tokens * sizeof(std::int64_t) +
                            3 * n_updates * sizeof(std::uint32_t);
   if (tokens > 1) {
@@ -548,13 +567,20 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   }
   hip_check(hipMemcpyAsync(step_.data(), host, used, hipMemcpyHostToDevice, stream),
             "decode batch step upload");
-  hip_check(hipEventRecord(uploaded_[which], stream), "decode batch event");
   items_ = hip::decode_items(host_lengths_.data(), B, c.kv_heads, max_blocks_, pages_per_split_);
   // The updates follow the slots in the device copy of the step buffer.
   const auto* dev_updates = reinterpret_cast<const std::uint32_t*>(this->slots() + B * tokens);
   hip_check(hip::launch_table_updates(static_cast<std::uint32_t*>(tables_.data()), max_blocks_,
                                       dev_updates, n_updates, stream),
             "decode batch table update");
+  // Marks the end of the step's upload: the staging copy may be reused once
+  // it completes, and per-step calls on other streams wait for it.
+  hip_check(hipEventRecord(uploaded_[which], stream), "decode batch event");
+  prepared_event_ = which;
+  prepared_stream_ = stream;
+  last_stream_ = stream;
+  any_call_ = true;
+  prepared_releases_ = s.releases.load(std::memory_order_acquire);
   // Cascade for decode steps: the longest run of leading pages that every
   // sequence shares (same physical IDs, all full before the step) is
   // attended once for the whole batch.
@@ -583,6 +609,26 @@ void DecodeBatch::prepare(hipStream_t stream, std::size_t tokens) {
   prepared_ = true;
 }
 
+void DecodeBatch::begin_call(hipStream_t stream, const char* op) const {
+  check(prepared_, Status::kInvalidArgument, std::string(op) + " before prepare");
+  CacheState& s = *state_;
+  if (s.releases.load(std::memory_order_acquire) != prepared_releases_) {
+    // Something was released since prepare(): the step is only valid if
+    // every member still lives (their pages are the step's).
+    std::scoped_lock lock(s.mutex);
+    for (std::uint64_t seq : sequences_) {
+      check(s.manager.contains(seq), Status::kInvalidArgument,
+            std::string(op) + ": a sequence of the batch was released after prepare");
+    }
+    prepared_releases_ = s.releases.load(std::memory_order_acquire);
+  }
+  if (stream != prepared_stream_) {
+    hip_check(hipStreamWaitEvent(stream, uploaded_[prepared_event_], 0),
+              "decode batch stream order");
+  }
+  last_stream_ = stream;
+}
+
 void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float* values,
                                hipStream_t stream) const {
   const PagedConfig& c = state_->manager.config();
@@ -591,6 +637,7 @@ void DecodeBatch::append_layer(std::size_t layer, const float* keys, const float
   check(keys != nullptr && values != nullptr, Status::kInvalidArgument,
         "decode batch append needs key and value rows");
   DeviceGuard guard(state_->device);
+  begin_call(stream, "decode batch append");
   hip_check(hip::launch_append_slots(keys, values, state_->key_pool(layer),
                                      state_->value_pool(layer),
                                      hip::PageGeometry{c.physical_blocks, c.kv_heads,
@@ -606,6 +653,7 @@ void DecodeBatch::append_all_layers(const float* keys, const float* values,
   check(keys != nullptr && values != nullptr, Status::kInvalidArgument,
         "decode batch append needs key and value rows");
   DeviceGuard guard(state_->device);
+  begin_call(stream, "decode batch append");
   hip_check(hip::launch_append_slots(keys, values, state_->key_pool(0), state_->value_pool(0),
                                      hip::PageGeometry{c.physical_blocks, c.kv_heads,
                                                        c.block_tokens, c.head_dimension},
@@ -624,6 +672,7 @@ void DecodeBatch::rope(float* query, float* key, const float* cosine, const floa
         Status::kInvalidArgument, "decode batch rope needs query, key and the rope tables");
   check(cache_rows != 0, Status::kInvalidArgument, "decode batch rope tables have no rows");
   DeviceGuard guard(state_->device);
+  begin_call(stream, "decode batch rope");
   hip_check(hip::launch_rope(hip::RopeTensor{query, query, q_heads_},
                              hip::RopeTensor{key, key, c.kv_heads}, batch(), c.head_dimension,
                              cosine, sine, cache_rows, lengths(), stream),
@@ -680,6 +729,7 @@ void DecodeBatch::attention_layer(std::size_t layer, const float* query, const f
     a.append_value_pool = state_->value_pool(layer);
   }
   DeviceGuard guard(state_->device);
+  begin_call(stream, "decode batch attention");
   hip_check(hip::launch_decode(a, stream), "decode batch attention launch");
 }
 
@@ -711,6 +761,7 @@ void DecodeBatch::prefill_layer(std::size_t layer, const float* query, const flo
         static_cast<const unsigned char*>(step_.data()) + order_offset(step_tokens_));
   }
   DeviceGuard guard(state_->device);
+  begin_call(stream, "decode batch prefill");
   hip_check(hip::launch_prefill(a, stream), "decode batch prefill launch");
 }
 

@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <memory>
@@ -78,6 +79,10 @@ struct CacheState {
   std::size_t layer_elements = 0;  // physical_blocks * kv_heads * block_tokens * head_dim
   std::mutex mutex;
   bool poisoned = false;
+  // Releases through the cache so far: a DecodeBatch compares it with the
+  // value at its last prepare() to notice that a member may have been
+  // released between the step's calls.
+  std::atomic<std::uint64_t> releases{0};
   DeviceBuffer staging;            // transient upload area (grown on demand)
 
   // Layer pools: fp32 elements, or bf16 bits for a bf16 cache (the pointer
@@ -157,8 +162,20 @@ private:
 // sequence (1 for a decode step, the chunk length for chunked prefill);
 // append_layer() must then write those slots for every layer before the
 // next prepare().  attention_layer() is the one-token decode,
-// prefill_layer() the chunk attention.  Sequences of a live batch must not
-// be released.
+// prefill_layer() the chunk attention.
+//
+// Rules the driver enforces:
+//  - pages a member gains outside the batch (cache.append /
+//    append_layer_major between steps) reach the device tables at the next
+//    prepare(): each prepare() uploads every table entry the device copy
+//    does not hold yet;
+//  - a member released after prepare() makes every later per-step call fail
+//    (kInvalidArgument) until the next prepare(), which fails too;
+//  - a per-step call on a stream other than prepare()'s waits for the step
+//    upload, and prepare() on a stream other than the previous step's last
+//    call waits for that call.  Per-step calls of one step on different
+//    streams are ordered by the caller (the attention calls share one
+//    workspace).
 class DecodeBatch {
 public:
   DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t* sequences,
@@ -232,7 +249,21 @@ private:
   static constexpr std::size_t kMinCascadeBatch = 4;
   static constexpr std::size_t kMinCascadePages = 4;
 
+  // Host mirror of the device tables and the entries of each row that the
+  // device copy holds (table rows only grow while a sequence lives).
+  std::vector<std::uint32_t> mirror_;
+  std::vector<std::size_t> mirrored_;
+  mutable std::uint64_t prepared_releases_ = 0;
+  hipStream_t prepared_stream_ = nullptr;
+  int prepared_event_ = 0;  // uploaded_[prepared_event_] follows the step upload
+  mutable hipStream_t last_stream_ = nullptr;
+  mutable bool any_call_ = false;
+  hipEvent_t order_event_ = nullptr;
+
   void reserve_step(std::size_t tokens);
+  // Checks that the step is prepared and its members still live, and orders
+  // `stream` after the step upload.
+  void begin_call(hipStream_t stream, const char* op) const;
   [[nodiscard]] std::size_t order_offset(std::size_t tokens) const;
   [[nodiscard]] std::size_t prefill_items(std::size_t tokens) const;
 };

@@ -1,8 +1,9 @@
 // HBM streaming-read probe: every thread reads 128-bit vectors in a
 // grid-stride loop (UNROLL loads in flight per thread) and writes one float,
 // so the kernel moves n * 4 bytes from HBM and almost nothing back.  Used by
-// bench.py to measure the attainable read bandwidth of the device.
-#include "../../include/helix_paged.h"
+// bench.py to measure the attainable read bandwidth of the device.  Built
+// into libhelix_probe.so, which only bench.py loads; return codes are 0 (ok),
+// 1 (invalid argument) and 5 (launch failed).
 
 #include <hip/hip_runtime.h>
 
@@ -76,10 +77,10 @@ __global__ __launch_bounds__(64) void page_read_kernel(const float* __restrict__
 
 extern "C" int helix_probe_page_read(const float* pool, const uint32_t* pairs, size_t steps,
                                      unsigned waves, int nontemporal, float* out,
-                                     helix_stream stream) {
+                                     void* stream) {
   if (pool == nullptr || pairs == nullptr || out == nullptr || steps == 0 || waves == 0 ||
       steps > 0x7fffffff) {
-    return HELIX_INVALID_ARGUMENT;
+    return 1;
   }
   const auto s = static_cast<hipStream_t>(stream);
   if (nontemporal != 0) {
@@ -87,15 +88,15 @@ extern "C" int helix_probe_page_read(const float* pool, const uint32_t* pairs, s
   } else {
     page_read_kernel<0><<<waves, 64, 0, s>>>(pool, pairs, static_cast<int>(steps), out);
   }
-  return hipGetLastError() == hipSuccess ? HELIX_OK : HELIX_RUNTIME;
+  return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 
 extern "C" int helix_probe_stream_read(const float* data, size_t n_floats, float* out,
-                                       unsigned blocks, helix_stream stream) {
+                                       unsigned blocks, void* stream) {
   if (data == nullptr || out == nullptr || n_floats % 4 != 0 || blocks == 0) {
-    return HELIX_INVALID_ARGUMENT;
+    return 1;
   }
   stream_read_kernel<8><<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
       reinterpret_cast<const float4*>(data), n_floats / 4, out);
-  return hipGetLastError() == hipSuccess ? HELIX_OK : HELIX_RUNTIME;
+  return hipGetLastError() == hipSuccess ? 0 : 5;
 }

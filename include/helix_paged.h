@@ -250,24 +250,30 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
 
 /* -------------------------------------------- batched decode (extension) ---- */
 /* One-token decode for `batch` sequences at once (the reference runs one
- * sequence per call, docs/ATTENTION.md:317), head_dim 128, 16-token pages,
- * q_heads / kv_heads in {1, 2, 4, 8}:
- *   query [batch, q_heads, 128]; tables [batch, max_blocks] uint32;
- *   lengths [batch] int32 history tokens; tail_key/value [batch, kv_heads, 128];
- *   output [batch, q_heads, 128].
- * Each sequence's history is cut into splits of `pages_per_split` pages (0
- * selects 16; at most 4096 splits per sequence), one wavefront per split;
- * the workspace holds the split partials (calls that overlap on one
- * workspace race).  helix_paged_decode_workspace_init zero-fills a workspace
- * (optional: every call writes the partials it reads). */
+ * sequence per call, docs/ATTENTION.md:317):
+ *   query [batch, q_heads, head_dim];
+ *   key_blocks, value_blocks [physical_blocks, kv_heads, block_tokens, head_dim];
+ *   tables [batch, max_blocks] uint32; lengths [batch] int32 history tokens;
+ *   tail_key/value [batch, kv_heads, head_dim]; output [batch, q_heads, head_dim].
+ * The kernels are built for head_dim 128, 16-token pages and q_heads /
+ * kv_heads in {1, 2, 4, 8}; any other geometry returns HELIX_UNSUPPORTED
+ * before a launch.  pages_per_split 0 (the default) runs the persistent
+ * stream kernel: a fixed grid of wavefronts streams the flat page list of
+ * all (sequence, kv head) units, and a merge launch combines the units that
+ * span wavefronts.  pages_per_split > 0 instead cuts each sequence's history
+ * into splits of that many pages, one wavefront per split (at most 4096
+ * splits per sequence), then merges the splits.  The workspace holds the
+ * partials (calls that overlap on one workspace race).
+ * helix_paged_decode_workspace_init zero-fills a workspace (optional: every
+ * call writes the partials it reads). */
 int helix_paged_decode_workspace_bytes(size_t batch, size_t q_heads, size_t kv_heads,
                                        size_t max_blocks, size_t pages_per_split, size_t* out);
 int helix_paged_decode_workspace_init(void* workspace, size_t workspace_bytes,
                                       helix_stream stream);
 int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
-                                 size_t kv_heads, const float* key_blocks,
+                                 size_t kv_heads, size_t head_dim, const float* key_blocks,
                                  const float* value_blocks, size_t physical_blocks,
-                                 const uint32_t* tables, size_t max_blocks,
+                                 size_t block_tokens, const uint32_t* tables, size_t max_blocks,
                                  const int32_t* lengths, const float* tail_key,
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
@@ -296,13 +302,17 @@ int helix_paged_append_slots(const float* keys, const float* values, float* key_
  * paged_reference.cpp:173-384) for `batch` sequences at once, computed on
  * the matrix cores (fp32 MFMA): query row t of sequence b sees the
  * lengths[b] history tokens of row b of `tables` and chunk rows 0..t.
- * head_dim 128, 16-token pages, q_heads / kv_heads in {1, 2, 4, 8}:
- *   query, output [batch, q_heads, tokens, 128];
- *   chunk_key, chunk_value [batch, kv_heads, tokens, 128];
- *   tables [batch, max_blocks] uint32; lengths [batch] int32. */
+ *   query, output [batch, q_heads, tokens, head_dim];
+ *   key_blocks, value_blocks [physical_blocks, kv_heads, block_tokens, head_dim];
+ *   chunk_key, chunk_value [batch, kv_heads, tokens, head_dim];
+ *   tables [batch, max_blocks] uint32; lengths [batch] int32.
+ * Built for head_dim 128, 16-token pages and q_heads / kv_heads in
+ * {1, 2, 4, 8}; any other geometry returns HELIX_UNSUPPORTED before a
+ * launch. */
 int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_heads,
-                                  size_t kv_heads, size_t tokens, const float* key_blocks,
-                                  const float* value_blocks, size_t physical_blocks,
+                                  size_t kv_heads, size_t tokens, size_t head_dim,
+                                  const float* key_blocks, const float* value_blocks,
+                                  size_t physical_blocks, size_t block_tokens,
                                   const uint32_t* tables, size_t max_blocks,
                                   const int32_t* lengths, const float* chunk_key,
                                   const float* chunk_value, float* output, helix_stream stream);
@@ -436,21 +446,6 @@ int helix_prefix_cache_clear(helix_prefix_cache* prefixes);
 int helix_prefix_cache_stats(helix_prefix_cache* prefixes, helix_prefix_stats* out);
 int helix_prefix_cache_config(helix_prefix_cache* prefixes, helix_prefix_config* out);
 int helix_prefix_cache_block_tokens(helix_prefix_cache* prefixes, size_t* out);
-
-/* ------------------------------------------------------- measurement ---- */
-/* Streaming-read probe (no reference counterpart): reads n_floats floats
- * with 128-bit loads using `blocks` workgroups of 256 threads and writes one
- * float per thread into out (blocks * 256 floats).  bench.py uses it to
- * measure the attainable HBM read bandwidth. */
-int helix_probe_stream_read(const float* data, size_t n_floats, float* out, unsigned blocks,
-                            helix_stream stream);
-/* Page-pair read probe (no reference counterpart): `waves` wavefronts each
- * read `steps` (key chunk, value chunk) pairs of 8 KiB chunks of `pool`,
- * two pairs in flight, as the stream decode kernel does; pairs holds
- * waves * steps * 2 chunk indices (wave-major).  nontemporal != 0 uses the
- * decode kernel's streaming cache policy.  out: waves * 64 floats. */
-int helix_probe_page_read(const float* pool, const uint32_t* pairs, size_t steps, unsigned waves,
-                          int nontemporal, float* out, helix_stream stream);
 
 #ifdef __cplusplus
 }

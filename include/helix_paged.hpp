@@ -947,13 +947,19 @@ class DecodeBatch final {
   DecodeBatch(const DecodeBatch&) = delete;
   DecodeBatch& operator=(const DecodeBatch&) = delete;
 
+  /// A one-token step: append_layer() then takes [B, kv_heads, D] rows and
+  /// prefill_layer() [B, heads, 1, D] rows.
   void prepare(const hip::Stream& stream) {
+    step_tokens_ = 0;  // a failed prepare leaves the batch unprepared
     detail::check(helix_decode_batch_prepare(batch_handle_, stream.native()));
-    chunk_ = 0;
+    step_tokens_ = 1;
+    chunked_ = false;
   }
   void prepare_chunk(std::size_t tokens, const hip::Stream& stream) {
+    step_tokens_ = 0;
     detail::check(helix_decode_batch_prepare_chunk(batch_handle_, tokens, stream.native()));
-    chunk_ = tokens;
+    step_tokens_ = tokens;
+    chunked_ = true;
   }
   void rope(Tensor& query, Tensor& key, const Tensor& cosine, const Tensor& sine,
             const hip::Stream& stream) {
@@ -991,7 +997,7 @@ class DecodeBatch final {
   /// [B, kv_heads, T, D] after prepare_chunk(T).
   void append_layer(std::size_t layer, const Tensor& keys, const Tensor& values,
                     const hip::Stream& stream) {
-    if (chunk_ == 0) {
+    if (!chunked_) {
       rows(keys, "keys", kv_heads_);
       rows(values, "values", kv_heads_);
     } else {
@@ -1005,11 +1011,11 @@ class DecodeBatch final {
   /// [layers, B, kv_heads, T, D] after prepare_chunk(T).
   void append_all_layers(const Tensor& keys, const Tensor& values, const hip::Stream& stream) {
     for (const Tensor* t : {&keys, &values}) {
-      const std::size_t rank = chunk_ == 0 ? 4 : 5;
+      const std::size_t rank = chunked_ ? 5 : 4;
       detail::require_float_on(*t, device_, rank, "append_all_layers");
       detail::require(detail::dim(*t, 0) == layers_ && detail::dim(*t, 1) == batch_ &&
                           detail::dim(*t, 2) == kv_heads_ &&
-                          (chunk_ == 0 || detail::dim(*t, 3) == chunk_) &&
+                          (!chunked_ || detail::dim(*t, 3) == step_tokens_) &&
                           detail::dim(*t, rank - 1) == head_dim_,
                       ErrorCode::kInvalidArgument,
                       "append_all_layers: rows must be [layers, batch, kv_heads, (tokens,) head_dim]");
@@ -1042,16 +1048,20 @@ class DecodeBatch final {
                     ErrorCode::kInvalidArgument, "DecodeBatch: rows must be [batch, heads, head_dim]");
   }
   void chunk_rows(const Tensor& t, const char* what, std::size_t heads) const {
+    detail::require(step_tokens_ != 0, ErrorCode::kInvalidArgument,
+                    "DecodeBatch: prepare() or prepare_chunk() must precede the step's calls");
     detail::require_float_on(t, device_, 4, what);
     detail::require(detail::dim(t, 0) == batch_ && detail::dim(t, 1) == heads &&
-                        detail::dim(t, 2) == chunk_ && detail::dim(t, 3) == head_dim_,
+                        detail::dim(t, 2) == step_tokens_ && detail::dim(t, 3) == head_dim_,
                     ErrorCode::kInvalidArgument,
                     "DecodeBatch: chunk rows must be [batch, heads, tokens, head_dim]");
   }
 
   helix_decode_batch* batch_handle_ = nullptr;
   int device_;
-  std::size_t batch_, q_heads_, kv_heads_, head_dim_, layers_, chunk_ = 0;
+  std::size_t batch_, q_heads_, kv_heads_, head_dim_, layers_;
+  std::size_t step_tokens_ = 0;  // tokens of the prepared step, 0: not prepared
+  bool chunked_ = false;         // prepared by prepare_chunk()
 };
 
 }  // namespace kv_cache

@@ -47,3 +47,38 @@ def test_status_names_and_last_error():
 def test_library_is_gfx950_code_object():
     blob = open(_native.LIB_PATH, "rb").read()
     assert b"gfx950" in blob
+
+
+def declared_arities():
+    text = open(os.path.join(ROOT, "include", "helix_paged.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(helix_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_python_binding_arities_match_the_header():
+    arity = declared_arities()
+    assert set(arity) == set(_native.SIGNATURES)
+    wrong = {n: (len(a), arity[n]) for n, (_, a) in _native.SIGNATURES.items()
+             if len(a) != arity[n]}
+    assert wrong == {}
+
+
+def test_batched_entry_points_reject_other_geometries_before_launch():
+    """A pool of head_dim 64 or 32-token pages is refused with
+    HELIX_UNSUPPORTED before any pointer is read or kernel launched (the
+    pointers here are NULL and no GPU is needed)."""
+    lib = hx.load()
+    for head_dim, block_tokens in ((64, 16), (128, 32), (256, 16)):
+        rc = lib.helix_paged_decode_attention(None, 4, 32, 8, head_dim, None, None, 100,
+                                              block_tokens, None, 8, None, None, None, None,
+                                              None, 1 << 20, 0, None)
+        assert rc == hx.UNSUPPORTED
+        assert b"head_dim 128 and 16-token pages" in lib.helix_last_error()
+        rc = lib.helix_paged_prefill_attention(None, 4, 32, 8, 16, head_dim, None, None, 100,
+                                               block_tokens, None, 8, None, None, None, None,
+                                               None)
+        assert rc == hx.UNSUPPORTED

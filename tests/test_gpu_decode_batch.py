@@ -300,3 +300,174 @@ def test_cascade_shared_prefix_decode(device, hq, mode):
             np.testing.assert_array_equal(host(gk), ok)
             np.testing.assert_array_equal(host(gv), ov)
     batch.close()
+
+
+def _fill(cache, pool, s, so, n, rng):
+    L, H = cache.layers, cache.kv_heads
+    k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+    v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+    cache.append_layer_major(s, [dev(k[l]) for l in range(L)], [dev(v[l]) for l in range(L)])
+    pool.append_layer_major(so, k, v)
+
+
+def _step_checked(batch, cache, pool, seqs, hq, rng, device, stream=None):
+    """One decode step (append_layer + attention_layer per layer) checked
+    against the oracle; the oracle pool takes the same tokens."""
+    L, H, B = cache.layers, cache.kv_heads, len(seqs)
+    batch.prepare(stream)
+    hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+    tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+    for b, (_, so) in enumerate(seqs):
+        t = pool.block_table(so)
+        tables[b, : len(t)] = t
+    keys = rng.standard_normal((L, B, H, D), dtype=np.float32)
+    values = rng.standard_normal((L, B, H, D), dtype=np.float32)
+    for layer in range(L):
+        q = rng.standard_normal((B, hq, D), dtype=np.float32)
+        out = torch.empty(B, hq, D, device=device)
+        batch.append_layer(layer, dev(keys[layer]), dev(values[layer]), stream)
+        batch.attention_layer(layer, dev(q), dev(keys[layer]), dev(values[layer]), out, stream)
+        torch.cuda.synchronize()
+        kp, vp = pool.layer_pages(layer)
+        ref = oracle.batched_decode(q, kp, vp, tables, hist, keys[layer], values[layer],
+                                    threads=8)
+        np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+    for b, (_, so) in enumerate(seqs):
+        pool.append(so, keys[:, b], values[:, b])
+
+
+def test_outside_append_between_steps_reaches_device_tables(device):
+    """A member appended to through the cache between steps (crossing page
+    boundaries) has its new pages in the device tables at the next
+    prepare(): attention reads the right pages and the fused step writes
+    into the right slot."""
+    L, H, HQ = 2, 4, 16
+    rng = np.random.default_rng(91)
+    N = 96
+    cache = hx.PagedKvCache(L, H, D, P, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for n in (5, 16, 30):
+        s, so = cache.create_sequence(), pool.create_sequence()
+        _fill(cache, pool, s, so, n, rng)
+        seqs.append((s, so))
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], HQ, max_tokens=256)
+    _step_checked(batch, cache, pool, seqs, HQ, rng, device)
+    # 40 tokens outside the batch: member 1 (17 tokens) gains three pages.
+    _fill(cache, pool, seqs[1][0], seqs[1][1], 40, rng)
+    # A bystander takes pages in between so a stale entry would point at
+    # someone else's data.
+    other, other_o = cache.create_sequence(), pool.create_sequence()
+    _fill(cache, pool, other, other_o, 33, rng)
+    _step_checked(batch, cache, pool, seqs, HQ, rng, device)
+    _step_checked(batch, cache, pool, seqs, HQ, rng, device)
+    assert cache.stats() == pool.stats()
+    for s, so in seqs:
+        assert cache.block_table(s) == pool.block_table(so).tolist()
+        for layer in range(L):
+            gk, gv = cache.retrieve_layer(s, layer)
+            ok, ov = pool.copy_layer(so, layer)
+            np.testing.assert_array_equal(host(gk), ok)
+            np.testing.assert_array_equal(host(gv), ov)
+    batch.close()
+
+
+def test_release_after_prepare_is_rejected(device):
+    """Releasing a member between prepare() and the step's calls makes every
+    later call of the step, and the next prepare(), fail instead of writing
+    into freed pages; releasing a bystander does not."""
+    cache = hx.PagedKvCache(1, 2, D, P, 32)
+    a, b, c = (cache.create_sequence() for _ in range(3))
+    x = torch.zeros(1, 2, D, device=device)
+    for s in (a, b, c):
+        cache.append(s, x, x)
+    batch = hx.DecodeBatch(cache, [a, b], 4, max_tokens=64)
+    q = torch.zeros(2, 4, D, device=device)
+    rows = torch.zeros(2, 2, D, device=device)
+    out = torch.empty(2, 4, D, device=device)
+    batch.prepare()
+    cache.release_sequence(c)  # not a member: the step stays valid
+    batch.append_attention_layer(0, q, rows, rows, out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    cache.release_sequence(b)
+    for call in (lambda: batch.append_layer(0, rows, rows),
+                 lambda: batch.attention_layer(0, q, rows, rows, out),
+                 lambda: batch.append_attention_layer(0, q, rows, rows, out)):
+        with pytest.raises(hx.HelixError) as e:
+            call()
+        assert e.value.status == hx.INVALID_ARGUMENT
+        assert "released" in str(e.value)
+    with pytest.raises(hx.HelixError):
+        batch.prepare()
+    batch.close()
+
+
+def test_failed_prepare_leaves_batch_unprepared(device):
+    """A prepare() that fails (the pool has no free page for the step) does
+    not leave the previous step usable."""
+    cache = hx.PagedKvCache(1, 2, D, P, 2)
+    s = cache.create_sequence()
+    x = torch.zeros(1, 2, D, device=device)
+    for _ in range(16):
+        cache.append(s, x, x)
+    filler = cache.create_sequence()
+    cache.append(filler, x, x)  # takes the last free page
+    batch = hx.DecodeBatch(cache, [s], 4, max_tokens=64)
+    rows = torch.zeros(1, 2, D, device=device)
+    with pytest.raises(hx.HelixError) as e:
+        batch.prepare()
+    assert e.value.status == hx.RESOURCE_EXHAUSTED
+    with pytest.raises(hx.HelixError) as e:
+        batch.append_layer(0, rows, rows)
+    assert "before prepare" in str(e.value)
+    cache.release_sequence(filler)
+    batch.prepare()
+    batch.append_layer(0, rows, rows)
+    torch.cuda.synchronize()
+    batch.close()
+
+
+def test_step_calls_on_other_streams(device):
+    """prepare() on one stream and the step's calls on another: the calls
+    wait for the step upload, and the next prepare() on the first stream
+    waits for them."""
+    L, H, HQ = 2, 4, 8
+    rng = np.random.default_rng(93)
+    cache = hx.PagedKvCache(L, H, D, P, 64)
+    pool = oracle.PagedPool(L, H, D, P, 64)
+    seqs = []
+    for n in (15, 16, 17, 100):
+        s, so = cache.create_sequence(), pool.create_sequence()
+        _fill(cache, pool, s, so, n, rng)
+        seqs.append((s, so))
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], HQ, max_tokens=256)
+    side = torch.cuda.Stream()
+    B = len(seqs)
+    for step in range(3):
+        hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+        keys = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        values = rng.standard_normal((L, B, H, D), dtype=np.float32)
+        qs = rng.standard_normal((L, B, HQ, D), dtype=np.float32)
+        dk, dvv, dq = dev(keys), dev(values), dev(qs)
+        outs = [torch.empty(B, HQ, D, device=device) for _ in range(L)]
+        torch.cuda.synchronize()
+        # No host synchronisation between the upload and the side stream's
+        # launches: only the library's stream ordering separates them.
+        batch.prepare(torch.cuda.current_stream())
+        for layer in range(L):
+            batch.append_attention_layer(layer, dq[layer], dk[layer], dvv[layer], outs[layer],
+                                         side)
+        side.synchronize()
+        tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+        for b, (_, so) in enumerate(seqs):
+            t = pool.block_table(so)
+            tables[b, : len(t)] = t
+        for layer in range(L):
+            kp, vp = pool.layer_pages(layer)
+            ref = oracle.batched_decode(qs[layer], kp, vp, tables, hist, keys[layer],
+                                        values[layer], threads=8)
+            np.testing.assert_allclose(host(outs[layer]), ref, atol=ATOL, rtol=RTOL)
+        for b, (_, so) in enumerate(seqs):
+            pool.append(so, keys[:, b], values[:, b])
+    batch.close()
