@@ -494,17 +494,23 @@ def paged_attention_out(query, key_blocks, value_blocks, block_table, kv_tokens,
 
 def paged_attention_with_tail_out(query, key_blocks, value_blocks, block_table, history_tokens,
                                   tail_key, tail_value, output, score_workspace, stream=None,
-                                  logical_blocks=None):
+                                  logical_blocks=None, probabilities=False):
+    """paged_scaled_dot_product_attention_with_tail_out.  A one-token decode
+    at head_dim 128 / 16-token pages runs the stream decode kernel and uses
+    score_workspace as scratch (content unspecified afterwards);
+    probabilities=True selects the reference's full workspace contract
+    (helix_paged_attention_with_tail_probabilities_out)."""
     hq, t, kd = query.shape
     n, hkv, p, vd = value_blocks.shape
     table_ptr = block_table.data_ptr() if hasattr(block_table, "data_ptr") else block_table
     if logical_blocks is None:
         logical_blocks = 0 if history_tokens == 0 else (history_tokens - 1) // p + 1
-    check(_lib().helix_paged_attention_with_tail_out(
-        _ptr(query), hq, t, kd, _ptr(key_blocks), _ptr(value_blocks), n, hkv, p, vd,
-        ctypes.c_void_p(table_ptr), logical_blocks, history_tokens, _ptr(tail_key),
-        _ptr(tail_value), _ptr(output), _ptr(score_workspace), score_workspace.numel(),
-        _stream(stream)))
+    fn = (_lib().helix_paged_attention_with_tail_probabilities_out if probabilities
+          else _lib().helix_paged_attention_with_tail_out)
+    check(fn(_ptr(query), hq, t, kd, _ptr(key_blocks), _ptr(value_blocks), n, hkv, p, vd,
+             ctypes.c_void_p(table_ptr), logical_blocks, history_tokens, _ptr(tail_key),
+             _ptr(tail_value), _ptr(output), _ptr(score_workspace), score_workspace.numel(),
+             _stream(stream)))
 
 
 def decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks, pages_per_split=0):

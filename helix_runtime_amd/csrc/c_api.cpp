@@ -683,16 +683,20 @@ int helix_paged_tail_score_workspace_bytes(size_t q_heads, size_t tail_tokens, s
 
 namespace {
 
-void run_reference_attention(const AttentionShape& s, const float* query,
-                             const float* key_blocks, const float* value_blocks,
-                             const std::uint32_t* block_table, const float* tail_key,
-                             const float* tail_value, float* output, float* workspace,
-                             std::size_t workspace_elements, hipStream_t stream, const char* op) {
+// Validates the caller's buffers (workspace shape, non-null pointers, no
+// aliasing) as cuda_paged.cu:211-352 does; false when there is nothing to
+// compute.
+bool validate_reference_buffers(const AttentionShape& s, const float* query,
+                                const float* key_blocks, const float* value_blocks,
+                                const std::uint32_t* block_table, const float* tail_key,
+                                const float* tail_value, const float* output,
+                                const float* workspace, std::size_t workspace_elements,
+                                const char* op) {
   const std::string o(op);
   const std::size_t ws = mul(mul(s.q_heads, s.queries), s.keys);
   check(workspace_elements == ws, Status::kInvalidArgument,
         o + ": score workspace shape does not match [heads, queries, kv tokens]");
-  if (s.queries == 0) return;
+  if (s.queries == 0) return false;
   check(query != nullptr && output != nullptr && workspace != nullptr, Status::kInvalidArgument,
         o + ": query, output and workspace must be non-null device pointers");
   check(s.history == 0 || (key_blocks != nullptr && value_blocks != nullptr &&
@@ -729,6 +733,18 @@ void run_reference_attention(const AttentionShape& s, const float* query,
         o + ": score workspace must not alias tail value");
   check(!overlap(workspace, wb, output, ob), Status::kInvalidArgument,
         o + ": output must not alias score workspace");
+  return true;
+}
+
+void run_reference_attention(const AttentionShape& s, const float* query,
+                             const float* key_blocks, const float* value_blocks,
+                             const std::uint32_t* block_table, const float* tail_key,
+                             const float* tail_value, float* output, float* workspace,
+                             std::size_t workspace_elements, hipStream_t stream, const char* op) {
+  if (!validate_reference_buffers(s, query, key_blocks, value_blocks, block_table, tail_key,
+                                  tail_value, output, workspace, workspace_elements, op)) {
+    return;
+  }
   helix::hip::GenericArgs a{};
   a.query = query;
   a.key_blocks = key_blocks;
@@ -748,7 +764,56 @@ void run_reference_attention(const AttentionShape& s, const float* query,
   a.history = s.history;
   a.tail = s.tail;
   a.offset = s.offset;
-  helix::hip_check(helix::hip::launch_generic(a, stream), (o + " launch").c_str());
+  helix::hip_check(helix::hip::launch_generic(a, stream), (std::string(op) + " launch").c_str());
+}
+
+// The one-token decode through the reference-shaped entry point on the
+// stream kernel: head_dim 128, 16-token pages, a supported query group,
+// 16-byte aligned buffers and a score workspace large enough to hold the
+// partials of at least one wavefront.  The workspace is scratch then.
+// Returns false (nothing launched) when the call does not qualify.
+bool try_stream_decode(const AttentionShape& s, const float* query, const float* key_blocks,
+                       const float* value_blocks, const std::uint32_t* block_table,
+                       const float* tail_key, const float* tail_value, float* output,
+                       float* workspace, std::size_t workspace_elements, hipStream_t stream,
+                       const char* op) {
+  namespace hh = helix::hip;
+  if (s.queries != 1 || s.tail != 1 || s.key_dim != hh::kDecodeHeadDim ||
+      s.value_dim != hh::kDecodeHeadDim || s.block_tokens != hh::kDecodeBlockTokens ||
+      s.kv_heads == 0 || s.q_heads % s.kv_heads != 0 ||
+      !hh::decode_group_supported(s.q_heads / s.kv_heads) ||
+      s.physical > std::numeric_limits<std::uint32_t>::max() ||
+      s.history > static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max() / 2)) {
+    return false;
+  }
+  const auto a16 = [](const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; };
+  if (!a16(query) || !a16(key_blocks) || !a16(value_blocks) || !a16(tail_key) ||
+      !a16(tail_value) || !a16(output) || !a16(workspace)) {
+    return false;
+  }
+  const std::size_t waves =
+      hh::single_decode_waves(s.q_heads, s.kv_heads, workspace_elements * sizeof(float));
+  if (waves == 0) return false;
+  hh::DecodeArgs a{};
+  a.query = query;
+  a.key_pool = key_blocks;
+  a.value_pool = value_blocks;
+  a.tables = block_table;
+  a.lengths = nullptr;
+  a.single_length = static_cast<std::int32_t>(s.history);
+  a.single_waves = waves;
+  a.tail_key = tail_key;
+  a.tail_value = tail_value;
+  a.out = output;
+  a.workspace = workspace;
+  a.batch = 1;
+  a.q_heads = s.q_heads;
+  a.kv_heads = s.kv_heads;
+  a.max_blocks = (s.history + s.block_tokens - 1) / s.block_tokens;
+  a.physical_blocks = s.physical;
+  a.pages_per_split = 0;
+  helix::hip_check(hh::launch_decode(a, stream), (std::string(op) + " launch").c_str());
+  return true;
 }
 
 }  // namespace
@@ -771,6 +836,40 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
   });
 }
 
+namespace {
+
+void attention_with_tail(const float* query, size_t q_heads, size_t tail_tokens, size_t key_dim,
+                         const float* key_blocks, const float* value_blocks,
+                         size_t physical_blocks, size_t kv_heads, size_t block_tokens,
+                         size_t value_dim, const uint32_t* block_table, size_t logical_blocks,
+                         size_t history_tokens, const float* tail_key, const float* tail_value,
+                         float* output, float* score_workspace, size_t workspace_elements,
+                         helix_stream stream, bool probabilities, const char* op) {
+  check(tail_tokens != 0, Status::kInvalidArgument,
+        std::string(op) + ": tail token count must be positive");
+  check(history_tokens <= std::numeric_limits<std::int64_t>::max() - tail_tokens,
+        Status::kResourceExhausted,
+        std::string(op) + ": history plus tail token count overflows shape range");
+  AttentionShape s{q_heads, tail_tokens, key_dim, physical_blocks, kv_heads, block_tokens,
+                   value_dim, logical_blocks, history_tokens, tail_tokens,
+                   history_tokens + tail_tokens, history_tokens};
+  validate_attention(s, true, op);
+  if (!probabilities) {
+    if (!validate_reference_buffers(s, query, key_blocks, value_blocks, block_table, tail_key,
+                                    tail_value, output, score_workspace, workspace_elements, op)) {
+      return;
+    }
+    if (try_stream_decode(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
+                          output, score_workspace, workspace_elements, as_stream(stream), op)) {
+      return;
+    }
+  }
+  run_reference_attention(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
+                          output, score_workspace, workspace_elements, as_stream(stream), op);
+}
+
+}  // namespace
+
 int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size_t tail_tokens,
                                         size_t key_dim, const float* key_blocks,
                                         const float* value_blocks, size_t physical_blocks,
@@ -781,19 +880,26 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
                                         float* score_workspace, size_t workspace_elements,
                                         helix_stream stream) {
   return guarded([&] {
-    constexpr const char* op = "paged_scaled_dot_product_attention_with_tail_out";
-    check(tail_tokens != 0, Status::kInvalidArgument, std::string(op) +
-                                                          ": tail token count must be positive");
-    check(history_tokens <= std::numeric_limits<std::int64_t>::max() - tail_tokens,
-          Status::kResourceExhausted,
-          std::string(op) + ": history plus tail token count overflows shape range");
-    AttentionShape s{q_heads, tail_tokens, key_dim, physical_blocks, kv_heads, block_tokens,
-                     value_dim, logical_blocks, history_tokens, tail_tokens,
-                     history_tokens + tail_tokens, history_tokens};
-    validate_attention(s, true, op);
-    run_reference_attention(s, query, key_blocks, value_blocks, block_table, tail_key,
-                            tail_value, output, score_workspace, workspace_elements,
-                            as_stream(stream), op);
+    attention_with_tail(query, q_heads, tail_tokens, key_dim, key_blocks, value_blocks,
+                        physical_blocks, kv_heads, block_tokens, value_dim, block_table,
+                        logical_blocks, history_tokens, tail_key, tail_value, output,
+                        score_workspace, workspace_elements, stream, false,
+                        "paged_scaled_dot_product_attention_with_tail_out");
+  });
+}
+
+int helix_paged_attention_with_tail_probabilities_out(
+    const float* query, size_t q_heads, size_t tail_tokens, size_t key_dim,
+    const float* key_blocks, const float* value_blocks, size_t physical_blocks, size_t kv_heads,
+    size_t block_tokens, size_t value_dim, const uint32_t* block_table, size_t logical_blocks,
+    size_t history_tokens, const float* tail_key, const float* tail_value, float* output,
+    float* score_workspace, size_t workspace_elements, helix_stream stream) {
+  return guarded([&] {
+    attention_with_tail(query, q_heads, tail_tokens, key_dim, key_blocks, value_blocks,
+                        physical_blocks, kv_heads, block_tokens, value_dim, block_table,
+                        logical_blocks, history_tokens, tail_key, tail_value, output,
+                        score_workspace, workspace_elements, stream, true,
+                        "paged_scaled_dot_product_attention_with_tail_out");
   });
 }
 

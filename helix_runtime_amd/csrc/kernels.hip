@@ -421,6 +421,7 @@ struct DecodeKernelArgs {
   const std::int64_t* append_slots;
   float* append_key_pool;
   float* append_value_pool;
+  int single_length;  // history of the one sequence when lengths is not used
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -915,7 +916,7 @@ __device__ __forceinline__ void stream_sync() {
 
 // The body of one stream wavefront: `wave` is its index among
 // a.stream_waves, `lane` its lane, `sh` its LDS.
-template <int G, bool APPEND, bool BF16, bool SHARED_BLOCK>
+template <int G, bool APPEND, bool BF16, bool SHARED_BLOCK, bool SINGLE = false>
 __device__ __forceinline__ void decode_stream_body(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
@@ -960,7 +961,12 @@ __device__ __forceinline__ void decode_stream_body(
 #pragma unroll
   for (int c = 0; c < kScanChunks; ++c) {
     const int bb = c * 64 + lane;
-    histc[c] = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
+    if constexpr (SINGLE) {
+      // One sequence whose length is a kernel argument.
+      histc[c] = bb < a.batch ? clamp_length(a.single_length, a.max_blocks) : -1;
+    } else {
+      histc[c] = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
+    }
   }
   long long lane_pages = 0;
 #pragma unroll
@@ -969,7 +975,7 @@ __device__ __forceinline__ void decode_stream_body(
     lane_pages += npc[c];
   }
   long long per_head = wave_sum(lane_pages);
-  if (a.batch > kScanChunks * 64) {
+  if (!SINGLE && a.batch > kScanChunks * 64) {
     per_head += stream_pages_between(a, kScanChunks * 64, a.batch, lane);
   }
   per_head = uniform64(per_head);
@@ -1051,7 +1057,8 @@ __device__ __forceinline__ void decode_stream_body(
       }
       if (cur.g < g1) {
         cur.b = __builtin_amdgcn_readfirstlane(cur.b);
-        cur.hist = __builtin_amdgcn_readfirstlane(clamp_length(a.lengths[cur.b], a.max_blocks));
+        cur.hist = __builtin_amdgcn_readfirstlane(
+            clamp_length(SINGLE ? a.single_length : a.lengths[cur.b], a.max_blocks));
         cur.np = unit_pages(cur.hist, a.first_page);
       }
     }
@@ -1429,7 +1436,7 @@ __device__ __forceinline__ void decode_stream_body(
   flush();
 }
 
-template <int G, bool APPEND, bool BF16>
+template <int G, bool APPEND, bool BF16, bool SINGLE = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
 void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
@@ -1446,7 +1453,7 @@ void decode_stream_kernel(
   __shared__ __align__(16) float4 s_app_k[kStreamStage][32];
   __shared__ __align__(16) float4 s_app_v[kStreamStage][32];
   __shared__ long long s_app_dst[kStreamStage];
-  decode_stream_body<G, APPEND, BF16, false>(
+  decode_stream_body<G, APPEND, BF16, false, SINGLE>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
       StreamLds<G>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k, s_app_v,
                    s_app_dst});
@@ -1869,15 +1876,18 @@ WorkspaceLayout layout_for(std::size_t batch, std::size_t q_heads, std::size_t k
 }
 
 // Stream mode: one partial slot per (sequence, kv head) unit plus one per
-// wavefront (slot = unit + wavefront).
-WorkspaceLayout stream_layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads) {
-  // Slots: [0, units + kMaxStreamWaves) stream partials (unit + wavefront),
-  // then kMaxCascadeChunks cascade prefix slots per unit.
-  WorkspaceLayout l = layout_for((1 + kMaxCascadeChunks) * batch * kv_heads + kMaxStreamWaves,
-                                 q_heads / kv_heads, 1, 1);
+// wavefront (slot = unit + wavefront), then `chunks` cascade prefix slots
+// per unit, then the per-unit segment records.
+WorkspaceLayout stream_layout(std::size_t batch, std::size_t q_heads, std::size_t kv_heads,
+                              std::size_t waves, std::size_t chunks) {
+  WorkspaceLayout l = layout_for((1 + chunks) * batch * kv_heads + waves, q_heads / kv_heads, 1, 1);
   l.segments = l.total;
   l.total += align256(batch * kv_heads * 2 * sizeof(int));
   return l;
+}
+
+WorkspaceLayout stream_layout_for(std::size_t batch, std::size_t q_heads, std::size_t kv_heads) {
+  return stream_layout(batch, q_heads, kv_heads, kMaxStreamWaves, kMaxCascadeChunks);
 }
 
 }  // namespace
@@ -1952,9 +1962,9 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix) {
 
 namespace {
 
-template <int G, bool APPEND, bool BF16>
+template <int G, bool APPEND, bool BF16, bool SINGLE = false>
 void launch_stream_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k) {
-  decode_stream_kernel<G, APPEND, BF16><<<grid, 64, 0, stream>>>(
+  decode_stream_kernel<G, APPEND, BF16, SINGLE><<<grid, 64, 0, stream>>>(
       k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
       APPEND ? k.append_slots : nullptr);
 }
@@ -2026,6 +2036,43 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.pages_per_split = static_cast<int>(a.pages_per_split);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
+  if (a.lengths == nullptr) {
+    // One sequence, history length passed by value, the caller's workspace
+    // laid out for single_waves wavefronts.
+    if (a.batch != 1 || !streamed || a.single_waves == 0 || a.shared_pages != 0 ||
+        a.append_slots != nullptr || a.page_type != PageType::kF32) {
+      return hipErrorInvalidValue;
+    }
+    const WorkspaceLayout lay = stream_layout(1, a.q_heads, a.kv_heads, a.single_waves, 0);
+    k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+    k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+    k.segments = reinterpret_cast<int*>(ws + lay.segments);
+    k.single_length = a.single_length;
+    k.stream_waves = static_cast<int>(a.single_waves);
+    const dim3 grid(static_cast<unsigned>(a.single_waves));
+    switch (group) {
+      case 1: launch_stream_variant<1, false, false, true>(grid, stream, k); break;
+      case 2: launch_stream_variant<2, false, false, true>(grid, stream, k); break;
+      case 4: launch_stream_variant<4, false, false, true>(grid, stream, k); break;
+      case 8: launch_stream_variant<8, false, false, true>(grid, stream, k); break;
+      default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (a.between_event != nullptr) {
+      e = hipEventRecord(a.between_event, stream);
+      if (e != hipSuccess) return e;
+    }
+    const dim3 mgrid(static_cast<unsigned>(a.kv_heads));
+    switch (group) {
+      case 1: decode_stream_merge_kernel<1><<<mgrid, 1 * 32, 0, stream>>>(k); break;
+      case 2: decode_stream_merge_kernel<2><<<mgrid, 2 * 32, 0, stream>>>(k); break;
+      case 4: decode_stream_merge_kernel<4><<<mgrid, 4 * 32, 0, stream>>>(k); break;
+      case 8: decode_stream_merge_kernel<8><<<mgrid, 8 * 32, 0, stream>>>(k); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (streamed) {
     // Cascade in one launch for groups up to kCascadeFusedMaxGroup (the
     // stream LDS of four wavefronts then fits beside a prefix workgroup's,
@@ -2167,6 +2214,25 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
+                                std::size_t workspace_bytes) {
+  if (kv_heads == 0 || q_heads % kv_heads != 0) return 0;
+  const std::size_t group = q_heads / kv_heads;
+  std::size_t w = stream_waves(group, false);
+  // The layout grows with the wave count: take the largest count that fits.
+  if (stream_layout(1, q_heads, kv_heads, w, 0).total <= workspace_bytes) return w;
+  std::size_t lo = 0, hi = w;
+  while (lo < hi) {
+    const std::size_t mid = (lo + hi + 1) / 2;
+    if (stream_layout(1, q_heads, kv_heads, mid, 0).total <= workspace_bytes) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  return lo;
 }
 
 hipError_t launch_generic(const GenericArgs& a, hipStream_t stream) {

@@ -142,6 +142,12 @@ struct DecodeArgs {
   const std::int64_t* append_slots = nullptr;
   float* append_key_pool = nullptr;
   float* append_value_pool = nullptr;
+  // One sequence whose history length is a host value (the reference-shaped
+  // entry point): lengths == nullptr, batch == 1, stream mode, no cascade.
+  // The stream kernel then runs `single_waves` wavefronts with the partials
+  // laid out for that count (single_decode_layout) in `workspace`.
+  std::int32_t single_length = 0;
+  std::size_t single_waves = 0;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;
@@ -163,6 +169,11 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 hipError_t launch_decode_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream);
 bool decode_group_supported(std::size_t group);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
+// Stream wavefronts a one-sequence decode can run with a caller workspace of
+// `workspace_bytes` (the partial slots of that many wavefronts must fit),
+// capped at the device's resident count; 0 when none fit.
+std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
+                                std::size_t workspace_bytes);
 
 // ------------------------------------------------------------ generic ----
 // Reference-shaped paged attention for any geometry (one query row per

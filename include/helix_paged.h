@@ -237,7 +237,17 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
                               helix_stream stream);
 /* paged_scaled_dot_product_attention_with_tail_out (cuda_paged.cu:483-548):
  * tail_key [kv_heads, tail_tokens, key_dim], tail_value [kv_heads,
- * tail_tokens, value_dim]; query row q sees the history and tail rows 0..q. */
+ * tail_tokens, value_dim]; query row q sees the history and tail rows 0..q.
+ * The reference model's per-layer decode call (src/model/cuda_llama.cpp:
+ * 365-367).  A one-token decode (tail_tokens 1) with key_dim = value_dim =
+ * 128, 16-token pages, q_heads / kv_heads in {1, 2, 4, 8} and 16-byte aligned
+ * buffers runs on the persistent stream decode kernel when score_workspace
+ * can hold that kernel's partial results for at least one wavefront (from a
+ * history of about 150 tokens on; more history, more wavefronts).  The
+ * workspace is scratch then and its content after the call is unspecified.
+ * Every other call runs the exact reference-shaped kernel, which leaves the
+ * probabilities in the workspace.  Callers that read the probabilities
+ * use helix_paged_attention_with_tail_probabilities_out. */
 int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size_t tail_tokens,
                                         size_t key_dim, const float* key_blocks,
                                         const float* value_blocks, size_t physical_blocks,
@@ -247,6 +257,16 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
                                         const float* tail_value, float* output,
                                         float* score_workspace, size_t workspace_elements,
                                         helix_stream stream);
+/* The same call with the reference's full workspace contract
+ * (cuda_paged.cu:483-548, checked by tests/cuda_attention_test.cpp:443):
+ * score_workspace [q_heads, tail_tokens, history + tail] receives the
+ * attention probabilities whatever the shape. */
+int helix_paged_attention_with_tail_probabilities_out(
+    const float* query, size_t q_heads, size_t tail_tokens, size_t key_dim,
+    const float* key_blocks, const float* value_blocks, size_t physical_blocks, size_t kv_heads,
+    size_t block_tokens, size_t value_dim, const uint32_t* block_table, size_t logical_blocks,
+    size_t history_tokens, const float* tail_key, const float* tail_value, float* output,
+    float* score_workspace, size_t workspace_elements, helix_stream stream);
 
 /* -------------------------------------------- batched decode (extension) ---- */
 /* One-token decode for `batch` sequences at once (the reference runs one

@@ -1194,25 +1194,53 @@ inline void paged_scaled_dot_product_attention_out(
       stream.native()));
 }
 
-/// include/helix/attention/cuda_paged.hpp:49-60: T tail queries at
-/// positions history.. attend over the history pages and, causally, the
-/// uncommitted tail rows; the workspace receives the probabilities.
-inline void paged_scaled_dot_product_attention_with_tail_out(
-    const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,
-    const PagedBlockTable& block_table, std::size_t history_tokens, const Tensor& tail_key,
-    const Tensor& tail_value, Tensor& output, Tensor& score_workspace, const Stream& stream) {
-  const int device = detail::check_operands(query, key_blocks, value_blocks, block_table);
-  detail::check_tail(query, value_blocks, tail_key, tail_value, device);
-  detail::check_output(output, detail::output_shape(query, value_blocks), device,
-                       "paged attention output");
+namespace detail {
+using TailEntry = int (*)(const float*, size_t, size_t, size_t, const float*, const float*,
+                          size_t, size_t, size_t, size_t, const uint32_t*, size_t, size_t,
+                          const float*, const float*, float*, float*, size_t, helix_stream);
+inline void with_tail_out(TailEntry entry, const Tensor& query, const Tensor& key_blocks,
+                          const Tensor& value_blocks, const PagedBlockTable& block_table,
+                          std::size_t history_tokens, const Tensor& tail_key,
+                          const Tensor& tail_value, Tensor& output, Tensor& score_workspace,
+                          const Stream& stream) {
+  const int device = check_operands(query, key_blocks, value_blocks, block_table);
+  check_tail(query, value_blocks, tail_key, tail_value, device);
+  check_output(output, output_shape(query, value_blocks), device, "paged attention output");
   helix_amd::detail::require_float_on(score_workspace, device, 3, "paged attention workspace");
-  helix_amd::detail::check(helix_paged_attention_with_tail_out(
+  helix_amd::detail::check(entry(
       query.data_as<float>(), detail::dim(query, 0), detail::dim(query, 1), detail::dim(query, 2),
       key_blocks.data_as<float>(), value_blocks.data_as<float>(), detail::dim(key_blocks, 0),
       detail::dim(key_blocks, 1), detail::dim(key_blocks, 2), detail::dim(value_blocks, 3),
       block_table.data(), block_table.logical_block_count(), history_tokens,
       tail_key.data_as<float>(), tail_value.data_as<float>(), output.data<float>(),
       score_workspace.data<float>(), score_workspace.numel(), stream.native()));
+}
+}  // namespace detail
+
+/// include/helix/attention/cuda_paged.hpp:49-60: T tail queries at
+/// positions history.. attend over the history pages and, causally, the
+/// uncommitted tail rows.  A one-token decode at head_dim 128 with 16-token
+/// pages runs the stream decode kernel and uses the workspace as scratch
+/// (its content afterwards is unspecified); other shapes leave the
+/// probabilities in it.
+inline void paged_scaled_dot_product_attention_with_tail_out(
+    const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,
+    const PagedBlockTable& block_table, std::size_t history_tokens, const Tensor& tail_key,
+    const Tensor& tail_value, Tensor& output, Tensor& score_workspace, const Stream& stream) {
+  detail::with_tail_out(&helix_paged_attention_with_tail_out, query, key_blocks, value_blocks,
+                        block_table, history_tokens, tail_key, tail_value, output,
+                        score_workspace, stream);
+}
+
+/// The same call with the reference's workspace contract: the workspace
+/// [heads, tail, history + tail] receives the probabilities for every shape.
+inline void paged_scaled_dot_product_attention_with_tail_probabilities_out(
+    const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,
+    const PagedBlockTable& block_table, std::size_t history_tokens, const Tensor& tail_key,
+    const Tensor& tail_value, Tensor& output, Tensor& score_workspace, const Stream& stream) {
+  detail::with_tail_out(&helix_paged_attention_with_tail_probabilities_out, query, key_blocks,
+                        value_blocks, block_table, history_tokens, tail_key, tail_value, output,
+                        score_workspace, stream);
 }
 
 /// include/helix/attention/cuda_paged.hpp:62-69: allocating form; returns
