@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstring>
 #include <limits>
 #include <memory>
@@ -914,10 +915,11 @@ bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15
 
 // The batched kernels are compiled for one page geometry.
 void require_kernel_geometry(std::size_t head_dim, std::size_t block_tokens, const char* op) {
-  check(head_dim == helix::hip::kDecodeHeadDim && block_tokens == helix::hip::kDecodeBlockTokens,
-        Status::kUnsupported,
-        std::string(op) + ": pools must have head_dim 128 and 16-token pages (got head_dim " +
-            std::to_string(head_dim) + ", " + std::to_string(block_tokens) + "-token pages)");
+  if (head_dim != helix::hip::kDecodeHeadDim || block_tokens != helix::hip::kDecodeBlockTokens) {
+    fail(Status::kUnsupported,
+         std::string(op) + ": pools must have head_dim 128 and 16-token pages (got head_dim " +
+             std::to_string(head_dim) + ", " + std::to_string(block_tokens) + "-token pages)");
+  }
 }
 
 }  // namespace
@@ -944,6 +946,112 @@ int helix_paged_decode_workspace_init(void* workspace, size_t workspace_bytes,
   });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Host validation shared by the batched decode entry points (the rules of
+// cuda_paged.cu:211-352 for the batched shapes); false when the batch is
+// empty.
+bool check_decode_call(const char* op, const float* query, size_t batch, size_t q_heads,
+                       size_t kv_heads, size_t head_dim, const float* key_blocks,
+                       const float* value_blocks, size_t physical_blocks, size_t block_tokens,
+                       const uint32_t* tables, size_t max_blocks, const int32_t* lengths,
+                       const float* tail_key, const float* tail_value, const float* output,
+                       size_t split) {
+  require_kernel_geometry(head_dim, block_tokens, op);
+  check(kv_heads != 0 && q_heads % kv_heads == 0 &&
+            helix::hip::decode_group_supported(q_heads / kv_heads),
+        Status::kUnsupported, op, "query groups of 1, 2, 4 or 8 heads only");
+  check(physical_blocks != 0 && physical_blocks <= std::numeric_limits<std::uint32_t>::max(),
+        Status::kInvalidArgument, op, "physical block count out of range");
+  check(max_blocks != 0 && max_blocks <= static_cast<std::size_t>(
+                                             std::numeric_limits<std::int32_t>::max() / 16),
+        Status::kInvalidArgument, op, "max_blocks out of range");
+  check(batch <= static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max()) /
+                     (kv_heads * (max_blocks + 1)),
+        Status::kInvalidArgument, op, "batch too large");
+  if (batch == 0) return false;
+  check(kv_heads * batch * helix::hip::decode_max_splits(max_blocks, split) <= (1u << 30),
+        Status::kInvalidArgument, op, "too many work items");
+  check(helix::hip::decode_max_splits(max_blocks, split) <= helix::hip::kMaxDecodeSplits,
+        Status::kUnsupported, op, "max_blocks / pages_per_split above 4096");
+  check(query && key_blocks && value_blocks && tables && lengths && tail_key && tail_value &&
+            output,
+        Status::kInvalidArgument, op, "device pointers must be non-null");
+  check(aligned16(query) && aligned16(key_blocks) && aligned16(value_blocks) &&
+            aligned16(tail_key) && aligned16(tail_value) && aligned16(output),
+        Status::kInvalidArgument, op, "tensors must be 16-byte aligned");
+  const std::size_t ob = batch * q_heads * helix::hip::kDecodeHeadDim * sizeof(float);
+  check(!overlap(output, ob, query, ob), Status::kInvalidArgument,
+        op, "output must not alias query");
+  return true;
+}
+
+// Largest workspace helix_paged_decode_attention_noalloc can use: the
+// partial results of the stream kernel for (units + wavefronts) slots.
+constexpr std::size_t kNoAllocScratchBytes = std::size_t{16} << 20;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+// The scratch of helix_paged_decode_attention_noalloc.  Every device the
+// library runs that entry point on holds its own copy until the process
+// ends.  In host code `scratch` is only a handle: its device address comes
+// from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on the
+// device's first call; concurrent first calls look it up twice, harmlessly).
+void* scratch_address(const char* op) {
+  int device = -1;
+  helix::hip_check(hipGetDevice(&device), op);
+  check(device >= 0 && device < kMaxDevices, Status::kUnsupported, op,
+        "device index above the scratch table");
+  void* p = g_scratch[device].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    helix::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), op);
+    check(p != nullptr, Status::kRuntime, op, "scratch symbol has no device address");
+    g_scratch[device].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+helix::hip::DecodeArgs decode_args(const float* query, size_t batch, size_t q_heads,
+                                   size_t kv_heads, const float* key_blocks,
+                                   const float* value_blocks, size_t physical_blocks,
+                                   const uint32_t* tables, size_t max_blocks,
+                                   const int32_t* lengths, const float* tail_key,
+                                   const float* tail_value, float* output, void* workspace,
+                                   size_t split) {
+  helix::hip::DecodeArgs a{};
+  a.query = query;
+  a.key_pool = key_blocks;
+  a.value_pool = value_blocks;
+  a.tables = tables;
+  a.lengths = lengths;
+  a.tail_key = tail_key;
+  a.tail_value = tail_value;
+  a.out = output;
+  a.workspace = workspace;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.max_blocks = max_blocks;
+  a.physical_blocks = physical_blocks;
+  a.pages_per_split = split;
+  a.items = 0;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
 int helix_paged_decode_attention(const float* query, size_t batch, size_t q_heads,
                                  size_t kv_heads, size_t head_dim, const float* key_blocks,
                                  const float* value_blocks, size_t physical_blocks,
@@ -954,55 +1062,53 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_decode_attention";
-    require_kernel_geometry(head_dim, block_tokens, op);
-    check(kv_heads != 0 && q_heads % kv_heads == 0 &&
-              helix::hip::decode_group_supported(q_heads / kv_heads),
-          Status::kUnsupported, std::string(op) + ": query groups of 1, 2, 4 or 8 heads only");
-    check(physical_blocks != 0 && physical_blocks <= std::numeric_limits<std::uint32_t>::max(),
-          Status::kInvalidArgument, std::string(op) + ": physical block count out of range");
-    check(max_blocks != 0 && max_blocks <= static_cast<std::size_t>(
-                                               std::numeric_limits<std::int32_t>::max() / 16),
-          Status::kInvalidArgument, std::string(op) + ": max_blocks out of range");
-    check(batch <= static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max()) /
-                       (kv_heads * (max_blocks + 1)),
-          Status::kInvalidArgument, std::string(op) + ": batch too large");
-    if (batch == 0) return;
     const std::size_t split = resolve_split(pages_per_split);
-    check(kv_heads * batch * helix::hip::decode_max_splits(max_blocks, split) <= (1u << 30),
-          Status::kInvalidArgument, std::string(op) + ": too many work items");
-    check(helix::hip::decode_max_splits(max_blocks, split) <= helix::hip::kMaxDecodeSplits,
-          Status::kUnsupported, std::string(op) + ": max_blocks / pages_per_split above 4096");
-    check(query && key_blocks && value_blocks && tables && lengths && tail_key && tail_value &&
-              output && workspace,
-          Status::kInvalidArgument, std::string(op) + ": device pointers must be non-null");
-    check(aligned16(query) && aligned16(key_blocks) && aligned16(value_blocks) &&
-              aligned16(tail_key) && aligned16(tail_value) && aligned16(output) &&
-              aligned16(workspace),
-          Status::kInvalidArgument, std::string(op) + ": tensors must be 16-byte aligned");
+    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, key_blocks,
+                           value_blocks, physical_blocks, block_tokens, tables, max_blocks,
+                           lengths, tail_key, tail_value, output, split)) {
+      return;
+    }
+    check(workspace != nullptr && aligned16(workspace), Status::kInvalidArgument,
+          std::string(op) + ": workspace must be a non-null 16-byte aligned device pointer");
     check(workspace_bytes >=
               helix::hip::decode_workspace_bytes(batch, q_heads, kv_heads, max_blocks, split),
           Status::kInvalidArgument, std::string(op) + ": workspace is too small");
     const std::size_t ob = batch * q_heads * helix::hip::kDecodeHeadDim * sizeof(float);
-    check(!overlap(output, ob, query, ob) && !overlap(output, ob, workspace, workspace_bytes),
-          Status::kInvalidArgument, std::string(op) + ": output must not alias query or workspace");
-    helix::hip::DecodeArgs a{};
-    a.query = query;
-    a.key_pool = key_blocks;
-    a.value_pool = value_blocks;
-    a.tables = tables;
-    a.lengths = lengths;
-    a.tail_key = tail_key;
-    a.tail_value = tail_value;
-    a.out = output;
-    a.workspace = workspace;
-    a.batch = batch;
-    a.q_heads = q_heads;
-    a.kv_heads = kv_heads;
-    a.max_blocks = max_blocks;
-    a.physical_blocks = physical_blocks;
-    a.pages_per_split = split;
-    a.items = 0;
-    helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), "paged_decode_attention");
+    check(!overlap(output, ob, workspace, workspace_bytes), Status::kInvalidArgument,
+          std::string(op) + ": output must not alias query or workspace");
+    const helix::hip::DecodeArgs a =
+        decode_args(query, batch, q_heads, kv_heads, key_blocks, value_blocks, physical_blocks,
+                    tables, max_blocks, lengths, tail_key, tail_value, output, workspace, split);
+    helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), op);
+  });
+}
+
+int helix_paged_decode_attention_noalloc(const float* query, size_t batch, size_t q_heads,
+                                         size_t kv_heads, size_t head_dim,
+                                         const float* key_blocks, const float* value_blocks,
+                                         size_t physical_blocks, size_t block_tokens,
+                                         const uint32_t* tables, size_t max_blocks,
+                                         const int32_t* lengths, const float* tail_key,
+                                         const float* tail_value, float* output,
+                                         helix_stream stream) {
+  return guarded([&] {
+    constexpr const char* op = "paged_decode_attention_noalloc";
+    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, key_blocks,
+                           value_blocks, physical_blocks, block_tokens, tables, max_blocks,
+                           lengths, tail_key, tail_value, output, 0)) {
+      return;
+    }
+    check(helix::hip::compact_decode_workspace_bytes(batch, q_heads, kv_heads) <=
+              kNoAllocScratchBytes,
+          Status::kOutOfRange, op,
+          "batch * kv_heads too large for the 16 MiB scratch (use "
+          "helix_paged_decode_attention with a workspace)");
+    void* ws = scratch_address(op);
+    helix::hip::DecodeArgs a =
+        decode_args(query, batch, q_heads, kv_heads, key_blocks, value_blocks, physical_blocks,
+                    tables, max_blocks, lengths, tail_key, tail_value, output, ws, 0);
+    a.compact_layout = true;
+    helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), op);
   });
 }
 

@@ -2082,7 +2082,10 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const bool overlap = !fused && a.shared_pages > 0 && a.side_stream != nullptr &&
                          a.fork_event != nullptr && a.join_event != nullptr;
     const std::size_t waves = stream_waves(group, overlap || fused);
-    const WorkspaceLayout lay = stream_layout_for(a.batch, a.q_heads, a.kv_heads);
+    if (a.compact_layout && a.shared_pages != 0) return hipErrorInvalidValue;
+    const WorkspaceLayout lay =
+        a.compact_layout ? stream_layout(a.batch, a.q_heads, a.kv_heads, waves, 0)
+                         : stream_layout_for(a.batch, a.q_heads, a.kv_heads);
     k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
     k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
     k.segments = reinterpret_cast<int*>(ws + lay.segments);
@@ -2214,6 +2217,12 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_heads,
+                                           std::size_t kv_heads) {
+  if (kv_heads == 0 || q_heads % kv_heads != 0) return 0;
+  return stream_layout(batch, q_heads, kv_heads, stream_waves(q_heads / kv_heads, false), 0).total;
 }
 
 std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,

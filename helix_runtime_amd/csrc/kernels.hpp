@@ -148,6 +148,10 @@ struct DecodeArgs {
   // laid out for that count (single_decode_layout) in `workspace`.
   std::int32_t single_length = 0;
   std::size_t single_waves = 0;
+  // Stream mode without a cascade: partials laid out for the launch's own
+  // wavefront count (compact_decode_workspace_bytes) instead of the
+  // worst-case layout of decode_workspace_bytes.
+  bool compact_layout = false;
 };
 
 constexpr std::size_t kDecodeHeadDim = 128;
@@ -169,6 +173,9 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 hipError_t launch_decode_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream);
 bool decode_group_supported(std::size_t group);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
+// Workspace of a stream-mode decode with compact_layout (no cascade).
+std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_heads,
+                                           std::size_t kv_heads);
 // Stream wavefronts a one-sequence decode can run with a caller workspace of
 // `workspace_bytes` (the partial slots of that many wavefronts must fit),
 // capped at the device's resident count; 0 when none fit.

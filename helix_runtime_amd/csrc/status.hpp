@@ -38,4 +38,9 @@ inline void check(bool condition, Status status, const std::string& message) {
   if (!condition) fail(status, message);
 }
 
+// "op: what", composed only on failure (no host allocation on success).
+inline void check(bool condition, Status status, const char* op, const char* what) {
+  if (!condition) fail(status, std::string(op) + ": " + what);
+}
+
 }  // namespace helix

@@ -298,6 +298,27 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
                                  helix_stream stream);
+/* helix_paged_decode_attention in stream mode without a workspace argument
+ * and without any allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The stream kernel's
+ * partial results go to a library-owned 16 MiB device array (one per GPU,
+ * held until the process ends); batch * kv_heads beyond what it holds
+ * (about 6000 (sequence, kv head) units at query groups of 4) returns
+ * HELIX_OUT_OF_RANGE.  Every call on one GPU shares that array, so calls
+ * that overlap on one GPU (on different streams, or from several threads
+ * without ordering) race; calls ordered on one stream do not.  Nothing in
+ * the array needs to start at zero: each call writes every partial it
+ * reads.  Same arguments and results as helix_paged_decode_attention with
+ * pages_per_split 0. */
+int helix_paged_decode_attention_noalloc(const float* query, size_t batch, size_t q_heads,
+                                         size_t kv_heads, size_t head_dim,
+                                         const float* key_blocks, const float* value_blocks,
+                                         size_t physical_blocks, size_t block_tokens,
+                                         const uint32_t* tables, size_t max_blocks,
+                                         const int32_t* lengths, const float* tail_key,
+                                         const float* tail_value, float* output,
+                                         helix_stream stream);
 /* kernels::rope / cpu::rope_out (src/kernels/cpu/reference.cpp:490-533):
  * rotates the adjacent pairs (2i, 2i+1) of every head vector, out[2i] =
  * x[2i]*cos - x[2i+1]*sin, out[2i+1] = x[2i]*sin + x[2i+1]*cos, each product

@@ -1,0 +1,85 @@
+"""helix_paged_decode_attention_noalloc (the entry point that allocates
+nothing; its partials live in a library-owned device array) against
+helix_paged_decode_attention with a caller workspace: identical outputs,
+bit for bit, on two calls in a row, the second with a smaller input, and
+both within the north-star tolerance of the oracle."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import helix_runtime_amd as hx
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+D, P = 128, 16
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def problem(seed, batch, hkv, g, max_len):
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(0, max_len + 1, size=batch).astype(np.int32)
+    lengths[0] = max_len
+    pages = (lengths + P - 1) // P
+    phys = int(pages.sum()) + 4
+    perm = rng.permutation(phys).astype(np.uint32)
+    max_blocks = int(pages.max()) + 1
+    tables = np.zeros((batch, max_blocks), np.uint32)
+    at = 0
+    for b, n in enumerate(pages):
+        tables[b, :n] = perm[at: at + n]
+        at += n
+    kp = rng.standard_normal((phys, hkv, P, D), dtype=np.float32)
+    vp = rng.standard_normal((phys, hkv, P, D), dtype=np.float32)
+    q = rng.standard_normal((batch, hkv * g, D), dtype=np.float32)
+    tk = rng.standard_normal((batch, hkv, D), dtype=np.float32)
+    tv = rng.standard_normal((batch, hkv, D), dtype=np.float32)
+    return q, kp, vp, tables, lengths, tk, tv
+
+
+def noalloc(q, kp, vp, tables, lengths, tk, tv, out):
+    b, hq, _ = q.shape
+    n, hkv, p, d = kp.shape
+    p_ = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    return hx.load().helix_paged_decode_attention_noalloc(
+        p_(q), b, hq, hkv, d, p_(kp), p_(vp), n, p, p_(tables), tables.shape[1], p_(lengths),
+        p_(tk), p_(tv), p_(out), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def test_noalloc_matches_workspace_entry_twice_shrinking(device):
+    for seed, batch, hkv, g, max_len in ((1, 24, 8, 4, 3000), (2, 5, 8, 4, 700)):
+        print(f"noalloc case seed={seed} batch={batch} hkv={hkv} g={g} max_len={max_len}",
+              flush=True)
+        q, kp, vp, tables, lengths, tk, tv = problem(seed, batch, hkv, g, max_len)
+        dq, dkp, dvp, dtab, dlen, dtk, dtv = (dev(x) for x in (q, kp, vp, tables.view(np.int32),
+                                                               lengths, tk, tv))
+        want = torch.empty(batch, hkv * g, D, device=device)
+        ws = hx.decode_workspace(batch, hkv * g, hkv, tables.shape[1])
+        hx.paged_decode_attention(dq, dkp, dvp, dtab, dlen, dtk, dtv, want, ws)
+        got = torch.full((batch, hkv * g, D), 7.0, device=device)
+        assert noalloc(dq, dkp, dvp, dtab, dlen, dtk, dtv, got) == 0, \
+            hx.load().helix_last_error()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+        ref = oracle.batched_decode(q, kp, vp, tables, lengths, tk, tv, threads=8)
+        np.testing.assert_allclose(got.cpu().numpy(), ref, atol=2e-5, rtol=1e-4)
+
+
+def test_noalloc_rejects_batches_beyond_its_scratch(device):
+    """More (sequence, kv head) units than the 16 MiB scratch holds are
+    refused before any launch."""
+    q = torch.zeros(4096, 32, D, device=device)
+    out = torch.zeros(4096, 32, D, device=device)
+    x = torch.zeros(16, device=device)
+    p_ = ctypes.c_void_p(x.data_ptr())
+    rc = hx.load().helix_paged_decode_attention_noalloc(
+        ctypes.c_void_p(q.data_ptr()), 4096, 32, 8, D, p_, p_, 100, P, p_, 4, p_, p_, p_,
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == hx.OUT_OF_RANGE
+    assert b"16 MiB scratch" in hx.load().helix_last_error()
