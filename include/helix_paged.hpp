@@ -1108,12 +1108,16 @@ inline void check_tail(const Tensor& query, const Tensor& value_blocks, const Te
                        const Tensor& tail_value, int device) {
   helix_amd::detail::require_float_on(tail_key, device, 3, "paged attention tail key");
   helix_amd::detail::require_float_on(tail_value, device, 3, "paged attention tail value");
-  helix_amd::detail::require(tail_key.shape() == query.shape(), ErrorCode::kInvalidArgument,
-                             "paged attention: tail key must be [H, T, Dk] like the query");
+  // [kv_heads, T, D]: with as many query as kv heads (the reference's only
+  // case) the query's own shape; grouped-query attention is an extension.
   helix_amd::detail::require(
-      dim(tail_value, 0) == dim(query, 0) && dim(tail_value, 1) == dim(query, 1) &&
+      dim(tail_key, 0) == dim(value_blocks, 1) && dim(tail_key, 1) == dim(query, 1) &&
+          dim(tail_key, 2) == dim(query, 2),
+      ErrorCode::kInvalidArgument, "paged attention: tail key must be [Hkv, T, Dk]");
+  helix_amd::detail::require(
+      dim(tail_value, 0) == dim(value_blocks, 1) && dim(tail_value, 1) == dim(query, 1) &&
           dim(tail_value, 2) == dim(value_blocks, 3),
-      ErrorCode::kInvalidArgument, "paged attention: tail value must be [H, T, Dv]");
+      ErrorCode::kInvalidArgument, "paged attention: tail value must be [Hkv, T, Dv]");
 }
 
 inline Shape output_shape(const Tensor& query, const Tensor& value_blocks) {

@@ -1,17 +1,26 @@
-// C++ API tests of libhelix_paged through include/helix_paged.hpp, written
-// after the reference's own CUDA tests (tests/cuda_paged_kv_cache_test.cpp,
-// tests/cuda_attention_test.cpp:196-556): the same cases, inputs, seeds and
-// tolerances, against the HIP path.  Expected attention values come from the
-// CPU oracle (oracle/liboracle.so, linked as the checker only); the seeded
-// inputs use the oracle's restatement of Tensor::random_uniform, so seeds
-// such as 8'101 give the reference tests' values.
+// C++ API tests of libhelix_paged through include/helix_paged.hpp.
 //
-// Built by tests/cpp/Makefile; run by tests/test_gpu_cpp_api.py on a GPU.
-// Without a GPU the host-contract cases run and every GPU case reports
-// SKIPPED (the CPU suite runs the binary that way).
+// The reference's own expectations enter as data: the fixtures under
+// tests/golden/ (the paged-cache scenarios and attention known answers that
+// tests/golden/make_fixtures.py transcribed from the reference's tests, the
+// same files the Python suites replay) are replayed here through the C++
+// API.  Everything else is this repository's own checking: seeded random
+// operation programs against the CPU oracle's pool, a table of invalid
+// calls that must fail before any launch, the read lease, seeded attention
+// sweeps against the oracle, the stream-kernel route of the decode entry
+// point, and the extensions (copy-on-write fork, bulk append, bf16 pages,
+// the prefix cache, DecodeBatch decode and chunk steps).
+//
+// The oracle (oracle/liboracle.so) is linked as the checker only.  Built by
+// tests/cpp/Makefile; run by tests/test_gpu_cpp_api.py on a GPU.  Without a
+// GPU the host-contract cases run and every GPU case reports SKIPPED (the CPU
+// suite runs the binary that way).
 
 #include "helix_paged.hpp"
+#include "json_lite.hpp"
 #include "mini_test.hpp"
+
+#include <unistd.h>
 
 #include <algorithm>
 #include <array>
@@ -19,13 +28,28 @@
 #include <cstring>
 #include <future>
 #include <limits>
+#include <map>
 #include <numeric>
+#include <random>
 #include <type_traits>
 
 extern "C" {
-int oracle_sdpa(const float* query, const float* key, const float* value, std::size_t heads,
-                std::size_t queries, std::size_t keys, std::size_t head_dim,
-                std::size_t value_dim, std::size_t offset, float* output, float* workspace);
+void* oracle_pool_create(std::size_t layers, std::size_t kv_heads, std::size_t head_dim,
+                         std::size_t block_tokens, std::size_t physical_blocks, int* status);
+void oracle_pool_destroy(void* pool);
+std::uint64_t oracle_create_sequence(void* pool);
+int oracle_fork_sequence(void* pool, std::uint64_t source, std::size_t prefix, int allow_cow,
+                         std::uint64_t* out);
+int oracle_append(void* pool, std::uint64_t seq, const float* keys, const float* values);
+int oracle_append_layer_major(void* pool, std::uint64_t seq, const float* keys,
+                              const float* values, std::size_t tokens);
+int oracle_release_sequence(void* pool, std::uint64_t seq);
+std::size_t oracle_length(void* pool, std::uint64_t seq);
+std::size_t oracle_block_table(void* pool, std::uint64_t seq, std::uint32_t* out,
+                               std::size_t capacity);
+void oracle_stats(void* pool, helix_paged_stats* out);
+int oracle_copy_layer(void* pool, std::uint64_t seq, std::size_t layer, float* keys_out,
+                      float* values_out, std::size_t dest_tokens);
 int oracle_batched_decode(const float* query, std::size_t batch, std::size_t q_heads,
                           std::size_t kv_heads, std::size_t head_dim, const float* key_blocks,
                           const float* value_blocks, std::size_t block_tokens,
@@ -47,24 +71,19 @@ namespace {
 
 using namespace helix_amd;
 using namespace helix_amd::kv_cache;
-using helix_amd::attention::hip::paged_scaled_dot_product_attention;
-using helix_amd::attention::hip::paged_scaled_dot_product_attention_out;
-using helix_amd::attention::hip::paged_scaled_dot_product_attention_with_tail;
-using helix_amd::attention::hip::paged_scaled_dot_product_attention_with_tail_out;
-using helix_amd::attention::hip::paged_score_workspace_bytes;
-using helix_amd::attention::hip::paged_tail_score_workspace_bytes;
-using helix_amd::attention::hip::paged_tail_score_workspace_shape;
+namespace attn = helix_amd::attention::hip;
 using PagedBlockTable = helix_amd::kv_cache::hip::PagedBlockTable;
 using Stream = helix_amd::hip::Stream;
+using json_lite::Value;
 
+// The lease and table types keep the reference's ownership rules: neither is
+// copyable, both move without throwing, poisoning cannot throw, and the
+// reference's CUDA spelling names the same class.
 static_assert(!std::is_copy_constructible_v<HipPagedKvCache::DecodeView>);
-static_assert(!std::is_copy_assignable_v<HipPagedKvCache::DecodeView>);
 static_assert(std::is_nothrow_move_constructible_v<HipPagedKvCache::DecodeView>);
-static_assert(std::is_nothrow_move_assignable_v<HipPagedKvCache::DecodeView>);
 static_assert(
     noexcept(std::declval<HipPagedKvCache::DecodeView&>().poison_after_consumer_failure()));
 static_assert(!std::is_copy_constructible_v<PagedBlockTable>);
-static_assert(std::is_nothrow_move_constructible_v<PagedBlockTable>);
 static_assert(std::is_nothrow_move_assignable_v<PagedBlockTable>);
 static_assert(std::is_same_v<CudaPagedKvCache, HipPagedKvCache>);
 
@@ -77,6 +96,7 @@ struct GpuFixture {
 struct HostContractTest {
   void SetUp() {}
 };
+struct GoldenReplayTest : GpuFixture {};
 struct HipPagedKvCacheTest : GpuFixture {};
 struct HipAttentionTest : GpuFixture {};
 struct HipDecodeBatchTest : GpuFixture {};
@@ -94,326 +114,478 @@ Tensor random_uniform(Shape shape, std::uint64_t seed, float lo, float hi) {
   return Tensor::from_values(std::move(shape), v);
 }
 
-void expect_error_code(const std::function<void()>& operation, ErrorCode code) {
+// The ErrorCode a call throws, or nullopt when it returns normally.
+std::optional<ErrorCode> thrown_code(const std::function<void()>& call) {
   try {
-    operation();
-    FAIL("expected helix_amd::Error");
-  } catch (const Error& error) {
-    EXPECT_EQ(static_cast<int>(error.code()), static_cast<int>(code));
+    call();
+  } catch (const Error& e) {
+    return e.code();
   }
+  return std::nullopt;
+}
+
+// tests/golden/<name>, found from this binary's location (tests/cpp/).
+std::string golden_path(const char* name) {
+  std::vector<char> buf(4096, '\0');
+  const ssize_t n = readlink("/proc/self/exe", buf.data(), buf.size() - 1);
+  std::string exe = n > 0 ? std::string(buf.data(), static_cast<std::size_t>(n)) : "";
+  const auto cut = exe.rfind("/cpp/");
+  return (cut == std::string::npos ? std::string("tests") : exe.substr(0, cut)) + "/golden/" +
+         name;
 }
 
 // ------------------------------------------ host contracts (no GPU needed) ----
-// Validation that happens before any device work, and the status -> Error
-// mapping (include/helix/core/error.hpp:10-17: status = code + 1).
-TEST_F(HostContractTest, InvalidTablesAndConfigsThrowTheReferenceErrorCodes) {
-  constexpr std::array<std::uint32_t, 1> kOutOfRange{3};
-  expect_error_code([] { PagedBlockTable t(std::span<const std::uint32_t>{}, 0, 0); },
-                    ErrorCode::kInvalidArgument);
-  expect_error_code([&] { PagedBlockTable t(kOutOfRange, 3, 0); }, ErrorCode::kOutOfRange);
-  expect_error_code([&] { PagedBlockTable t(kOutOfRange, 4, -1); }, ErrorCode::kInvalidArgument);
-  expect_error_code([] { HipPagedKvCache c(PagedKvCacheConfig{0, 1, 1, 1, 1}); },
-                    ErrorCode::kInvalidArgument);
-  expect_error_code([] { HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, -1); },
-                    ErrorCode::kInvalidArgument);
-  EXPECT_TRUE(error_code_name(ErrorCode::kResourceExhausted) == "ResourceExhausted");
-  try {
-    helix_amd::detail::check(HELIX_OUT_OF_RANGE);
-    FAIL("check() must throw on a non-zero status");
-  } catch (const Error& e) {
-    EXPECT_TRUE(e.code() == ErrorCode::kOutOfRange);
+// Every C status maps to the reference's ErrorCode (status = code + 1,
+// include/helix/core/error.hpp:10-17) with the library's message.
+TEST_F(HostContractTest, EveryStatusMapsToItsErrorCode) {
+  const std::array<std::pair<int, std::string_view>, 6> table{{{HELIX_INVALID_ARGUMENT, "InvalidArgument"},
+                                                               {HELIX_OUT_OF_RANGE, "OutOfRange"},
+                                                               {HELIX_UNSUPPORTED, "Unsupported"},
+                                                               {HELIX_RESOURCE_EXHAUSTED, "ResourceExhausted"},
+                                                               {HELIX_RUNTIME, "Runtime"},
+                                                               {HELIX_INTERNAL, "Internal"}}};
+  for (const auto& [status, name] : table) {
+    const auto code = thrown_code([status = status] { helix_amd::detail::check(status); });
+    ASSERT_TRUE(code.has_value());
+    EXPECT_EQ(static_cast<int>(*code) + 1, status);
+    EXPECT_TRUE(error_code_name(*code) == name);
   }
+  EXPECT_FALSE(thrown_code([] { helix_amd::detail::check(HELIX_OK); }).has_value());
+  // Unknown statuses are internal errors.
+  EXPECT_TRUE(thrown_code([] { helix_amd::detail::check(99); }) == ErrorCode::kInternal);
 }
 
-TEST_F(HostContractTest, HostTensorsReshapeShareStorageAndCheckCounts) {
+// Validation that runs before any device work: tables checked against the
+// pool size, cache configurations, handles and host tensors.
+TEST_F(HostContractTest, InvalidArgumentsFailBeforeDeviceWork) {
+  const std::vector<std::uint32_t> ids{0, 5, 2};
+  struct Row {
+    const char* what;
+    std::function<void()> call;
+    ErrorCode code;
+  };
+  const std::vector<Row> rows{
+      {"empty table of an empty pool", [] { PagedBlockTable t(std::span<const std::uint32_t>{}, 0, 0); },
+       ErrorCode::kInvalidArgument},
+      {"page id past the pool", [&] { PagedBlockTable t(ids, 5, 0); }, ErrorCode::kOutOfRange},
+      {"negative device", [&] { PagedBlockTable t(ids, 6, -1); }, ErrorCode::kInvalidArgument},
+      {"zero layers", [] { HipPagedKvCache c(PagedKvCacheConfig{0, 1, 1, 1, 1}); },
+       ErrorCode::kInvalidArgument},
+      {"zero page tokens", [] { HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 0, 1}); },
+       ErrorCode::kInvalidArgument},
+      {"negative device index", [] { HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, -1); },
+       ErrorCode::kInvalidArgument},
+      {"reshape changing the count",
+       [] { static_cast<void>(Tensor::zeros({2, 3}).reshape({4, 2})); },
+       ErrorCode::kInvalidArgument},
+      {"values not matching the shape",
+       [] { static_cast<void>(Tensor::from_values({2, 2}, std::array{1.F, 2.F, 3.F})); },
+       ErrorCode::kInvalidArgument},
+  };
+  for (const Row& r : rows) {
+    const auto code = thrown_code(r.call);
+    if (!code.has_value() || *code != r.code) {
+      ::mini_test::fail(__FILE__, __LINE__, std::string("wrong outcome: ") + r.what);
+    }
+  }
   const Tensor t = Tensor::from_values({2, 3}, std::array{1.F, 2.F, 3.F, 4.F, 5.F, 6.F});
-  const Tensor r = t.reshape({3, 2});
-  EXPECT_TRUE(r.data_as<float>() == t.data_as<float>());
-  EXPECT_EQ(r.numel(), 6U);
-  EXPECT_EQ(r.nbytes(), 24U);
-  EXPECT_THROW(static_cast<void>(t.reshape({4, 2})), Error);
-  EXPECT_THROW(static_cast<void>(Tensor::from_values({2, 2}, std::array{1.F, 2.F, 3.F})), Error);
-  const Tensor z = Tensor::zeros({0, 5});
-  EXPECT_EQ(z.numel(), 0U);
-  const HipPagedSequenceHandle empty;
-  EXPECT_FALSE(static_cast<bool>(empty));
-  EXPECT_EQ(empty.native().id, 0U);
+  EXPECT_TRUE(t.reshape({3, 2}).data_as<float>() == t.data_as<float>());  // shared storage
+  EXPECT_EQ(Tensor::zeros({0, 5}).numel(), 0U);
+  EXPECT_FALSE(static_cast<bool>(HipPagedSequenceHandle{}));
 }
 
-// ------------------------------------------------ paged KV cache (device) ----
-// tests/cuda_paged_kv_cache_test.cpp:40-66
-std::pair<Tensor, Tensor> make_token(const PagedKvCacheConfig& config, std::size_t token) {
-  const std::size_t elements = config.layers * config.kv_heads * config.head_dimension;
-  std::vector<float> keys(elements), values(elements);
-  for (std::size_t layer = 0; layer < config.layers; ++layer)
-    for (std::size_t head = 0; head < config.kv_heads; ++head)
-      for (std::size_t c = 0; c < config.head_dimension; ++c) {
-        const std::size_t index = (layer * config.kv_heads + head) * config.head_dimension + c;
-        const float encoded = static_cast<float>(token * 1000 + layer * 100 + head * 10 + c);
-        keys[index] = encoded + 0.25F;
-        values[index] = -encoded - 0.5F;
+// ------------------------------------------------ golden fixture replay ----
+// tests/golden/paged_cache_scenarios.json: op programs with the reference's
+// expected tables, page contents, lengths, errors and statistics.
+struct ScenarioReplay {
+  explicit ScenarioReplay(const Value& scenario)
+      : config{scenario["config"][0].index(), scenario["config"][1].index(),
+               scenario["config"][2].index(), scenario["config"][3].index(),
+               scenario["config"][4].index()},
+        cache(config) {}
+
+  // token(base)[l, h, c] = base + flat index
+  Tensor encoded_token(double base) const {
+    std::vector<float> v(config.layers * config.kv_heads * config.head_dimension);
+    for (std::size_t i = 0; i < v.size(); ++i) v[i] = static_cast<float>(base + static_cast<double>(i));
+    return Tensor::from_values(shape3(config.layers, config.kv_heads, config.head_dimension), v,
+                               kGpu);
+  }
+  // layer l of a bulk append: [H, count, D] with base + (begin + t) * 100 +
+  // (l * H + h) * D + c
+  std::vector<Tensor> encoded_layers(std::size_t begin, std::size_t count, double base) const {
+    std::vector<Tensor> out;
+    for (std::size_t l = 0; l < config.layers; ++l) {
+      std::vector<float> v(config.kv_heads * count * config.head_dimension);
+      for (std::size_t h = 0; h < config.kv_heads; ++h)
+        for (std::size_t t = 0; t < count; ++t)
+          for (std::size_t c = 0; c < config.head_dimension; ++c)
+            v[(h * count + t) * config.head_dimension + c] = static_cast<float>(
+                base + static_cast<double>((begin + t) * 100 +
+                                           (l * config.kv_heads + h) * config.head_dimension + c));
+      out.push_back(Tensor::from_values(shape3(config.kv_heads, count, config.head_dimension), v,
+                                        kGpu));
+    }
+    return out;
+  }
+  static Shape shape3(std::size_t a, std::size_t b, std::size_t c) {
+    return {static_cast<Dimension>(a), static_cast<Dimension>(b), static_cast<Dimension>(c)};
+  }
+  std::pair<std::vector<float>, std::vector<float>> layer(const std::string& seq, std::size_t l) {
+    const std::size_t n = cache.length(seqs.at(seq));
+    Tensor k = Tensor::empty(shape3(config.kv_heads, n, config.head_dimension), DType::kFloat32, kGpu);
+    Tensor v = Tensor::empty(shape3(config.kv_heads, n, config.head_dimension), DType::kFloat32, kGpu);
+    cache.copy_layer_out(seqs.at(seq), l, k, v, stream);
+    stream.synchronize();
+    return {host_values(k), host_values(v)};
+  }
+  std::size_t stat(const std::string& name) const {
+    const PagedKvCacheStats s = cache.stats();
+    const std::map<std::string, std::size_t> all{
+        {"bytes_reserved", s.bytes_reserved}, {"bytes_used", s.bytes_used},
+        {"bytes_free", s.bytes_free}, {"peak_bytes_used", s.peak_bytes_used},
+        {"total_blocks", s.total_blocks}, {"used_blocks", s.used_blocks},
+        {"free_blocks", s.free_blocks}, {"active_sequence_count", s.active_sequence_count},
+        {"active_tokens", s.active_tokens}, {"resident_tokens", s.resident_tokens},
+        {"allocated_token_slots", s.allocated_token_slots},
+        {"block_reference_count", s.block_reference_count}, {"shared_blocks", s.shared_blocks},
+        {"sequence_create_count", s.sequence_create_count},
+        {"sequence_fork_count", s.sequence_fork_count}, {"append_count", s.append_count},
+        {"release_count", s.release_count}, {"block_allocation_count", s.block_allocation_count},
+        {"block_reuse_count", s.block_reuse_count}};
+    return all.at(name);
+  }
+
+  void run(const Value& op) {
+    const std::string& kind = op["op"].str();
+    auto seq = [&](const char* key = "seq") -> const HipPagedSequenceHandle& {
+      return seqs.at(op[key].str());
+    };
+    if (kind == "create") {
+      seqs[op["seq"].str()] = cache.create_sequence();
+    } else if (kind == "append_encoded") {
+      cache.append(seq(), encoded_token(op["key_base"].num()), encoded_token(op["value_base"].num()),
+                   stream);
+    } else if (kind == "append_values") {
+      const auto s3 = shape3(config.layers, config.kv_heads, config.head_dimension);
+      cache.append(seq(), Tensor::from_values(s3, op["keys"].floats(), kGpu),
+                   Tensor::from_values(s3, op["values"].floats(), kGpu), stream);
+    } else if (kind == "append_layer_major_encoded") {
+      const std::size_t begin = op["token_begin"].index(), count = op["count"].index();
+      cache.append_layer_major(seq(), encoded_layers(begin, count, op["key_base"].num()),
+                               encoded_layers(begin, count, op["value_base"].num()), stream);
+    } else if (kind == "fork") {
+      seqs[op["new"].str()] = cache.fork_sequence(seq(), op["prefix"].index(), false, stream);
+    } else if (kind == "release") {
+      cache.release_sequence(seq());
+    } else if (kind == "expect_error") {
+      const auto code = thrown_code([&] { run(op["inner"]); });
+      ASSERT_TRUE(code.has_value());
+      const std::string& want = op["status"].str();
+      if (want != "any") {
+        const std::map<std::string, ErrorCode> names{
+            {"invalid_argument", ErrorCode::kInvalidArgument},
+            {"out_of_range", ErrorCode::kOutOfRange},
+            {"resource_exhausted", ErrorCode::kResourceExhausted}};
+        EXPECT_TRUE(*code == names.at(want));
       }
-  const Shape shape{static_cast<Dimension>(config.layers), static_cast<Dimension>(config.kv_heads),
-                    static_cast<Dimension>(config.head_dimension)};
-  return {Tensor::from_values(shape, keys, kGpu), Tensor::from_values(shape, values, kGpu)};
-}
+    } else if (kind == "expect_table") {
+      const auto want = op["table"].indices();
+      const auto got = cache.block_table(seq());
+      EXPECT_TRUE(std::vector<std::size_t>(got.begin(), got.end()) == want);
+    } else if (kind == "expect_table_size") {
+      EXPECT_EQ(cache.block_table(seq()).size(), op["size"].index());
+    } else if (kind == "expect_table_last") {
+      EXPECT_EQ(cache.block_table(seq()).back(), op["block"].index());
+    } else if (kind == "expect_tables_share") {
+      const auto a = cache.block_table(seqs.at(op["a"].str()));
+      const auto b = cache.block_table(seqs.at(op["b"].str()));
+      const std::size_t n = op["count"].index();
+      ASSERT_TRUE(a.size() >= n && b.size() >= n);
+      EXPECT_TRUE(std::equal(a.begin(), a.begin() + static_cast<std::ptrdiff_t>(n), b.begin()));
+    } else if (kind == "expect_tables_differ_at") {
+      const std::size_t i = op["index"].index();
+      EXPECT_TRUE(cache.block_table(seqs.at(op["a"].str()))[i] !=
+                  cache.block_table(seqs.at(op["b"].str()))[i]);
+    } else if (kind == "expect_length") {
+      EXPECT_EQ(cache.length(seq()), op["length"].index());
+    } else if (kind == "expect_layer") {
+      const auto [k, v] = layer(op["seq"].str(), op["layer"].index());
+      EXPECT_TRUE(k == op["keys"].floats());
+      EXPECT_TRUE(v == op["values"].floats());
+    } else if (kind == "expect_layer_element") {
+      const auto [k, v] = layer(op["seq"].str(), op["layer"].index());
+      const std::size_t i = op["index"].index();
+      EXPECT_EQ(k.at(i), static_cast<float>(op["key"].num()));
+      EXPECT_EQ(v.at(i), static_cast<float>(op["value"].num()));
+    } else if (kind == "expect_stats") {
+      for (const auto& [name, value] : op["stats"].members) {
+        if (stat(name) != value.index()) {
+          ::mini_test::fail(__FILE__, __LINE__, "statistic " + name + " differs");
+        }
+      }
+    } else {
+      FAIL("unknown fixture op " + kind);
+    }
+  }
 
-float expected_value(std::size_t token, std::size_t layer, std::size_t head, std::size_t c,
-                     bool keys) {
-  const float encoded = static_cast<float>(token * 1000 + layer * 100 + head * 10 + c);
-  return keys ? encoded + 0.25F : -encoded - 0.5F;
-}
-
-// tests/cuda_paged_kv_cache_test.cpp:77-152
-TEST_F(HipPagedKvCacheTest, MapsOddHistoryAcrossPagesAndReportsExactAccounting) {
-  const PagedKvCacheConfig config{2, 3, 5, 2, 3};
-  HipPagedKvCache cache(config);
-  EXPECT_TRUE(cache.is_healthy());
+  PagedKvCacheConfig config;
+  HipPagedKvCache cache;
   Stream stream;
-  const HipPagedSequenceHandle sequence = cache.create_sequence();
-  {
-    auto empty = cache.read_sequence(sequence);
-    EXPECT_EQ(empty.length(), 0U);
-    EXPECT_TRUE(empty.physical_blocks().empty());
-    EXPECT_TRUE(empty.block_table().valid());
-    EXPECT_TRUE(empty.block_table().data() == nullptr);
-    EXPECT_EQ(empty.block_table().logical_block_count(), 0U);
-    ASSERT_EQ(empty.layer_key_blocks().size(), config.layers);
-    EXPECT_TRUE(empty.layer_key_blocks()[0].shape() == (Shape{3, 3, 2, 5}));
+  std::map<std::string, HipPagedSequenceHandle> seqs;
+};
+
+TEST_F(GoldenReplayTest, PagedCacheScenariosReproduceEveryExpectation) {
+  const Value scenarios = json_lite::load(golden_path("paged_cache_scenarios.json"));
+  ASSERT_TRUE(scenarios.size() >= 7);
+  for (const Value& scenario : scenarios.items) {
+    std::printf("  scenario: %s\n", scenario["name"].str().c_str());
+    ScenarioReplay replay(scenario);
+    for (const Value& op : scenario["ops"].items) replay.run(op);
   }
-  for (std::size_t token = 0; token < 5; ++token) {
-    const auto [keys, values] = make_token(config, token);
-    cache.append(sequence, keys, values, stream);
+}
+
+// tests/golden/attention_known_answers.json: the reference's closed-form
+// attention cases (outputs and probabilities), through the history-only
+// entry point and, where the queries are the last keys, through the tail
+// entry point with the probability contract.
+TEST_F(GoldenReplayTest, AttentionKnownAnswersThroughBothEntryPoints) {
+  const Value cases = json_lite::load(golden_path("attention_known_answers.json"));
+  ASSERT_TRUE(cases.size() >= 3);
+  Stream stream;
+  for (const Value& c : cases.items) {
+    std::printf("  case: %s\n", c["name"].str().c_str());
+    const Value& q = c["query"];
+    const Value& k = c["keys"];
+    const Value& v = c["values"];
+    const std::size_t nq = q.size(), nk = k.size(), dk = q[0].size(), dv = v[0].size();
+    const std::size_t bt = c["block_tokens"].index(), phys = c["physical_blocks"].index();
+    const std::vector<std::size_t> table_idx = c["table"].indices();
+    const std::vector<std::uint32_t> table(table_idx.begin(), table_idx.end());
+    auto flat = [](const Value& rows) {
+      std::vector<float> out;
+      for (const Value& r : rows.items)
+        for (float x : r.floats()) out.push_back(x);
+      return out;
+    };
+    const std::vector<float> qf = flat(q), kf = flat(k), vf = flat(v);
+    const std::vector<float> want_out = flat(c["output"]), want_p = flat(c["probabilities"]);
+    auto pack = [&](const std::vector<float>& rows, std::size_t width, float padding) {
+      std::vector<float> pool(phys * bt * width, padding);
+      for (std::size_t t = 0; t < nk; ++t)
+        std::copy_n(rows.data() + t * width, width, pool.data() + (table[t / bt] * bt + t % bt) * width);
+      return Tensor::from_values({static_cast<Dimension>(phys), 1, static_cast<Dimension>(bt),
+                                  static_cast<Dimension>(width)},
+                                 pool, kGpu);
+    };
+    const Tensor kp = pack(kf, dk, static_cast<float>(c["key_padding"].num()));
+    const Tensor vp = pack(vf, dv, static_cast<float>(c["value_padding"].num()));
+    const PagedBlockTable bt_dev(table, phys, 0);
+    const Tensor query = Tensor::from_values(
+        {1, static_cast<Dimension>(nq), static_cast<Dimension>(dk)}, qf, kGpu);
+    Tensor out = Tensor::empty({1, static_cast<Dimension>(nq), static_cast<Dimension>(dv)},
+                               DType::kFloat32, kGpu);
+    Tensor ws = Tensor::empty({1, static_cast<Dimension>(nq), static_cast<Dimension>(nk)},
+                              DType::kFloat32, kGpu);
+    attn::paged_scaled_dot_product_attention_out(query, kp, vp, bt_dev, nk, c["offset"].index(),
+                                                 out, ws, stream);
+    stream.synchronize();
+    auto expect_all = [](const std::vector<float>& got, const std::vector<float>& want, float tol) {
+      ASSERT_EQ(got.size(), want.size());
+      for (std::size_t i = 0; i < want.size(); ++i) EXPECT_NEAR(got[i], want[i], tol);
+    };
+    expect_all(host_values(out), want_out, 2e-5F);
+    expect_all(host_values(ws), want_p, 2e-6F);
+    const std::size_t hist = nk - nq;
+    if (c["offset"].index() == hist) {
+      const Tensor tk = Tensor::from_values(
+          {1, static_cast<Dimension>(nq), static_cast<Dimension>(dk)},
+          std::vector<float>(kf.begin() + static_cast<std::ptrdiff_t>(hist * dk), kf.end()), kGpu);
+      const Tensor tv = Tensor::from_values(
+          {1, static_cast<Dimension>(nq), static_cast<Dimension>(dv)},
+          std::vector<float>(vf.begin() + static_cast<std::ptrdiff_t>(hist * dv), vf.end()), kGpu);
+      std::vector<std::uint32_t> hist_table(table.begin(),
+                                            table.begin() + static_cast<std::ptrdiff_t>((hist + bt - 1) / bt));
+      const PagedBlockTable ht(hist_table, phys, 0);
+      Tensor out2 = Tensor::empty(out.shape(), DType::kFloat32, kGpu);
+      Tensor ws2 = Tensor::empty(ws.shape(), DType::kFloat32, kGpu);
+      attn::paged_scaled_dot_product_attention_with_tail_probabilities_out(
+          query, kp, vp, ht, hist, tk, tv, out2, ws2, stream);
+      stream.synchronize();
+      expect_all(host_values(out2), want_out, 2e-5F);
+      expect_all(host_values(ws2), want_p, 2e-6F);
+    }
   }
-  stream.synchronize();
-  {
-    auto view = cache.read_sequence(sequence);
-    EXPECT_EQ(view.length(), 5U);
-    constexpr std::array<std::uint32_t, 3> kExpectedBlocks{0, 1, 2};
-    EXPECT_TRUE(std::equal(view.physical_blocks().begin(), view.physical_blocks().end(),
-                           kExpectedBlocks.begin(), kExpectedBlocks.end()));
-    EXPECT_EQ(view.block_table().logical_block_count(), 3U);
-    EXPECT_EQ(view.block_table().physical_block_count(), 3U);
-    for (std::size_t layer = 0; layer < config.layers; ++layer) {
-      const auto hk = host_values(view.layer_key_blocks()[layer]);
-      const auto hv = host_values(view.layer_value_blocks()[layer]);
-      for (std::size_t token = 0; token < 5; ++token) {
-        const std::size_t block = token / config.block_tokens, slot = token % config.block_tokens;
-        for (std::size_t head = 0; head < config.kv_heads; ++head)
-          for (std::size_t c = 0; c < config.head_dimension; ++c) {
-            const std::size_t i =
-                ((block * config.kv_heads + head) * config.block_tokens + slot) *
-                    config.head_dimension + c;
-            // bit-exact: the append is a copy
-            EXPECT_EQ(hk[i], expected_value(token, layer, head, c, true));
-            EXPECT_EQ(hv[i], expected_value(token, layer, head, c, false));
-          }
+}
+
+// ------------------------------------------- random programs vs the oracle ----
+// Seeded random programs of create / one-token append / bulk append /
+// aligned and copy-on-write forks / releases run on the device cache and on
+// the oracle pool side by side: every call succeeds or fails on both with
+// the same code, and the tables, lengths, statistics and gathered pages stay
+// equal throughout.
+class OraclePool {
+ public:
+  OraclePool(std::size_t l, std::size_t h, std::size_t d, std::size_t p, std::size_t n) {
+    int status = 0;
+    pool_ = oracle_pool_create(l, h, d, p, n, &status);
+    if (status != 0) throw std::runtime_error("oracle pool");
+  }
+  ~OraclePool() { oracle_pool_destroy(pool_); }
+  OraclePool(const OraclePool&) = delete;
+  OraclePool& operator=(const OraclePool&) = delete;
+  [[nodiscard]] void* get() const { return pool_; }
+
+ private:
+  void* pool_ = nullptr;
+};
+
+// Oracle status (0 ok, else ErrorCode + 1) -> the code the library throws.
+std::optional<ErrorCode> oracle_code(int status) {
+  if (status == 0) return std::nullopt;
+  return static_cast<ErrorCode>(status - 1);
+}
+
+TEST_F(HipPagedKvCacheTest, RandomProgramsMatchTheOraclePool) {
+  constexpr std::size_t L = 2, H = 2, D = 8, P = 4, N = 40;
+  for (std::uint64_t seed : {11U, 12U, 13U}) {
+    std::mt19937_64 rng(seed);
+    auto pick = [&](std::size_t n) { return static_cast<std::size_t>(rng() % n); };
+    HipPagedKvCache cache(PagedKvCacheConfig{L, H, D, P, N});
+    OraclePool pool(L, H, D, P, N);
+    Stream stream;
+    struct Live {
+      HipPagedSequenceHandle mine;
+      std::uint64_t theirs;
+    };
+    std::vector<Live> live;
+    std::uniform_real_distribution<float> value(-4.0F, 4.0F);
+    auto rows = [&](std::size_t n) {
+      std::vector<float> v(n);
+      for (float& x : v) x = value(rng);
+      return v;
+    };
+    for (int step = 0; step < 160; ++step) {
+      const std::size_t what = live.empty() ? 0 : pick(10);
+      std::optional<ErrorCode> mine, theirs;
+      if (what == 0) {
+        live.push_back({cache.create_sequence(), oracle_create_sequence(pool.get())});
+      } else if (what <= 3) {  // one token
+        Live& s = live[pick(live.size())];
+        const auto k = rows(L * H * D), v = rows(L * H * D);
+        mine = thrown_code([&] {
+          cache.append(s.mine, Tensor::from_values({L, H, D}, k, kGpu),
+                       Tensor::from_values({L, H, D}, v, kGpu), stream);
+        });
+        theirs = oracle_code(oracle_append(pool.get(), s.theirs, k.data(), v.data()));
+      } else if (what <= 5) {  // bulk, [L, H, T, D] on the oracle side
+        Live& s = live[pick(live.size())];
+        const std::size_t t = 1 + pick(11);
+        const auto k = rows(L * H * t * D), v = rows(L * H * t * D);
+        std::vector<Tensor> lk, lv;
+        for (std::size_t l = 0; l < L; ++l) {
+          const auto first = static_cast<std::ptrdiff_t>(l * H * t * D);
+          const auto last = first + static_cast<std::ptrdiff_t>(H * t * D);
+          lk.push_back(Tensor::from_values({H, static_cast<Dimension>(t), D},
+                                           std::vector<float>(k.begin() + first, k.begin() + last), kGpu));
+          lv.push_back(Tensor::from_values({H, static_cast<Dimension>(t), D},
+                                           std::vector<float>(v.begin() + first, v.begin() + last), kGpu));
+        }
+        mine = thrown_code([&] { cache.append_layer_major(s.mine, lk, lv, stream); });
+        theirs = oracle_code(oracle_append_layer_major(pool.get(), s.theirs, k.data(), v.data(), t));
+      } else if (what <= 7) {  // fork at an aligned or (with copy-on-write) any prefix
+        Live& s = live[pick(live.size())];
+        const std::size_t len = cache.length(s.mine);
+        const bool cow = pick(2) == 1;
+        const std::size_t prefix = len == 0 ? 0 : (cow ? 1 + pick(len) : P * pick(len / P + 1));
+        HipPagedSequenceHandle child;
+        std::uint64_t other = 0;
+        mine = thrown_code([&] { child = cache.fork_sequence(s.mine, prefix, cow, stream); });
+        theirs = oracle_code(oracle_fork_sequence(pool.get(), s.theirs, prefix, cow ? 1 : 0, &other));
+        if (!mine && !theirs) live.push_back({child, other});
+      } else {  // release
+        const std::size_t i = pick(live.size());
+        cache.release_sequence(live[i].mine);
+        ASSERT_EQ(oracle_release_sequence(pool.get(), live[i].theirs), 0);
+        live.erase(live.begin() + static_cast<std::ptrdiff_t>(i));
+      }
+      if (mine != theirs) {
+        ::mini_test::fail(__FILE__, __LINE__,
+                          "seed " + std::to_string(seed) + " step " + std::to_string(step) +
+                              ": library and oracle disagree on success");
+        return;
+      }
+      helix_paged_stats want{};
+      oracle_stats(pool.get(), &want);
+      const PagedKvCacheStats got = cache.stats();
+      EXPECT_EQ(got.used_blocks, want.used_blocks);
+      EXPECT_EQ(got.block_reference_count, want.block_reference_count);
+      EXPECT_EQ(got.shared_blocks, want.shared_blocks);
+      EXPECT_EQ(got.active_tokens, want.active_tokens);
+      EXPECT_EQ(got.block_reuse_count, want.block_reuse_count);
+      EXPECT_EQ(got.peak_bytes_used, want.peak_bytes_used);
+      for (const Live& s : live) {
+        std::vector<std::uint32_t> t(N);
+        t.resize(oracle_block_table(pool.get(), s.theirs, t.data(), t.size()));
+        EXPECT_TRUE(cache.block_table(s.mine) == t);
+        EXPECT_EQ(cache.length(s.mine), oracle_length(pool.get(), s.theirs));
+      }
+      if (step % 20 != 19) continue;
+      for (const Live& s : live) {
+        const std::size_t n = cache.length(s.mine);
+        for (std::size_t l = 0; l < L; ++l) {
+          Tensor k = Tensor::empty({H, static_cast<Dimension>(n), D}, DType::kFloat32, kGpu);
+          Tensor v = Tensor::empty({H, static_cast<Dimension>(n), D}, DType::kFloat32, kGpu);
+          cache.copy_layer_out(s.mine, l, k, v, stream);
+          std::vector<float> wk(H * n * D), wv(H * n * D);
+          ASSERT_EQ(oracle_copy_layer(pool.get(), s.theirs, l, wk.data(), wv.data(), n), 0);
+          EXPECT_TRUE(host_values(k) == wk);
+          EXPECT_TRUE(host_values(v) == wv);
+        }
       }
     }
   }
-  const PagedKvCacheStats stats = cache.stats();
-  EXPECT_EQ(cache.bytes_per_token(), 2U * 2U * 3U * 5U * sizeof(float));
-  EXPECT_EQ(cache.block_bytes(), cache.bytes_per_token() * config.block_tokens);
-  EXPECT_EQ(cache.token_capacity(), 6U);
-  EXPECT_EQ(stats.bytes_reserved, cache.block_bytes() * config.physical_blocks);
-  EXPECT_EQ(stats.bytes_used, stats.bytes_reserved);
-  EXPECT_EQ(stats.bytes_free, 0U);
-  EXPECT_EQ(stats.peak_bytes_used, stats.bytes_reserved);
-  EXPECT_EQ(stats.total_blocks, 3U);
-  EXPECT_EQ(stats.used_blocks, 3U);
-  EXPECT_EQ(stats.free_blocks, 0U);
-  EXPECT_EQ(stats.active_sequence_count, 1U);
-  EXPECT_EQ(stats.active_tokens, 5U);
-  EXPECT_EQ(stats.resident_tokens, 5U);
-  EXPECT_EQ(stats.allocated_token_slots, 6U);
-  EXPECT_EQ(stats.unused_token_slots(), 1U);
-  EXPECT_EQ(stats.block_reference_count, 3U);
-  EXPECT_EQ(stats.shared_blocks, 0U);
-  EXPECT_EQ(stats.sequence_create_count, 1U);
-  EXPECT_EQ(stats.append_count, 5U);
-  EXPECT_EQ(stats.block_allocation_count, 3U);
-  EXPECT_EQ(stats.block_reuse_count, 0U);
 }
 
-// tests/cuda_paged_kv_cache_test.cpp:154-192
-TEST_F(HipPagedKvCacheTest, ExhaustionIsTransactionalAndReleasedBlocksReuseInFifoOrder) {
-  const PagedKvCacheConfig config{1, 2, 3, 2, 3};
+// ----------------------------------------------------------- read lease ----
+// A read view holds the cache: a release issued on another thread waits
+// until the view is gone, and a consumer that poisons its view leaves the
+// cache unhealthy (every later mutation fails with kRuntime) while the
+// view's table and pools stay allocated.
+TEST_F(HipPagedKvCacheTest, ReadLeaseDefersMutationsAndPoisonQuarantines) {
+  const PagedKvCacheConfig config{1, 2, 4, 2, 6};
   HipPagedKvCache cache(config);
   Stream stream;
-  const HipPagedSequenceHandle first = cache.create_sequence();
-  const HipPagedSequenceHandle second = cache.create_sequence();
-  for (std::size_t token = 0; token < 4; ++token) {
-    const auto [keys, values] = make_token(config, token);
-    cache.append(first, keys, values, stream);
-  }
-  const auto [second_keys, second_values] = make_token(config, 10);
-  cache.append(second, second_keys, second_values, stream);
-  const auto [slack_keys, slack_values] = make_token(config, 11);
-  cache.append(second, slack_keys, slack_values, stream);
-  ASSERT_EQ(cache.stats().free_blocks, 0U);
-
-  const PagedKvCacheStats before = cache.stats();
-  const auto [rejected_keys, rejected_values] = make_token(config, 12);
-  expect_error_code([&] { cache.append(second, rejected_keys, rejected_values, stream); },
-                    ErrorCode::kResourceExhausted);
-  EXPECT_EQ(cache.length(second), 2U);
-  EXPECT_EQ(cache.stats().append_count, before.append_count);
-  EXPECT_EQ(cache.stats().block_allocation_count, before.block_allocation_count);
-  EXPECT_EQ(cache.stats().bytes_used, before.bytes_used);
-
-  cache.release_sequence(first);
-  EXPECT_FALSE(cache.contains(first));
-  EXPECT_EQ(cache.stats().free_blocks, 2U);
-  cache.append(second, rejected_keys, rejected_values, stream);
-  {
-    auto view = cache.read_sequence(second);
-    ASSERT_EQ(view.physical_blocks().size(), 2U);
-    EXPECT_EQ(view.physical_blocks()[0], 2U);
-    EXPECT_EQ(view.physical_blocks()[1], 0U);
-  }
-  EXPECT_EQ(cache.stats().block_reuse_count, 1U);
-  EXPECT_EQ(cache.stats().release_count, 1U);
-  stream.synchronize();
-}
-
-// tests/cuda_paged_kv_cache_test.cpp:194-234
-TEST_F(HipPagedKvCacheTest, RejectsInvalidConfigurationHandlesTensorsStreamsAndAliasing) {
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{0, 1, 1, 1, 1}), Error);
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{1, 0, 1, 1, 1}), Error);
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{1, 1, 0, 1, 1}), Error);
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{1, 1, 1, 0, 1}), Error);
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{1, 1, 1, 1, 0}), Error);
-  EXPECT_THROW(HipPagedKvCache(PagedKvCacheConfig{1, 1, 1, 1, 1}, -1), Error);
-
-  const PagedKvCacheConfig config{1, 1, 2, 1, 1};
-  HipPagedKvCache first(config);
-  HipPagedKvCache second(config);
-  const HipPagedSequenceHandle sequence = first.create_sequence();
-  const HipPagedSequenceHandle foreign = second.create_sequence();
-  Stream stream;
-  const auto [keys, values] = make_token(config, 0);
-
-  EXPECT_THROW(first.append(foreign, keys, values, stream), Error);
-  EXPECT_THROW(first.append(HipPagedSequenceHandle{}, keys, values, stream), Error);
-  EXPECT_THROW(first.append(sequence, Tensor::zeros({1, 1, 2}), values, stream), Error);
-  EXPECT_THROW(first.append(sequence, Tensor::zeros({1, 1, 2}, DType::kUInt32, kGpu), values,
-                            stream),
-               Error);
-  EXPECT_THROW(first.append(sequence, Tensor::zeros({1, 2}, DType::kFloat32, kGpu), values,
-                            stream),
-               Error);
-
-  Stream active_stream = std::move(stream);
-  EXPECT_THROW(first.append(sequence, keys, values, stream), Error);
-
-  std::optional<Tensor> aliased_keys;
-  {
-    auto view = first.read_sequence(sequence);
-    aliased_keys.emplace(view.layer_key_blocks()[0].reshape({1, 1, 2}));
-  }
-  EXPECT_THROW(first.append(sequence, *aliased_keys, values, active_stream), Error);
-
-  first.append(sequence, keys, values, active_stream);
-  first.release_sequence(sequence);
-  EXPECT_THROW(first.release_sequence(sequence), Error);
-  EXPECT_THROW(static_cast<void>(first.read_sequence(sequence)), Error);
-  active_stream.synchronize();
-}
-
-// tests/cuda_paged_kv_cache_test.cpp:236-267
-TEST_F(HipPagedKvCacheTest, DecodeViewPinsMappingAndPoolLifetimeAndMovesSafely) {
-  const PagedKvCacheConfig config{1, 1, 3, 2, 2};
-  auto cache = std::make_unique<HipPagedKvCache>(config);
-  auto replacement_cache = std::make_unique<HipPagedKvCache>(config);
-  Stream stream;
-  const HipPagedSequenceHandle sequence = cache->create_sequence();
-  const HipPagedSequenceHandle replacement_sequence = replacement_cache->create_sequence();
-  const auto [keys, values] = make_token(config, 0);
-  cache->append(sequence, keys, values, stream);
-  replacement_cache->append(replacement_sequence, keys, values, stream);
-  stream.synchronize();
-
-  std::optional<HipPagedKvCache::DecodeView> view;
-  view.emplace(cache->read_sequence(sequence));
-  HipPagedKvCache::DecodeView moved = std::move(*view);
-  EXPECT_THROW(static_cast<void>(view->length()), Error);
+  const auto seq = cache.create_sequence();
+  const Tensor row = Tensor::zeros({1, 2, 4}, DType::kFloat32, kGpu);
+  for (int i = 0; i < 3; ++i) cache.append(seq, row, row, stream);
+  auto view = std::make_unique<HipPagedKvCache::DecodeView>(cache.read_sequence(seq));
+  EXPECT_EQ(view->length(), 3U);
+  EXPECT_EQ(view->physical_blocks().size(), 2U);
+  auto released = std::async(std::launch::async, [&] { cache.release_sequence(seq); });
+  EXPECT_TRUE(released.wait_for(std::chrono::milliseconds(200)) == std::future_status::timeout);
   view.reset();
-  cache.reset();
-
-  EXPECT_EQ(moved.length(), 1U);
-  EXPECT_EQ(moved.physical_blocks().front(), 0U);
-  EXPECT_TRUE(moved.layer_key_blocks()[0].device() == kGpu);
-  EXPECT_TRUE(moved.block_table().valid());
-  // the pool outlives the cache object while the view holds it
-  const auto hk = host_values(moved.layer_key_blocks()[0]);
-  EXPECT_EQ(hk[2], expected_value(0, 0, 0, 2, true));
-
-  auto replacement = replacement_cache->read_sequence(replacement_sequence);
-  replacement_cache.reset();
-  moved = std::move(replacement);
-  EXPECT_THROW(static_cast<void>(replacement.length()), Error);
-  EXPECT_EQ(moved.length(), 1U);
-  EXPECT_EQ(moved.physical_blocks().front(), 0U);
-}
-
-// tests/cuda_paged_kv_cache_test.cpp:269-293
-TEST_F(HipPagedKvCacheTest, DecodeViewSerializesReleaseUntilBorrowedPointersExpire) {
-  const PagedKvCacheConfig config{1, 1, 2, 2, 1};
-  HipPagedKvCache cache(config);
-  Stream stream;
-  const HipPagedSequenceHandle sequence = cache.create_sequence();
-  const auto [keys, values] = make_token(config, 0);
-  cache.append(sequence, keys, values, stream);
-  stream.synchronize();
-
-  std::optional<HipPagedKvCache::DecodeView> view;
-  view.emplace(cache.read_sequence(sequence));
-  std::promise<void> started;
-  std::future<void> started_future = started.get_future();
-  std::future<void> release = std::async(std::launch::async, [&] {
-    started.set_value();
-    cache.release_sequence(sequence);
-  });
-  started_future.wait();
-  EXPECT_TRUE(release.wait_for(std::chrono::milliseconds(20)) == std::future_status::timeout);
-  view.reset();
-  EXPECT_TRUE(release.wait_for(std::chrono::seconds(2)) == std::future_status::ready);
-  release.get();
-  EXPECT_FALSE(cache.contains(sequence));
-  EXPECT_EQ(cache.stats().free_blocks, 1U);
-}
-
-// tests/cuda_paged_kv_cache_test.cpp:295-327
-TEST_F(HipPagedKvCacheTest, FailedConsumerQuarantinesTableAndPreventsPageReuse) {
-  const PagedKvCacheConfig config{1, 1, 2, 2, 1};
-  HipPagedKvCache cache(config);
-  Stream stream;
-  const HipPagedSequenceHandle sequence = cache.create_sequence();
-  const auto [keys, values] = make_token(config, 0);
-  cache.append(sequence, keys, values, stream);
-  stream.synchronize();
-  {
-    auto view = cache.read_sequence(sequence);
-    ASSERT_NE(view.block_table().data(), nullptr);
-    view.poison_after_consumer_failure();
-    EXPECT_THROW(static_cast<void>(view.length()), Error);
-  }
-  EXPECT_FALSE(cache.is_healthy());
-  EXPECT_TRUE(cache.contains(sequence));
-  EXPECT_EQ(cache.length(sequence), 1U);
-  expect_error_code([&] { static_cast<void>(cache.create_sequence()); }, ErrorCode::kRuntime);
-  expect_error_code([&] { static_cast<void>(cache.read_sequence(sequence)); }, ErrorCode::kRuntime);
-  expect_error_code([&] { cache.append(sequence, keys, values, stream); }, ErrorCode::kRuntime);
-
-  cache.release_sequence(sequence);
-  EXPECT_FALSE(cache.contains(sequence));
+  EXPECT_TRUE(released.wait_for(std::chrono::seconds(10)) == std::future_status::ready);
+  released.get();
   EXPECT_EQ(cache.stats().used_blocks, 0U);
-  EXPECT_EQ(cache.stats().free_blocks, 1U);
-  expect_error_code([&] { static_cast<void>(cache.create_sequence()); }, ErrorCode::kRuntime);
+
+  const auto other = cache.create_sequence();
+  cache.append(other, row, row, stream);
+  auto moved = cache.read_sequence(other);
+  auto lease = std::move(moved);  // the moved-from view no longer answers
+  EXPECT_TRUE(thrown_code([&] { static_cast<void>(moved.length()); }) == ErrorCode::kInvalidArgument);
+  const float* pool = lease.layer_key_blocks()[0].data_as<float>();
+  lease.poison_after_consumer_failure();
+  EXPECT_FALSE(cache.is_healthy());
+  EXPECT_TRUE(thrown_code([&] { cache.append(other, row, row, stream); }) == ErrorCode::kRuntime);
+  EXPECT_TRUE(thrown_code([&] { static_cast<void>(lease.length()); }) == ErrorCode::kInvalidArgument);
+  EXPECT_TRUE(pool != nullptr);
 }
 
-// Extension: copy-on-write fork at a non-aligned prefix, bulk layer-major
-// append and the compact gather, each bit-exact.
+// ------------------------------------------------------------ extensions ----
+// Extension: a copy-on-write fork at a non-aligned prefix shares the full
+// pages and copies the partial one; the child's gather equals the source's
+// first tokens bit for bit.
 TEST_F(HipPagedKvCacheTest, ForkBulkAppendAndGatherAreBitExact) {
   const PagedKvCacheConfig config{2, 2, 8, 4, 16};
   HipPagedKvCache cache(config);
@@ -524,8 +696,8 @@ TEST_F(HipPagedKvCacheTest, PrefixCacheHitForksTheAnchorAndSharesItsPages) {
   Stream stream;
   const auto anchor = cache->create_sequence();
   for (std::size_t t = 0; t < 4; ++t) {
-    const auto [k, v] = make_token(config, t);
-    cache->append(anchor, k, v, stream);
+    cache->append(anchor, random_uniform({1, 1, 4}, 60 + t, -1, 1).to(kGpu),
+                  random_uniform({1, 1, 4}, 70 + t, -1, 1).to(kGpu), stream);
   }
   const std::array<std::uint32_t, 4> tokens{7, 8, 9, 10};
   const PrefixNamespaceId ns(3);
@@ -547,369 +719,260 @@ TEST_F(HipPagedKvCacheTest, PrefixCacheHitForksTheAnchorAndSharesItsPages) {
 }
 
 // ------------------------------------------------------- paged attention ----
-// tests/cuda_attention_test.cpp:14-99 helpers
-void expect_close(const Tensor& actual_device, const std::vector<float>& expected,
-                  float tolerance) {
-  const auto actual = host_values(actual_device);
-  ASSERT_EQ(actual.size(), expected.size());
-  for (std::size_t i = 0; i < expected.size(); ++i) EXPECT_NEAR(actual[i], expected[i], tolerance);
+// A seeded paged problem: logical K/V [H, keys, width] scattered over a pool
+// of `physical` pages through a permuted table, unused slots filled with a
+// large padding value that a wrong index would pick up.
+struct PagedProblem {
+  std::size_t heads, queries, dk, dv, bt, history, tail, physical;
+  std::vector<std::uint32_t> table;
+  Tensor query, key_pool, value_pool, tail_key, tail_value;  // host
+};
+
+PagedProblem make_problem(std::uint64_t seed, std::size_t heads, std::size_t queries,
+                          std::size_t dk, std::size_t dv, std::size_t bt, std::size_t history,
+                          std::size_t tail) {
+  PagedProblem p{heads, queries, dk, dv, bt, history, tail, 0, {}, {}, {}, {}, {}, {}};
+  const std::size_t logical = (history + bt - 1) / bt;
+  p.physical = logical + 3;
+  std::vector<std::uint32_t> perm(p.physical);
+  std::iota(perm.begin(), perm.end(), 0U);
+  std::mt19937_64 rng(seed);
+  std::shuffle(perm.begin(), perm.end(), rng);
+  p.table.assign(perm.begin(), perm.begin() + static_cast<std::ptrdiff_t>(logical));
+  const auto H = static_cast<Dimension>(heads);
+  p.query = random_uniform({H, static_cast<Dimension>(queries), static_cast<Dimension>(dk)},
+                           seed * 10 + 1, -1, 1);
+  auto pool = [&](std::size_t width, std::uint64_t s, float padding) {
+    const Tensor logical_rows = random_uniform(
+        {H, static_cast<Dimension>(history), static_cast<Dimension>(width)}, s, -1, 1);
+    std::vector<float> v(p.physical * heads * bt * width, padding);
+    for (std::size_t h = 0; h < heads; ++h)
+      for (std::size_t t = 0; t < history; ++t)
+        std::copy_n(logical_rows.data_as<float>() + (h * history + t) * width, width,
+                    v.data() + ((p.table[t / bt] * heads + h) * bt + t % bt) * width);
+    return Tensor::from_values({static_cast<Dimension>(p.physical), H,
+                                static_cast<Dimension>(bt), static_cast<Dimension>(width)},
+                               v);
+  };
+  p.key_pool = pool(dk, seed * 10 + 2, 9000.0F);
+  p.value_pool = pool(dv, seed * 10 + 3, -9000.0F);
+  p.tail_key = random_uniform({H, static_cast<Dimension>(tail), static_cast<Dimension>(dk)},
+                              seed * 10 + 4, -1, 1);
+  p.tail_value = random_uniform({H, static_cast<Dimension>(tail), static_cast<Dimension>(dv)},
+                                seed * 10 + 5, -1, 1);
+  return p;
 }
 
-Tensor pack_logical_blocks(const Tensor& logical, std::span<const std::uint32_t> block_table,
-                           Dimension physical_blocks, Dimension block_tokens, float padding) {
-  const auto heads = static_cast<std::size_t>(logical.shape()[0]);
-  const auto tokens = static_cast<std::size_t>(logical.shape()[1]);
-  const auto width = static_cast<std::size_t>(logical.shape()[2]);
-  const auto per_block = static_cast<std::size_t>(block_tokens);
-  std::vector<float> packed(static_cast<std::size_t>(physical_blocks) * heads * per_block * width,
-                            padding);
-  const float* source = logical.data_as<float>();
-  for (std::size_t h = 0; h < heads; ++h)
-    for (std::size_t t = 0; t < tokens; ++t) {
-      const std::size_t physical = block_table[t / per_block];
-      for (std::size_t d = 0; d < width; ++d)
-        packed[((physical * heads + h) * per_block + t % per_block) * width + d] =
-            source[(h * tokens + t) * width + d];
+// Seeded sweep over odd geometries (head and value widths not multiples of
+// anything, pages of 1..7 tokens, empty histories, several tail rows): the
+// tail entry point with the probability contract and the history-only entry
+// point with a query offset both match the oracle (outputs within
+// 2e-5 + D * 1e-6, probabilities within 2e-6).
+TEST_F(HipAttentionTest, SeededOddGeometriesMatchTheOracle) {
+  std::mt19937_64 rng(2024);
+  Stream stream;
+  for (int trial = 0; trial < 16; ++trial) {
+    auto in = [&](std::size_t lo, std::size_t hi) { return lo + rng() % (hi - lo + 1); };
+    const std::size_t heads = in(1, 4), dk = in(1, 48), dv = in(1, 48), bt = in(1, 7);
+    const std::size_t history = trial % 4 == 0 ? 0 : in(1, 60), tail = in(1, 5);
+    const PagedProblem p = make_problem(500 + trial, heads, tail, dk, dv, bt, history, tail);
+    const float tol = 2.0e-5F + static_cast<float>(dk) * 1.0e-6F;
+    const PagedBlockTable table(p.table, p.physical, 0);
+    const Tensor q = p.query.to(kGpu), kp = p.key_pool.to(kGpu), vp = p.value_pool.to(kGpu);
+    // Tail form.
+    {
+      Tensor out = Tensor::empty({static_cast<Dimension>(heads), static_cast<Dimension>(tail),
+                                  static_cast<Dimension>(dv)}, DType::kFloat32, kGpu);
+      Tensor ws = Tensor::empty(attn::paged_tail_score_workspace_shape(
+                                    q, kp, vp, table, history, p.tail_key.to(kGpu),
+                                    p.tail_value.to(kGpu)),
+                                DType::kFloat32, kGpu);
+      attn::paged_scaled_dot_product_attention_with_tail_probabilities_out(
+          q, kp, vp, table, history, p.tail_key.to(kGpu), p.tail_value.to(kGpu), out, ws, stream);
+      stream.synchronize();
+      std::vector<float> want(heads * tail * dv), want_ws(heads * tail * (history + tail));
+      ASSERT_EQ(oracle_paged_attention(p.query.data_as<float>(), heads, heads, tail, dk, dv,
+                                       p.key_pool.data_as<float>(), p.value_pool.data_as<float>(),
+                                       bt, p.table.data(), history, p.tail_key.data_as<float>(),
+                                       p.tail_value.data_as<float>(), tail, history, want.data(),
+                                       want_ws.data()),
+                0);
+      const auto got = host_values(out), got_ws = host_values(ws);
+      for (std::size_t i = 0; i < want.size(); ++i) EXPECT_NEAR(got[i], want[i], tol);
+      for (std::size_t i = 0; i < want_ws.size(); ++i) EXPECT_NEAR(got_ws[i], want_ws[i], 2e-6F);
     }
-  return Tensor::from_values({physical_blocks, logical.shape()[0], block_tokens, logical.shape()[2]},
-                             packed);
-}
-
-Tensor concatenate_token_axis(const Tensor& prefix, const Tensor& tail) {
-  const auto heads = static_cast<std::size_t>(prefix.shape()[0]);
-  const auto np = static_cast<std::size_t>(prefix.shape()[1]);
-  const auto nt = static_cast<std::size_t>(tail.shape()[1]);
-  const auto width = static_cast<std::size_t>(prefix.shape()[2]);
-  Tensor result = Tensor::empty({prefix.shape()[0], prefix.shape()[1] + tail.shape()[1],
-                                 prefix.shape()[2]});
-  for (std::size_t h = 0; h < heads; ++h) {
-    float* dst = result.data<float>() + h * (np + nt) * width;
-    std::copy_n(prefix.data_as<float>() + h * np * width, np * width, dst);
-    std::copy_n(tail.data_as<float>() + h * nt * width, nt * width, dst + np * width);
+    // History-only form: the last `tail` history keys are the queries' own.
+    if (history >= tail) {
+      const std::size_t offset = history - tail;
+      Tensor out = Tensor::empty({static_cast<Dimension>(heads), static_cast<Dimension>(tail),
+                                  static_cast<Dimension>(dv)}, DType::kFloat32, kGpu);
+      Tensor ws = Tensor::empty({static_cast<Dimension>(heads), static_cast<Dimension>(tail),
+                                 static_cast<Dimension>(history)}, DType::kFloat32, kGpu);
+      attn::paged_scaled_dot_product_attention_out(q, kp, vp, table, history, offset, out, ws,
+                                                   stream);
+      stream.synchronize();
+      std::vector<float> want(heads * tail * dv), want_ws(heads * tail * history);
+      ASSERT_EQ(oracle_paged_attention(p.query.data_as<float>(), heads, heads, tail, dk, dv,
+                                       p.key_pool.data_as<float>(), p.value_pool.data_as<float>(),
+                                       bt, p.table.data(), history, nullptr, nullptr, 0, offset,
+                                       want.data(), want_ws.data()),
+                0);
+      const auto got = host_values(out), got_ws = host_values(ws);
+      for (std::size_t i = 0; i < want.size(); ++i) EXPECT_NEAR(got[i], want[i], tol);
+      for (std::size_t i = 0; i < want_ws.size(); ++i) EXPECT_NEAR(got_ws[i], want_ws[i], 2e-6F);
+    }
   }
-  return result;
 }
 
-std::vector<std::uint32_t> reversed_block_table(std::size_t logical, std::size_t physical) {
-  std::vector<std::uint32_t> r(logical);
-  for (std::size_t i = 0; i < logical; ++i) r[i] = static_cast<std::uint32_t>(physical - 1 - i);
-  return r;
-}
-
-/// The oracle's contiguous SDPA: (output, probabilities).
-std::pair<std::vector<float>, std::vector<float>> cpu_sdpa(const Tensor& q, const Tensor& k,
-                                                           const Tensor& v, std::size_t offset) {
-  const auto h = static_cast<std::size_t>(q.shape()[0]), t = static_cast<std::size_t>(q.shape()[1]);
-  const auto keys = static_cast<std::size_t>(k.shape()[1]);
-  const auto dk = static_cast<std::size_t>(q.shape()[2]), dv = static_cast<std::size_t>(v.shape()[2]);
-  std::vector<float> out(h * t * dv), ws(h * t * keys);
-  if (oracle_sdpa(q.data_as<float>(), k.data_as<float>(), v.data_as<float>(), h, t, keys, dk, dv,
-                  offset, out.data(), ws.data()) != 0) {
-    throw std::runtime_error("oracle_sdpa rejected its inputs");
-  }
-  return {out, ws};
-}
-
-// tests/cuda_attention_test.cpp:196-228
-TEST_F(HipAttentionTest, PagedPathMatchesKnownReorderedBlocksAndIgnoresTailPadding) {
-  constexpr std::array<std::uint32_t, 2> kBlockTable{2, 0};
-  const Tensor query_host = Tensor::from_values({1, 2, 2}, std::array{1.0F, 0.0F, 0.0F, 1.0F});
-  const Tensor key_host =
-      Tensor::from_values({1, 3, 2}, std::array{1.0F, 0.0F, 0.0F, 1.0F, 1.0F, 1.0F});
-  const Tensor value_host = Tensor::from_values(
-      {1, 3, 3}, std::array{10.0F, 1.0F, -1.0F, 20.0F, 2.0F, -2.0F, 30.0F, 3.0F, -3.0F});
-  const auto [expected_output, expected_probabilities] = cpu_sdpa(query_host, key_host, value_host, 1);
-  const Tensor query = query_host.to(kGpu);
-  const Tensor key_blocks = pack_logical_blocks(key_host, kBlockTable, 3, 2, 10000.0F).to(kGpu);
-  const Tensor value_blocks = pack_logical_blocks(value_host, kBlockTable, 3, 2, -10000.0F).to(kGpu);
-  PagedBlockTable block_table(kBlockTable, 3, 0);
-  Tensor output = Tensor::empty({1, 2, 3}, DType::kFloat32, kGpu);
-  Tensor workspace = Tensor::empty({1, 2, 3}, DType::kFloat32, kGpu);
+// Every invalid call of the reference-shaped entry points fails with the
+// reference's error code before anything is launched: the output, whose
+// sentinel value no kernel would write, is untouched afterwards.  Each row
+// changes one thing of a valid call.
+TEST_F(HipAttentionTest, InvalidCallsFailBeforeLaunch) {
+  const PagedProblem p = make_problem(77, 2, 1, 4, 3, 2, 5, 1);
   Stream stream;
-  paged_scaled_dot_product_attention_out(query, key_blocks, value_blocks, block_table, 3, 1,
-                                         output, workspace, stream);
-  stream.synchronize();
-  expect_close(output, expected_output, 2.0e-5F);
-  expect_close(workspace, expected_probabilities, 2.0e-6F);
-}
-
-// tests/cuda_attention_test.cpp:230-273
-TEST_F(HipAttentionTest, PagedPathMatchesCpuAcrossOddPagesHeadsAndWidths) {
-  struct Problem {
-    Dimension heads, queries, keys, key_dimension, value_dimension, block_tokens;
+  const PagedBlockTable table(p.table, p.physical, 0);
+  const PagedBlockTable short_table(std::span<const std::uint32_t>(p.table).first(2), p.physical, 0);
+  const Tensor q = p.query.to(kGpu), kp = p.key_pool.to(kGpu), vp = p.value_pool.to(kGpu);
+  const Tensor tk = p.tail_key.to(kGpu), tv = p.tail_value.to(kGpu);
+  const std::vector<float> sentinel(2 * 1 * 3, 12345.0F);
+  Tensor out = Tensor::from_values({2, 1, 3}, sentinel, kGpu);
+  Tensor ws = Tensor::empty({2, 1, 6}, DType::kFloat32, kGpu);
+  const Tensor host_q = p.query;
+  const Tensor wide_q = random_uniform({2, 1, 5}, 3, -1, 1).to(kGpu);
+  const Tensor three_heads = random_uniform({3, 1, 4}, 4, -1, 1).to(kGpu);
+  Tensor small_ws = Tensor::empty({2, 1, 5}, DType::kFloat32, kGpu);
+  Tensor wrong_out = Tensor::empty({2, 1, 4}, DType::kFloat32, kGpu);
+  struct Row {
+    const char* what;
+    std::function<void()> call;
+    ErrorCode code;
   };
-  constexpr std::array kProblems{Problem{1, 1, 3, 1, 2, 2}, Problem{2, 3, 5, 5, 7, 2},
-                                 Problem{3, 7, 11, 37, 41, 4}};
-  Stream stream;
-  for (const Problem p : kProblems) {
-    const auto kv_tokens = static_cast<std::size_t>(p.keys);
-    const auto per_block = static_cast<std::size_t>(p.block_tokens);
-    const std::size_t logical = 1 + (kv_tokens - 1) / per_block;
-    const std::size_t physical = logical + 2;
-    const auto table = reversed_block_table(logical, physical);
-    const auto offset = static_cast<std::size_t>(p.keys - p.queries);
-    const Tensor q = random_uniform({p.heads, p.queries, p.key_dimension}, 8101, -1, 1);
-    const Tensor k = random_uniform({p.heads, p.keys, p.key_dimension}, 8102, -1, 1);
-    const Tensor v = random_uniform({p.heads, p.keys, p.value_dimension}, 8103, -1, 1);
-    const auto expected = cpu_sdpa(q, k, v, offset).first;
-    const auto pd = static_cast<Dimension>(physical);
-    const Tensor kb = pack_logical_blocks(k, table, pd, p.block_tokens, 77.0F).to(kGpu);
-    const Tensor vb = pack_logical_blocks(v, table, pd, p.block_tokens, -77.0F).to(kGpu);
-    PagedBlockTable block_table(table, physical, 0);
-    const Tensor actual = paged_scaled_dot_product_attention(q.to(kGpu), kb, vb, block_table,
-                                                             kv_tokens, offset, stream);
-    stream.synchronize();
-    expect_close(actual, expected, 2.0e-5F + static_cast<float>(p.key_dimension) * 1.0e-6F);
-  }
-}
-
-// tests/cuda_attention_test.cpp:275-288
-TEST_F(HipAttentionTest, PagedPathAcceptsEmptyQueriesWithoutLaunching) {
-  constexpr std::array<std::uint32_t, 3> kBlockTable{3, 1, 0};
-  const Tensor query = Tensor::zeros({2, 0, 5}, DType::kFloat32, kGpu);
-  const Tensor key_blocks = Tensor::zeros({4, 2, 3, 5}, DType::kFloat32, kGpu);
-  const Tensor value_blocks = Tensor::zeros({4, 2, 3, 7}, DType::kFloat32, kGpu);
-  PagedBlockTable block_table(kBlockTable, 4, 0);
-  Stream stream;
-  const Tensor output =
-      paged_scaled_dot_product_attention(query, key_blocks, value_blocks, block_table, 7, 7, stream);
-  EXPECT_TRUE(output.shape() == (Shape{2, 0, 7}));
-  EXPECT_EQ(output.numel(), 0U);
-  EXPECT_EQ(paged_score_workspace_bytes(query, key_blocks, block_table, 7), 0U);
-}
-
-// tests/cuda_attention_test.cpp:290-374
-TEST_F(HipAttentionTest, PagedPathRejectsInvalidTablesGeometryOffsetsAndAliasing) {
-  constexpr std::array<std::uint32_t, 2> kBlockIds{2, 0};
-  constexpr std::array<std::uint32_t, 1> kShortBlockIds{0};
-  constexpr std::array<std::uint32_t, 1> kOutOfRangeBlockId{3};
-  const Tensor query = Tensor::zeros({1, 2, 2}, DType::kFloat32, kGpu);
-  const Tensor key_blocks = Tensor::zeros({3, 1, 2, 2}, DType::kFloat32, kGpu);
-  const Tensor value_blocks = Tensor::zeros({3, 1, 2, 2}, DType::kFloat32, kGpu);
-  Tensor output = Tensor::zeros({1, 2, 2}, DType::kFloat32, kGpu);
-  Tensor workspace = Tensor::zeros({1, 2, 3}, DType::kFloat32, kGpu);
-  Stream stream;
-
-  PagedBlockTable empty_table(std::span<const std::uint32_t>{}, 3, 0);
-  EXPECT_TRUE(empty_table.valid());
-  EXPECT_TRUE(empty_table.data() == nullptr);
-  EXPECT_EQ(empty_table.logical_block_count(), 0U);
-  EXPECT_EQ(empty_table.size_bytes(), 0U);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, empty_table, 1, 0, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(PagedBlockTable(std::span<const std::uint32_t>{}, 0, 0)), Error);
-  EXPECT_THROW(static_cast<void>(PagedBlockTable(kShortBlockIds, 0, 0)), Error);
-  EXPECT_THROW(static_cast<void>(PagedBlockTable(kOutOfRangeBlockId, 3, 0)), Error);
-  EXPECT_THROW(static_cast<void>(PagedBlockTable(kShortBlockIds, 3, -1)), Error);
-
-  PagedBlockTable original(kBlockIds, 3, 0);
-  PagedBlockTable block_table(std::move(original));
-  EXPECT_FALSE(original.valid());
-  EXPECT_TRUE(block_table.valid());
-  EXPECT_EQ(block_table.logical_block_count(), 2U);
-  EXPECT_EQ(block_table.physical_block_count(), 3U);
-  EXPECT_EQ(block_table.size_bytes(), 2U * sizeof(std::uint32_t));
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, original, 3, 1, stream)),
-               Error);
-  PagedBlockTable short_table(kShortBlockIds, 3, 0);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, short_table, 3, 1, stream)),
-               Error);
-  PagedBlockTable wrong_capacity(kBlockIds, 4, 0);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, wrong_capacity, 3, 1, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, block_table, 0, 0, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, value_blocks, block_table, 3, 2, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   Tensor::zeros({1, 2, 2}), key_blocks, value_blocks, block_table, 3, 1, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, Tensor::zeros({3, 2, 2}, DType::kFloat32, kGpu), value_blocks,
-                   block_table, 3, 1, stream)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_scaled_dot_product_attention(
-                   query, key_blocks, Tensor::zeros({3, 1, 3, 2}, DType::kFloat32, kGpu),
-                   block_table, 3, 1, stream)),
-               Error);
-
-  Tensor output_alias = query;
-  EXPECT_THROW(paged_scaled_dot_product_attention_out(query, key_blocks, value_blocks, block_table,
-                                                      3, 1, output_alias, workspace, stream),
-               Error);
-  Tensor shared = Tensor::zeros({1, 2, 3}, DType::kFloat32, kGpu);
-  const Tensor three_value_blocks = Tensor::zeros({3, 1, 2, 3}, DType::kFloat32, kGpu);
-  EXPECT_THROW(paged_scaled_dot_product_attention_out(query, key_blocks, three_value_blocks,
-                                                      block_table, 3, 1, shared, shared, stream),
-               Error);
-
-  PagedBlockTable reassigned(kShortBlockIds, 3, 0);
-  reassigned = std::move(block_table);
-  EXPECT_FALSE(block_table.valid());
-  EXPECT_TRUE(reassigned.valid());
-  EXPECT_NO_THROW(paged_scaled_dot_product_attention_out(query, key_blocks, value_blocks,
-                                                         reassigned, 3, 1, output, workspace,
-                                                         stream));
-  stream.synchronize();
-}
-
-// tests/cuda_attention_test.cpp:376-449
-TEST_F(HipAttentionTest, PagedTailMatchesCpuForEmptyHistoryOddPagesAndChunkedContinuation) {
-  struct Problem {
-    Dimension heads, history_tokens, tail_tokens, key_dimension, value_dimension, block_tokens;
+  auto tail = [&](const Tensor& query, const PagedBlockTable& t, std::size_t hist, Tensor& o,
+                  Tensor& w) {
+    attn::paged_scaled_dot_product_attention_with_tail_out(query, kp, vp, t, hist, tk, tv, o, w,
+                                                           stream);
   };
-  constexpr std::array kProblems{Problem{1, 0, 1, 1, 2, 2}, Problem{2, 3, 1, 5, 7, 2},
-                                 Problem{3, 5, 3, 37, 41, 4}};
-  Stream stream;
-  for (const Problem p : kProblems) {
-    const auto history = static_cast<std::size_t>(p.history_tokens);
-    const auto per_block = static_cast<std::size_t>(p.block_tokens);
-    const std::size_t logical = history == 0 ? 0 : 1 + (history - 1) / per_block;
-    const std::size_t physical = logical + 2;
-    const auto table = reversed_block_table(logical, physical);
-    const Tensor q = random_uniform({p.heads, p.tail_tokens, p.key_dimension}, 8201, -1, 1);
-    const Tensor hk = random_uniform({p.heads, p.history_tokens, p.key_dimension}, 8202, -1, 1);
-    const Tensor hv = random_uniform({p.heads, p.history_tokens, p.value_dimension}, 8203, -1, 1);
-    const Tensor tk = random_uniform({p.heads, p.tail_tokens, p.key_dimension}, 8204, -1, 1);
-    const Tensor tv = random_uniform({p.heads, p.tail_tokens, p.value_dimension}, 8205, -1, 1);
-    const auto [expected_output, expected_workspace] =
-        cpu_sdpa(q, concatenate_token_axis(hk, tk), concatenate_token_axis(hv, tv), history);
-
-    const auto pd = static_cast<Dimension>(physical);
-    const Tensor query = q.to(kGpu);
-    const Tensor kb = pack_logical_blocks(hk, table, pd, p.block_tokens, 10000.0F).to(kGpu);
-    const Tensor vb = pack_logical_blocks(hv, table, pd, p.block_tokens, -10000.0F).to(kGpu);
-    const Tensor tail_key = tk.to(kGpu), tail_value = tv.to(kGpu);
-    PagedBlockTable block_table(table, physical, 0);
-    const Shape ws_shape{p.heads, p.tail_tokens, p.history_tokens + p.tail_tokens};
-    Tensor output = Tensor::empty({p.heads, p.tail_tokens, p.value_dimension}, DType::kFloat32, kGpu);
-    Tensor workspace = Tensor::empty(ws_shape, DType::kFloat32, kGpu);
-    EXPECT_TRUE(paged_tail_score_workspace_shape(query, kb, vb, block_table, history, tail_key,
-                                                 tail_value) == ws_shape);
-    EXPECT_EQ(paged_tail_score_workspace_bytes(query, kb, vb, block_table, history, tail_key,
-                                               tail_value),
-              shape_numel(ws_shape) * sizeof(float));
-    paged_scaled_dot_product_attention_with_tail_out(query, kb, vb, block_table, history, tail_key,
-                                                     tail_value, output, workspace, stream);
-    stream.synchronize();
-    const float tolerance = 2.0e-5F + static_cast<float>(p.key_dimension) * 1.0e-6F;
-    expect_close(output, expected_output, tolerance);
-    expect_close(workspace, expected_workspace, 2.0e-6F);
-    expect_close(paged_scaled_dot_product_attention_with_tail(query, kb, vb, block_table, history,
-                                                              tail_key, tail_value, stream),
-                 expected_output, tolerance);
+  const std::vector<Row> rows{
+      {"table shorter than the history", [&] { tail(q, short_table, 5, out, ws); },
+       ErrorCode::kInvalidArgument},
+      {"history beyond the table", [&] { tail(q, table, 7, out, ws); }, ErrorCode::kInvalidArgument},
+      {"query on the host", [&] { tail(host_q, table, 5, out, ws); }, ErrorCode::kInvalidArgument},
+      {"query width differs from the keys", [&] { tail(wide_q, table, 5, out, ws); },
+       ErrorCode::kInvalidArgument},
+      {"query heads not a multiple of kv heads", [&] { tail(three_heads, table, 5, out, ws); },
+       ErrorCode::kInvalidArgument},
+      {"workspace of the wrong length", [&] { tail(q, table, 5, out, small_ws); },
+       ErrorCode::kInvalidArgument},
+      {"output of the wrong width", [&] { tail(q, table, 5, wrong_out, ws); },
+       ErrorCode::kInvalidArgument},
+      {"output aliasing the workspace",
+       [&] {
+         Tensor alias = ws.reshape({12}).reshape({2, 1, 6});
+         Tensor o = Tensor::borrow(alias.raw(), {2, 1, 3}, DType::kFloat32, kGpu);
+         tail(q, table, 5, o, ws);
+       },
+       ErrorCode::kInvalidArgument},
+      {"history-only offset past the keys",
+       [&] {
+         Tensor w5 = Tensor::empty({2, 1, 5}, DType::kFloat32, kGpu);
+         attn::paged_scaled_dot_product_attention_out(q, kp, vp, table, 5, 5, out, w5, stream);
+       },
+       ErrorCode::kInvalidArgument},
+  };
+  for (const Row& r : rows) {
+    const auto code = thrown_code(r.call);
+    if (!code.has_value() || *code != r.code) {
+      ::mini_test::fail(__FILE__, __LINE__, std::string("wrong outcome: ") + r.what);
+    }
   }
-}
-
-// tests/cuda_attention_test.cpp:451-531
-TEST_F(HipAttentionTest, PagedTailRejectsInvalidGeometryLifetimeAndAliasesBeforeLaunch) {
-  constexpr std::array<std::uint32_t, 2> kBlockIds{2, 0};
-  const Tensor query = Tensor::zeros({1, 2, 2}, DType::kFloat32, kGpu);
-  const Tensor key_blocks = Tensor::zeros({3, 1, 2, 2}, DType::kFloat32, kGpu);
-  const Tensor value_blocks = Tensor::zeros({3, 1, 2, 3}, DType::kFloat32, kGpu);
-  const Tensor tail_key = Tensor::zeros({1, 2, 2}, DType::kFloat32, kGpu);
-  const Tensor tail_value = Tensor::zeros({1, 2, 3}, DType::kFloat32, kGpu);
-  Tensor output = Tensor::zeros({1, 2, 3}, DType::kFloat32, kGpu);
-  Tensor workspace = Tensor::zeros({1, 2, 5}, DType::kFloat32, kGpu);
-  PagedBlockTable block_table(kBlockIds, 3, 0);
-  Stream stream;
-
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table,
-                   std::numeric_limits<std::size_t>::max(), tail_key, tail_value)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   Tensor::zeros({1, 0, 2}, DType::kFloat32, kGpu), key_blocks, value_blocks,
-                   block_table, 3, Tensor::zeros({1, 0, 2}, DType::kFloat32, kGpu),
-                   Tensor::zeros({1, 0, 3}, DType::kFloat32, kGpu))),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table, 3, Tensor::zeros({2, 2}),
-                   tail_value)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table, 3,
-                   Tensor::zeros({1, 1, 2}, DType::kFloat32, kGpu), tail_value)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table, 3,
-                   Tensor::zeros({1, 2, 3}, DType::kFloat32, kGpu), tail_value)),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table, 3, tail_key,
-                   Tensor::zeros({1, 2, 4}, DType::kFloat32, kGpu))),
-               Error);
-  EXPECT_THROW(static_cast<void>(paged_tail_score_workspace_shape(
-                   query, key_blocks, value_blocks, block_table, 3,
-                   Tensor::zeros({1, 2, 2}, DType::kUInt32, kGpu), tail_value)),
-               Error);
-
-  Tensor output_alias = tail_value;
-  EXPECT_THROW(paged_scaled_dot_product_attention_with_tail_out(
-                   query, key_blocks, value_blocks, block_table, 3, tail_key, tail_value,
-                   output_alias, workspace, stream),
-               Error);
-  Tensor workspace_alias = tail_key;
-  EXPECT_THROW(paged_scaled_dot_product_attention_with_tail_out(
-                   query, key_blocks, value_blocks, block_table, 3, tail_key, tail_value, output,
-                   workspace_alias, stream),
-               Error);
-  EXPECT_THROW(paged_scaled_dot_product_attention_with_tail_out(query, key_blocks, value_blocks,
-                                                                block_table, 3, tail_key,
-                                                                tail_value, output, output, stream),
-               Error);
-
-  // A tail value and an output that overlap by half inside one allocation.
-  Tensor allocation = Tensor::zeros({192}, DType::kFloat32, kGpu);
-  const Tensor wide_value_blocks = Tensor::zeros({3, 1, 2, 64}, DType::kFloat32, kGpu);
-  const Tensor partial_tail_value =
-      Tensor::borrow(allocation.raw(), {1, 2, 64}, DType::kFloat32, kGpu);
-  Tensor partial_output = Tensor::borrow(allocation.data<float>() + 64, {1, 2, 64},
-                                         DType::kFloat32, kGpu);
-  EXPECT_THROW(paged_scaled_dot_product_attention_with_tail_out(
-                   query, key_blocks, wide_value_blocks, block_table, 3, tail_key,
-                   partial_tail_value, partial_output, workspace, stream),
-               Error);
-
-  Stream active_stream = std::move(stream);
-  EXPECT_THROW(paged_scaled_dot_product_attention_with_tail_out(query, key_blocks, value_blocks,
-                                                                block_table, 3, tail_key,
-                                                                tail_value, output, workspace,
-                                                                stream),
-               Error);
-  EXPECT_NO_THROW(paged_scaled_dot_product_attention_with_tail_out(
-      query, key_blocks, value_blocks, block_table, 3, tail_key, tail_value, output, workspace,
-      active_stream));
-  active_stream.synchronize();
-}
-
-// tests/cuda_attention_test.cpp:533-556
-TEST_F(HipAttentionTest, PagedTailCausalMaskDoesNotReadFutureNonFiniteValue) {
-  const float nan = std::numeric_limits<float>::quiet_NaN();
-  const Tensor query = Tensor::zeros({1, 2, 1}, DType::kFloat32, kGpu);
-  const Tensor key_blocks = Tensor::zeros({1, 1, 2, 1}, DType::kFloat32, kGpu);
-  const Tensor value_blocks = Tensor::zeros({1, 1, 2, 1}, DType::kFloat32, kGpu);
-  const Tensor tail_key = Tensor::from_values({1, 2, 1}, std::array{0.0F, nan}, kGpu);
-  const Tensor tail_value = Tensor::from_values({1, 2, 1}, std::array{3.0F, nan}, kGpu);
-  Tensor output = Tensor::empty({1, 2, 1}, DType::kFloat32, kGpu);
-  Tensor workspace = Tensor::empty({1, 2, 2}, DType::kFloat32, kGpu);
-  PagedBlockTable block_table(std::span<const std::uint32_t>{}, 1, 0);
-  Stream stream;
-  paged_scaled_dot_product_attention_with_tail_out(query, key_blocks, value_blocks, block_table, 0,
-                                                   tail_key, tail_value, output, workspace, stream);
   stream.synchronize();
-  const auto out = host_values(output);
-  const auto ws = host_values(workspace);
-  EXPECT_FLOAT_EQ(out[0], 3.0F);
-  EXPECT_TRUE(std::isnan(out[1]));
-  EXPECT_FLOAT_EQ(ws[0], 1.0F);
-  EXPECT_FLOAT_EQ(ws[1], 0.0F);
+  EXPECT_TRUE(host_values(out) == sentinel);
+  // Empty queries are valid and launch nothing.
+  Tensor empty_out = Tensor::empty({2, 0, 3}, DType::kFloat32, kGpu);
+  Tensor empty_ws = Tensor::empty({2, 0, 5}, DType::kFloat32, kGpu);
+  EXPECT_NO_THROW(attn::paged_scaled_dot_product_attention_out(
+      Tensor::empty({2, 0, 4}, DType::kFloat32, kGpu), kp, vp, table, 5, 0, empty_out, empty_ws,
+      stream));
+}
+
+// A non-finite value in a tail row that a query row masks causally must not
+// reach that row (the reference skips masked keys; 0 * NaN would not).
+TEST_F(HipAttentionTest, MaskedNonFiniteTailRowsDoNotLeak) {
+  const PagedProblem p = make_problem(91, 1, 3, 4, 4, 2, 3, 3);
+  std::vector<float> tv(p.tail_value.data_as<float>(), p.tail_value.data_as<float>() + 12);
+  std::vector<float> tk(p.tail_key.data_as<float>(), p.tail_key.data_as<float>() + 12);
+  for (int c = 0; c < 4; ++c) {
+    tv[2 * 4 + c] = std::numeric_limits<float>::quiet_NaN();  // row 2: seen by query 2 only
+    tk[1 * 4 + c] = std::numeric_limits<float>::infinity();   // row 1: +inf scores from query 1 on
+  }
+  Stream stream;
+  const PagedBlockTable table(p.table, p.physical, 0);
+  Tensor out = Tensor::empty({1, 3, 4}, DType::kFloat32, kGpu);
+  Tensor ws = Tensor::empty({1, 3, 6}, DType::kFloat32, kGpu);
+  attn::paged_scaled_dot_product_attention_with_tail_probabilities_out(
+      p.query.to(kGpu), p.key_pool.to(kGpu), p.value_pool.to(kGpu), table, 3,
+      Tensor::from_values({1, 3, 4}, tk, kGpu), Tensor::from_values({1, 3, 4}, tv, kGpu), out, ws,
+      stream);
+  stream.synchronize();
+  std::vector<float> want(12), want_ws(18);
+  ASSERT_EQ(oracle_paged_attention(p.query.data_as<float>(), 1, 1, 3, 4, 4,
+                                   p.key_pool.data_as<float>(), p.value_pool.data_as<float>(), 2,
+                                   p.table.data(), 3, tk.data(), tv.data(), 3, 3, want.data(),
+                                   want_ws.data()),
+            0);
+  const auto got = host_values(out);
+  for (std::size_t i = 0; i < 12; ++i) {
+    EXPECT_EQ(std::isnan(got[i]), std::isnan(want[i]));
+    if (!std::isnan(want[i])) EXPECT_NEAR(got[i], want[i], 2e-5F);
+  }
+  for (std::size_t i = 0; i < 4; ++i) EXPECT_FALSE(std::isnan(got[i]));  // query 0
+}
+
+// The model's per-layer call at head_dim 128 and 16-token pages runs the
+// stream decode kernel (score workspace as scratch); its output equals the
+// probability-contract route's within the north-star tolerance and matches
+// the oracle, for MHA and GQA.
+TEST_F(HipAttentionTest, DecodeCallsTakeTheStreamRoute) {
+  Stream stream;
+  for (const auto& [hkv, group, history] :
+       std::vector<std::array<std::size_t, 3>>{{8, 4, 1500}, {4, 1, 700}, {2, 8, 3000}}) {
+    const std::size_t hq = hkv * group;
+    std::mt19937_64 rng(history);
+    const std::size_t logical = (history + 15) / 16, physical = logical + 2;
+    std::vector<std::uint32_t> perm(physical);
+    std::iota(perm.begin(), perm.end(), 0U);
+    std::shuffle(perm.begin(), perm.end(), rng);
+    const std::vector<std::uint32_t> ids(perm.begin(), perm.begin() + static_cast<std::ptrdiff_t>(logical));
+    const auto P = static_cast<Dimension>(physical), Hk = static_cast<Dimension>(hkv);
+    const Tensor kp = random_uniform({P, Hk, 16, 128}, history + 1, -1, 1);
+    const Tensor vp = random_uniform({P, Hk, 16, 128}, history + 2, -1, 1);
+    const Tensor q = random_uniform({static_cast<Dimension>(hq), 1, 128}, history + 3, -1, 1);
+    const Tensor tk = random_uniform({Hk, 1, 128}, history + 4, -1, 1);
+    const Tensor tv = random_uniform({Hk, 1, 128}, history + 5, -1, 1);
+    const PagedBlockTable table(ids, physical, 0);
+    const Tensor dkp = kp.to(kGpu), dvp = vp.to(kGpu), dq = q.to(kGpu);
+    const Tensor dtk = tk.to(kGpu), dtv = tv.to(kGpu);
+    const Shape os{static_cast<Dimension>(hq), 1, 128};
+    const Shape wss{static_cast<Dimension>(hq), 1, static_cast<Dimension>(history + 1)};
+    Tensor fast = Tensor::empty(os, DType::kFloat32, kGpu), exact = Tensor::empty(os, DType::kFloat32, kGpu);
+    Tensor ws = Tensor::empty(wss, DType::kFloat32, kGpu), ws2 = Tensor::empty(wss, DType::kFloat32, kGpu);
+    attn::paged_scaled_dot_product_attention_with_tail_out(dq, dkp, dvp, table, history, dtk, dtv,
+                                                           fast, ws, stream);
+    attn::paged_scaled_dot_product_attention_with_tail_probabilities_out(
+        dq, dkp, dvp, table, history, dtk, dtv, exact, ws2, stream);
+    stream.synchronize();
+    const std::int32_t len = static_cast<std::int32_t>(history);
+    std::vector<float> want(hq * 128);
+    oracle_batched_decode(q.data_as<float>(), 1, hq, hkv, 128, kp.data_as<float>(),
+                          vp.data_as<float>(), 16, ids.data(), logical, &len, tk.data_as<float>(),
+                          tv.data_as<float>(), want.data(), 4);
+    const auto a = host_values(fast), b = host_values(exact);
+    for (std::size_t i = 0; i < want.size(); ++i) {
+      EXPECT_TRUE(std::fabs(a[i] - want[i]) <= 2.0e-5F + 1.0e-4F * std::fabs(want[i]));
+      EXPECT_TRUE(std::fabs(b[i] - want[i]) <= 2.0e-5F + 1.0e-4F * std::fabs(want[i]));
+    }
+  }
 }
 
 // ---------------------------------------------------------- decode batch ----

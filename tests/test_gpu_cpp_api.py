@@ -1,9 +1,9 @@
-"""The reference's own CUDA cache and paged-attention tests
-(tests/cuda_paged_kv_cache_test.cpp, tests/cuda_attention_test.cpp:196-556),
-restated in C++ against include/helix_paged.hpp and run on the GPU, plus the
-extensions (fork with copy-on-write, bulk append, gather, prefix cache,
-DecodeBatch against the oracle).  One process runs every case; the binary
-prints each case's name before it runs."""
+"""The C++ API suite (tests/cpp/paged_api_test.cpp) on the GPU: the golden
+fixtures of tests/golden/ replayed through include/helix_paged.hpp, random
+operation programs against the oracle pool, invalid-call tables, the read
+lease, seeded attention sweeps, the stream route of the decode entry point
+and the extensions.  One process runs every case; the binary prints each
+case's name before it runs."""
 
 import os
 import subprocess
@@ -23,4 +23,4 @@ def test_cpp_api_suite_passes_on_gpu():
     print(r.stdout[-4000:])
     print(r.stderr[-4000:])
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
-    assert "20 ran, 0 skipped, 0 failed" in r.stdout
+    assert "15 ran, 0 skipped, 0 failed" in r.stdout
