@@ -44,32 +44,42 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def decode_bytes(lengths, hq=HQ, hkv=HKV, d=D, p=P):
+def decode_bytes(lengths, hq=None, hkv=None, d=D, p=P):
     """Algorithmic HBM bytes of one decode-attention launch (one layer):
     sum over sequences of K+V history (each byte once per KV head), the K/V
     tail, Q in and O out, and the block-table entries."""
+    hq, hkv = hq or HQ, hkv or HKV
     lengths = np.asarray(lengths, np.int64)
     return int(np.sum(2 * hkv * lengths * d * PAGE_BYTES + 2 * hkv * d * 4 + 2 * hq * d * 4 +
                       ((lengths + p - 1) // p) * 4))
 
 
-def append_bytes(batch, hkv=HKV, d=D):
+def append_bytes(batch, hkv=None, d=D):
     """Read the fp32 source row + write the page row, keys and values, one
     token per sequence."""
+    hkv = hkv or HKV
     return 2 * hkv * d * (4 + PAGE_BYTES) * batch
 
 
-def append_write_bytes(batch, hkv=HKV, d=D):
+def append_write_bytes(batch, hkv=None, d=D):
     """The page writes of append_bytes alone."""
+    hkv = hkv or HKV
     return 2 * hkv * d * PAGE_BYTES * batch
 
 
-def build_workload(seed, batch, layers, steps_total, shuffle=True):
+def build_workload(seed, batch, layers, steps_total, shuffle=True, config=3):
+    """Config 3: contexts log-uniform in [512, 8192], pool sized to the need.
+    Config 2: contexts uniform in [128, 2048], pool 1.25x the need."""
     rng = np.random.default_rng(seed)
-    lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=batch)).astype(np.int64)
+    if config == 2:
+        lengths = rng.integers(128, 2049, size=batch).astype(np.int64)
+    else:
+        lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=batch)).astype(np.int64)
     pages = (lengths + P - 1) // P
     grow = (steps_total + P) // P + 1
     n_phys = int(pages.sum() + batch * grow + 16)
+    if config == 2:
+        n_phys = int(math.ceil(1.25 * n_phys))
     cache = hx.PagedKvCache(layers, HKV, D, P, n_phys, page_dtype=PAGE_DTYPE)
     log(f"pool: {n_phys} blocks x {layers} layers "
         f"({n_phys * layers * 2 * HKV * P * D * PAGE_BYTES / 1e9:.1f} GB)")
@@ -153,10 +163,11 @@ def build_prefix_workload(seed, layers, steps_total):
     return cache, seqs, lengths
 
 
-def unique_decode_bytes(lengths, shared_tokens=PREFIX_TOKENS, hq=HQ, hkv=HKV, d=D, p=P):
+def unique_decode_bytes(lengths, shared_tokens=PREFIX_TOKENS, hq=None, hkv=None, d=D, p=P):
     """HBM bytes of one config-4 decode launch when every shared prefix page
     is read from HBM once: the logical formula with the shared tokens counted
     once instead of once per sequence."""
+    hq, hkv = hq or HQ, hkv or HKV
     lengths = np.asarray(lengths, np.int64)
     shared = 2 * hkv * shared_tokens * d * PAGE_BYTES
     own = 2 * hkv * (lengths - shared_tokens) * d * PAGE_BYTES
@@ -436,6 +447,95 @@ def run_reference_entry(args):
     cache.close()
 
 
+def run_tiny(args):
+    """Config 1: the tiny reference-shaped decode (1 sequence, 4/4 heads,
+    head_dim 16, 16-token pages, a 64-token history in 4 pages drawn by a
+    seeded permutation from an 8-page pool, one-token tail), through
+    paged_scaled_dot_product_attention_with_tail_out.  head_dim 16 is outside
+    the batched kernels' geometry, so the call runs the exact kernel and
+    writes the probabilities.  A latency measurement: `value` is the device
+    time per call (calls queued back to back behind a device-side sleep so
+    host overhead is hidden); `call_wall_us` is the host-inclusive rate of
+    calls issued one after another."""
+    rng = np.random.default_rng(1)
+    table = rng.permutation(8)[:4].astype(np.int32)
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")  # noqa: E731
+    kp_h = rng.standard_normal((8, 4, 16, 16), dtype=np.float32)
+    vp_h = rng.standard_normal((8, 4, 16, 16), dtype=np.float32)
+    q_h = rng.standard_normal((4, 1, 16), dtype=np.float32)
+    tk_h = rng.standard_normal((4, 1, 16), dtype=np.float32)
+    tv_h = rng.standard_normal((4, 1, 16), dtype=np.float32)
+    kp, vp, q, tk, tv, tab = dv(kp_h), dv(vp_h), dv(q_h), dv(tk_h), dv(tv_h), dv(table)
+    out = torch.empty(4, 1, 16, device="cuda:0")
+    ws = torch.empty(4, 1, 65, device="cuda:0")
+    stream = torch.cuda.current_stream()
+
+    def call():
+        hx.paged_attention_with_tail_out(q, kp, vp, tab, 64, tk, tv, out, ws, stream)
+
+    for _ in range(args.warmup + 5):
+        call()
+    torch.cuda.synchronize()
+    reps = max(200, args.steps * 20)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(50_000_000)
+    e0.record(stream)
+    for _ in range(reps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dev_us = e0.elapsed_time(e1) * 1e3 / reps
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) * 1e6 / reps
+    # Algorithmic bytes: the 4 history pages of K and V (4 heads x 16 tokens
+    # x 16 dims), tail K/V, query, output, table, probability workspace.
+    nbytes = 2 * 4 * 64 * 16 * 4 + 2 * 4 * 16 * 4 + 2 * 4 * 16 * 4 + 4 * 4 + 4 * 65 * 4
+    gbps = nbytes / (dev_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        got = out.cpu().numpy()
+        n = 2000
+        t0 = time.perf_counter()
+        for _ in range(n):
+            ref, _ = oracle.paged_attention(q_h, kp_h, vp_h, table.astype(np.uint32), 64, tk_h,
+                                            tv_h)
+        cpu_us = (time.perf_counter() - t0) * 1e6 / n
+        err = float(np.abs(got - ref).max())
+        if not (np.abs(got - ref) <= 2e-5 + 1e-4 * np.abs(ref)).all():
+            raise SystemExit(f"config 1 parity failure: max abs err {err}")
+        hostinfo = host_cpu()
+        cpu = {"value": round(cpu_us, 3), "unit": "us per call", "cores": 1, "kind": "port",
+               "threads": 1, "nproc": hostinfo["nproc"], "usable_cpus": hostinfo["usable_cpus"],
+               "cpu_model": hostinfo["cpu_model"],
+               "sample": f"CPU oracle (C++ restatement of the reference CPU paged attention, "
+                         f"fp64 accumulation) on the same inputs, {n} calls on one thread "
+                         f"including the ctypes call; GPU output matched it to max abs err "
+                         f"{err:.2e}"}
+    line = {
+        "metric": "tiny paged decode latency (config 1, reference-shaped entry point)",
+        "value": round(dev_us, 3), "unit": "us per call", "n_gpus": 1, "steps": reps,
+        "warmup": args.warmup + 5, "ms_per_step": round(dev_us * 1e-3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic N(0,1) K/V/Q, seeded (numpy default_rng(1))",
+        "config": {"workload": "config1: 1 sequence, 1 layer, 4/4 heads, head_dim 16, page 16, "
+                               "64-token history in 4 of 8 pages (seeded permutation), "
+                               "one-token tail", "q_heads": 4, "kv_heads": 4, "head_dim": 16,
+                   "block_tokens": 16, "history": 64},
+        "call_wall_us": round(wall_us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 3), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 8),
+                     "traffic": None,
+                     "note": "latency-bound: 35 KB per call; the time is the kernel's launch "
+                             "and its three dependent passes, not HBM bandwidth"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 # Llama-3-8B decoder shapes for --model-step.
 MODEL_HIDDEN, MODEL_INTER, MODEL_VOCAB, ROPE_THETA = 4096, 14336, 128256, 500000.0
 
@@ -584,9 +684,10 @@ MFMA_F32_PEAK_TFLOPS = 157.3
 CHUNK_BATCH, CHUNK_TOKENS = 16, 512
 
 
-def prefill_flops(hists, t=CHUNK_TOKENS, hq=HQ, d=D):
+def prefill_flops(hists, t=CHUNK_TOKENS, hq=None, d=D):
     """Algorithmic FLOPs of one chunked-prefill launch (one layer): QK^T and
     P.V over the history plus the causal triangle of the chunk."""
+    hq = hq or HQ
     hists = np.asarray(hists, np.float64)
     return float(np.sum(4.0 * hq * d * (t * hists + t * (t + 1) / 2.0)))
 
@@ -763,7 +864,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--layers", type=int, default=None,
+                    help="layers of the pool and step (default: 32; config 2: 1, the "
+                         "single-layer MHA decode BASELINE names)")
     ap.add_argument("--pages-per-split", type=int, default=0,
                     help="decode split size in pages (0: library default)")
     ap.add_argument("--cpu-layers", type=int, default=32,
@@ -778,8 +881,9 @@ def main():
                          "of the append fused into each layer's decode launch)")
     ap.add_argument("--no-shuffle", action="store_true",
                     help="allocate pages in pool order instead of scattering them")
-    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
-                    help="3: batched GQA decode (default, the headline metric); "
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5),
+                    help="3: batched GQA decode (default, the headline metric); 1: the tiny "
+                         "reference-shaped decode (latency); 2: batch-8 MHA decode; "
                          "4: prefix-sharing decode; 5: chunked prefill on the matrix cores")
     ap.add_argument("--cpu-seqs", type=int, default=4,
                     help="config 5: sequences of layer 0 timed on the CPU oracle")
@@ -805,8 +909,12 @@ def main():
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    global PAGE_DTYPE, PAGE_BYTES
+    global PAGE_DTYPE, PAGE_BYTES, HQ, HKV, BATCH
     PAGE_DTYPE, PAGE_BYTES = args.page_dtype, (2 if args.page_dtype == "bf16" else 4)
+    if args.layers is None:
+        args.layers = 1 if args.config == 2 else LAYERS
+    if args.config == 2:
+        HQ, HKV, BATCH = 32, 32, 8
     torch.cuda.set_device(0)
     if args.copy_probe:
         copy_probe()
@@ -823,6 +931,9 @@ def main():
     if args.config == 5:
         run_prefill(args)
         return
+    if args.config == 1:
+        run_tiny(args)
+        return
     # warmup, the timed steps, then as many instrumented steps (per-kernel events)
     steps_total = args.warmup + 2 * args.steps + 2
     t_setup = time.perf_counter()
@@ -830,7 +941,7 @@ def main():
         cache, seqs, lengths0 = build_prefix_workload(args.seed, args.layers, steps_total)
     else:
         cache, seqs, lengths0 = build_workload(args.seed, BATCH, args.layers, steps_total,
-                                                 shuffle=not args.no_shuffle)
+                                                 shuffle=not args.no_shuffle, config=args.config)
     nseq = len(seqs)
     log(f"setup {time.perf_counter() - t_setup:.1f}s; mean context {lengths0.mean():.0f}")
 
@@ -967,7 +1078,8 @@ def main():
                          f"fp64 accumulation), {threads} threads (one per usable host CPU, "
                          f"capped at the GPU box's {CPU_SHARE}-CPU share per GPU; host has "
                          f"{hostinfo['nproc']} logical CPUs, {hostinfo['usable_cpus']} usable) "
-                         f"over {args.cpu_layers} layers x all {nseq} sequences "
+                         f"over {args.cpu_layers} layer passes (the cache's {cache.layers} "
+                         f"layer(s) in turn) x all {nseq} sequences "
                          f"({secs:.1f} s wall), plus 1 thread (the reference's own mode) over "
                          f"{args.cpu_single_layers} layer(s) ({secs1:.1f} s). The reference has "
                          f"no GQA, so the CPU runs GQA as MHA with each KV head replicated for "
@@ -975,7 +1087,15 @@ def main():
                          f"byte, whose formula (each K/V byte once per KV head) is the GPU's. "
                          f"GPU kernel matched it on every sampled layer, max abs err {err:.2e}"}
 
-    if args.config == 4:
+    if args.config == 2:
+        metric = "paged decode attn GB/s (% of HBM peak) + append GB/s, 7B-MHA batch 8"
+        workload = {"workload": "config2: Llama-2-7B MHA decode, batch 8, 32q/32kv heads, "
+                                "head_dim 128, page 16, ctx uniform [128, 2048], pool 1.25x "
+                                "need, shuffled",
+                    "batch": nseq, "layers": L, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+                    "block_tokens": P, "mean_context": float(lengths0.mean()),
+                    "pages_per_split": split}
+    elif args.config == 4:
         metric = ("prefix-sharing paged decode attn GB/s on unique HBM bytes + append GB/s, "
                   "8B-GQA batch 128")
         workload = {"workload": "config4: prefix-sharing decode, 128 sequences share a 1024-token "

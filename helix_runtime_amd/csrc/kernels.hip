@@ -1669,9 +1669,49 @@ __global__ __launch_bounds__(kThreads) void generic_attention_kernel(GenericArgs
     srow[k] = p;
   }
 
-  // Pass 3: thread d accumulates sum_k p_k * V[k][d]; probabilities of a
-  // 256-key tile are staged in LDS by the threads that wrote them.
+  // Pass 3: P.V over the visible keys, 256 keys per tile.  The tile's
+  // probabilities are staged in LDS by the threads that wrote them.  With
+  // value_dim <= 256 the threads split into kThreads / value_dim key lanes:
+  // thread (lane, d) sums lane's keys of the tile for output dim d, the loads
+  // of different keys independent of each other, and the lanes are summed
+  // through LDS at the end.  Wider values keep one thread per dim (up to 4
+  // dims per thread) over every key.
   const std::size_t dv_count = a.value_dim;
+  auto value_row = [&](std::size_t key) -> const float* {
+    if (key >= a.history) return a.tail_value + (kvh * a.tail + (key - a.history)) * a.value_dim;
+    const std::size_t phys = a.table[key / a.block_tokens];
+    if (phys >= a.physical_blocks) return nullptr;
+    return a.value_blocks +
+           ((phys * a.kv_heads + kvh) * a.block_tokens + key % a.block_tokens) * a.value_dim;
+  };
+  if (dv_count <= kThreads) {
+    const std::size_t lanes = kThreads / dv_count;
+    const std::size_t d = threadIdx.x % dv_count;
+    const std::size_t lane = threadIdx.x / dv_count;
+    float acc = 0.0f;
+    for (std::size_t k0 = 0; k0 < visible; k0 += kThreads) {
+      const std::size_t k = k0 + threadIdx.x;
+      tile[threadIdx.x] = k < visible ? srow[k] : 0.0f;
+      __syncthreads();
+      const std::size_t n = visible - k0 < kThreads ? visible - k0 : kThreads;
+      if (lane < lanes) {
+        for (std::size_t kk = lane; kk < n; kk += lanes) {
+          const float* vrow = value_row(k0 + kk);
+          acc += vrow == nullptr ? NAN : tile[kk] * vrow[d];
+        }
+      }
+      __syncthreads();
+    }
+    // Sum the key lanes of each dim (tile is free again).
+    tile[threadIdx.x] = lane < lanes ? acc : 0.0f;
+    __syncthreads();
+    if (lane == 0) {
+      float sum = 0.0f;
+      for (std::size_t l = 0; l < lanes; ++l) sum += tile[l * dv_count + d];
+      a.out[(h * a.queries + qi) * a.value_dim + d] = sum;
+    }
+    return;
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};  // up to 4 output dims per thread
   for (std::size_t k0 = 0; k0 < visible; k0 += kThreads) {
     const std::size_t k = k0 + threadIdx.x;
@@ -1683,20 +1723,8 @@ __global__ __launch_bounds__(kThreads) void generic_attention_kernel(GenericArgs
       if (d >= dv_count) break;
       float s = acc[part];
       for (std::size_t kk = 0; kk < n; ++kk) {
-        const std::size_t key = k0 + kk;
-        const float* vrow;
-        if (key < a.history) {
-          const std::size_t phys = a.table[key / a.block_tokens];
-          if (phys >= a.physical_blocks) {
-            s = NAN;
-            continue;
-          }
-          vrow = a.value_blocks +
-                 ((phys * a.kv_heads + kvh) * a.block_tokens + key % a.block_tokens) * a.value_dim;
-        } else {
-          vrow = a.tail_value + (kvh * a.tail + (key - a.history)) * a.value_dim;
-        }
-        s += tile[kk] * vrow[d];
+        const float* vrow = value_row(k0 + kk);
+        s += vrow == nullptr ? NAN : tile[kk] * vrow[d];
       }
       acc[part] = s;
     }
