@@ -114,6 +114,7 @@ prefill_detail::PrefillKernelArgs prefill_detail::cascade_prefix_args(const Casc
   k.prefix_slot0 = static_cast<long long>(a.prefix_slot0);
   const std::size_t chunks =
       (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
+  k.cascade_chunks = static_cast<int>(chunks);
   *work_items = static_cast<std::size_t>(k.pos_blocks) * a.kv_heads * chunks;
   return k;
 }

@@ -65,6 +65,9 @@ constexpr int kCascadeTilesPerWave = 1;
 constexpr int kKeys = 16;       // keys per LDS stage (one page)
 constexpr int kKStride = D + 4; // padded K row: 8 consecutive rows hit distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
+// XCDs of the device: the dispatcher hands consecutive workgroups of a
+// launch to the XCDs in turn, and each XCD has its own L2.
+constexpr unsigned kXcds = 8;
 
 struct PrefillKernelArgs {
   const float* query;
@@ -88,6 +91,7 @@ struct PrefillKernelArgs {
   int batch;
   int cascade_keys;
   int cascade_chunk_pages;  // key pages per work item (the prefix is split)
+  int cascade_chunks;       // key chunks of the shared prefix
   float* part_o;
   float* part_ml;
   long long prefix_slot0;
@@ -204,17 +208,32 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   // longest-first order; by default later position blocks (more keys) of a
   // (sequence, kv head) go first.
   std::uint32_t item = block;
-  if (order != nullptr) {
-    item = order[block];
+  int pb, kvh, b, chunk;
+  if constexpr (CASCADE) {
+    // Cascade items, kv head major: (kvh * chunks + chunk) * pos_blocks +
+    // pb.  Every item of a kv head reads the same shared pages (each row
+    // block) and the same query rows (each key chunk), so the items of one
+    // kv head are given to workgroups that land on one XCD, whose L2 then
+    // serves the repeats: workgroup `block` runs on XCD block % kXcds.
+    const std::uint32_t n =
+        static_cast<std::uint32_t>(a.pos_blocks * a.kv_heads * a.cascade_chunks);
+    if (n % kXcds == 0) item = (block % kXcds) * (n / kXcds) + block / kXcds;
+    pb = static_cast<int>(item % a.pos_blocks);
+    chunk = static_cast<int>((item / a.pos_blocks) % a.cascade_chunks);
+    kvh = static_cast<int>(item / a.pos_blocks / a.cascade_chunks);
+    b = 0;
   } else {
-    const std::uint32_t x = item % a.pos_blocks;
-    item = item - x + (a.pos_blocks - 1 - x);
+    if (order != nullptr) {
+      item = order[block];
+    } else {
+      const std::uint32_t x = item % a.pos_blocks;
+      item = item - x + (a.pos_blocks - 1 - x);
+    }
+    pb = static_cast<int>(item % a.pos_blocks);
+    kvh = static_cast<int>((item / a.pos_blocks) % a.kv_heads);
+    b = static_cast<int>(item / a.pos_blocks / a.kv_heads);
+    chunk = 0;
   }
-  const int pb = static_cast<int>(item % a.pos_blocks);
-  const int kvh = static_cast<int>((item / a.pos_blocks) % a.kv_heads);
-  // Prefill: the sequence.  Cascade: the key chunk of the shared prefix.
-  const int b = CASCADE ? 0 : static_cast<int>(item / a.pos_blocks / a.kv_heads);
-  const int chunk = CASCADE ? static_cast<int>(item / a.pos_blocks / a.kv_heads) : 0;
   const int T = a.tokens;
   const int pos0 = pb * PW;
 
