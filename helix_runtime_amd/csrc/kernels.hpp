@@ -12,6 +12,12 @@
 
 namespace helix::hip {
 
+// XCDs of an MI355X.  The dispatcher hands consecutive workgroups of a launch
+// to the XCDs in turn (workgroup i runs on XCD i % kXcds), and each XCD has
+// its own L2: work items that read the same pages go to workgroups of one
+// XCD so that the repeats hit that L2.
+constexpr unsigned kXcds = 8;
+
 // Pool geometry of one layer: [physical_blocks, kv_heads, block_tokens, dim].
 struct PageGeometry {
   std::size_t physical_blocks;

@@ -65,9 +65,6 @@ constexpr int kCascadeTilesPerWave = 1;
 constexpr int kKeys = 16;       // keys per LDS stage (one page)
 constexpr int kKStride = D + 4; // padded K row: 8 consecutive rows hit distinct banks
 constexpr float kLog2e = 1.4426950408889634f;
-// XCDs of the device: the dispatcher hands consecutive workgroups of a
-// launch to the XCDs in turn, and each XCD has its own L2.
-constexpr unsigned kXcds = 8;
 
 struct PrefillKernelArgs {
   const float* query;
