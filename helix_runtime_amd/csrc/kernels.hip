@@ -862,6 +862,18 @@ struct PageDesc {
 // global store after the last load.  A full stage is flushed early (many
 // short units per wavefront).
 constexpr int kStreamStage = 4;
+
+// One token row's 4 dims of a page buffer as fp32: fp32 pages as loaded,
+// bf16 pages (4 per 64-bit lane load) widened where the row is used, so a
+// buffer never holds a widened copy of its page.
+__device__ __forceinline__ float4 page_row(const float4& x) { return x; }
+__device__ __forceinline__ float4 page_row(const uint2& x) { return bf16_widen(x.x, x.y); }
+__device__ __forceinline__ float4 masked_row(const float4& x, bool keep) {
+  return make_float4(keep ? x.x : 0.0f, keep ? x.y : 0.0f, keep ? x.z : 0.0f, keep ? x.w : 0.0f);
+}
+__device__ __forceinline__ uint2 masked_row(const uint2& x, bool keep) {
+  return make_uint2(keep ? x.x : 0u, keep ? x.y : 0u);
+}
 template <int G>
 struct StreamShared {
   __align__(16) float p[2][8 * G];
@@ -1144,31 +1156,6 @@ __device__ __forceinline__ void decode_stream_body(
     }
   };
 
-  // fp32 view of a loaded page: bf16 pairs widened, the bf16 tail row (fp32
-  // in slots 0, 1) rounded to bf16 and copied to every slot.
-  auto widen = [&](const Raw (&k)[8], const Raw (&v)[8], bool tail, float4 (&kf)[8],
-                   float4 (&vf)[8]) {
-    if constexpr (BF16) {
-      if (tail) {
-        const float4 tk = bf16_rounded(make_float4(__uint_as_float(k[0].x), __uint_as_float(k[0].y),
-                                                   __uint_as_float(k[1].x), __uint_as_float(k[1].y)));
-        const float4 tv = bf16_rounded(make_float4(__uint_as_float(v[0].x), __uint_as_float(v[0].y),
-                                                   __uint_as_float(v[1].x), __uint_as_float(v[1].y)));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          kf[i] = tk;
-          vf[i] = tv;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          kf[i] = bf16_widen(k[i].x, k[i].y);
-          vf[i] = bf16_widen(v[i].x, v[i].y);
-        }
-      }
-    }
-  };
-
   float acc[G][4];
   float m[R], l[R];
   bool unit_bad = false;
@@ -1184,13 +1171,14 @@ __device__ __forceinline__ void decode_stream_body(
   };
   reset();
 
-  auto process = [&](const float4 (&k)[8], float4 (&v)[8], const float4 (&q)[G], int valid) {
+  auto process = [&](const auto& k, auto& v, const float4 (&q)[G], int valid) {
     float xs[NV];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      const float4 ki = page_row(k[i]);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        xs[i * G + h] = q[h].x * k[i].x + q[h].y * k[i].y + q[h].z * k[i].z + q[h].w * k[i].w;
+        xs[i * G + h] = q[h].x * ki.x + q[h].y * ki.y + q[h].z * ki.z + q[h].w * ki.w;
       }
     }
     reduce_scores<G>(xs, j);
@@ -1224,13 +1212,7 @@ __device__ __forceinline__ void decode_stream_body(
     stream_sync<SHARED_BLOCK>();
     if (valid < P) {  // wave-uniform: only partial pages and the tail
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool keep = 2 * i + parity < valid;
-        v[i].x = keep ? v[i].x : 0.0f;
-        v[i].y = keep ? v[i].y : 0.0f;
-        v[i].z = keep ? v[i].z : 0.0f;
-        v[i].w = keep ? v[i].w : 0.0f;
-      }
+      for (int i = 0; i < 8; ++i) v[i] = masked_row(v[i], 2 * i + parity < valid);
     }
     bool rescale = false;
 #pragma unroll
@@ -1246,13 +1228,14 @@ __device__ __forceinline__ void decode_stream_body(
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      const float4 vi = page_row(v[i]);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float pv = pp[i * G + h];
-        acc[h][0] += pv * v[i].x;
-        acc[h][1] += pv * v[i].y;
-        acc[h][2] += pv * v[i].z;
-        acc[h][3] += pv * v[i].w;
+        acc[h][0] += pv * vi.x;
+        acc[h][1] += pv * vi.y;
+        acc[h][2] += pv * vi.z;
+        acc[h][3] += pv * vi.w;
       }
     }
   };
@@ -1363,8 +1346,8 @@ __device__ __forceinline__ void decode_stream_body(
   };
 
   float4 qc[G];  // query rows of the unit being processed
-  auto step_body = [&](const PageDesc& d, const float4 (&k)[8], float4 (&v)[8],
-                       const float4 (&qn)[G], bool bad) {
+  auto step_body = [&](const PageDesc& d, const auto& k, auto& v, const float4 (&qn)[G],
+                       bool bad) {
     int valid = 0;
     if (!d.skip) {
       valid = d.p == d.np - 1 ? 1 : min(P, d.hist - (d.p + a.first_page) * P);
@@ -1388,8 +1371,8 @@ __device__ __forceinline__ void decode_stream_body(
         // The tail row is this step's new token: stage its page write.
         if (napp == kStage) flush();
         if (parity == 0) {
-          s_app_k[napp][j] = k[0];
-          s_app_v[napp][j] = v[0];
+          s_app_k[napp][j] = page_row(k[0]);
+          s_app_v[napp][j] = page_row(v[0]);
         }
         if (lane == 0) {
           const std::int64_t slot = a.append_slots[d.b];
@@ -1406,16 +1389,24 @@ __device__ __forceinline__ void decode_stream_body(
   };
   auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad) {
     if constexpr (BF16) {
-      float4 k[8], v[8];
-      widen(kr, vr, !d.skip && d.p == d.np - 1, k, v);
-      step_body(d, k, v, qn, bad);
-    } else {
-      step_body(d, kr, vr, qn, bad);
+      if (!d.skip && d.p == d.np - 1) {
+        // The tail row arrived as fp32 in slots 0 and 1: round it onto the
+        // bf16 grid (the value its page will hold) and pack it into slot 0
+        // like a page row; the other slots are masked.
+        kr[0] = make_uint2(bf16_pack(__uint_as_float(kr[0].x), __uint_as_float(kr[0].y)),
+                           bf16_pack(__uint_as_float(kr[1].x), __uint_as_float(kr[1].y)));
+        vr[0] = make_uint2(bf16_pack(__uint_as_float(vr[0].x), __uint_as_float(vr[0].y)),
+                           bf16_pack(__uint_as_float(vr[1].x), __uint_as_float(vr[1].y)));
+      }
     }
+    step_body(d, kr, vr, qn, bad);
   };
 
-  // Two pages in flight, each in its own register buffer (a deeper bf16
-  // pipeline spills: the query rows ride with every buffer).
+  // Two pages in flight, each in its own register buffer.  bf16 pages hold
+  // half the bytes, yet more bf16 pages in flight measured slower (3 pages:
+  // 130 against 125 us per config-3 layer, query rows moved to LDS to fit
+  // the registers; 4 pages: LDS-limited occupancy, 191 us): at two
+  // wavefronts per SIMD the bf16 kernel is held by its per-page math.
   Raw ka[8], va[8], kb[8], vb[8];
   float4 qa[G], qb[G];
 #pragma unroll
