@@ -36,7 +36,8 @@ import helix_runtime_amd as hx  # noqa: E402
 HBM_PEAK_GBPS = 8000.0
 LAYERS, HQ, HKV, D, P, BATCH = 32, 32, 8, 128, 16, 64
 # Page element type (--page-dtype): "f32" is the reference's format and the
-# headline; "bf16" is the reduced-precision extension.
+# headline; "bf16" and "fp8" (E4M3, scales 1) are the reduced-precision
+# extension.
 PAGE_DTYPE, PAGE_BYTES = "f32", 4
 
 
@@ -315,11 +316,13 @@ def copy_probe(nbytes=1 << 30, reps=10):
                       "read_probe_gbps": round(4 * nbytes / ms_read / 1e6, 1)}), flush=True)
 
 
-def page_probe(seed, reps=10):
+def page_probe(seed, reps=10, order="head"):
     """Reads the config-3 decode's pages in the stream kernel's order (kv-head
     major, each wavefront a contiguous range of the page list, two K/V page
     pairs in flight) with loads only: the attainable rate for this access
-    pattern, with default and with non-temporal (streaming) loads."""
+    pattern, with default and with non-temporal (streaming) loads.  Pages of
+    the --page-dtype element size; order "sequence" lists the units
+    sequence-major instead (the kv heads of one sequence in turn)."""
     rng = np.random.default_rng(seed)
     lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=BATCH)).astype(np.int64)
     pages = (lengths + P - 1) // P
@@ -329,21 +332,26 @@ def page_probe(seed, reps=10):
     for n in pages:
         tables.append(perm[at: at + n])
         at += n
-    kv = [(ph * HKV + h, n_phys * HKV + ph * HKV + h)
-          for h in range(HKV) for t in tables for ph in t]
+    if order == "sequence":
+        kv = [(ph * HKV + h, n_phys * HKV + ph * HKV + h)
+              for t in tables for h in range(HKV) for ph in t]
+    else:
+        kv = [(ph * HKV + h, n_phys * HKV + ph * HKV + h)
+              for h in range(HKV) for t in tables for ph in t]
     props = torch.cuda.get_device_properties(0)
     waves = props.multi_processor_count * 8
     steps = len(kv) // waves
     pairs = np.array(kv[: waves * steps], np.uint32).reshape(-1)
-    pool = torch.zeros(2 * n_phys * HKV * P * D, device="cuda:0")
+    pool = torch.zeros(2 * n_phys * HKV * P * D * PAGE_BYTES, dtype=torch.uint8, device="cuda:0")
     dpairs = torch.from_numpy(pairs.view(np.int32)).to("cuda:0")
     sink = torch.empty(waves * 64, device="cuda:0")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    out = {"page_probe_pairs": waves * steps, "page_probe_bytes": waves * steps * 2 * P * D * 4}
+    out = {"page_probe_pairs": waves * steps, "page_dtype": PAGE_DTYPE, "order": order,
+           "page_probe_bytes": waves * steps * 2 * P * D * PAGE_BYTES}
     for nt in (0, 1):
         args = (ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(dpairs.data_ptr()),
                 ctypes.c_size_t(steps), ctypes.c_uint(waves), ctypes.c_int(nt),
-                ctypes.c_void_p(sink.data_ptr()),
+                ctypes.c_int(PAGE_BYTES), ctypes.c_void_p(sink.data_ptr()),
                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         probe_check(probe_lib().helix_probe_page_read(*args))
         e0.record()
@@ -887,12 +895,14 @@ def main():
                          "4: prefix-sharing decode; 5: chunked prefill on the matrix cores")
     ap.add_argument("--cpu-seqs", type=int, default=4,
                     help="config 5: sequences of layer 0 timed on the CPU oracle")
-    ap.add_argument("--page-dtype", default="f32", choices=("f32", "bf16"),
-                    help="page element type (bf16: the reduced-precision extension; the CPU "
+    ap.add_argument("--page-dtype", default="f32", choices=("f32", "bf16", "fp8"),
+                    help="page element type (bf16, fp8: the reduced-precision extension; the CPU "
                          "baseline is reported for f32 pages only)")
     ap.add_argument("--page-probe", action="store_true",
                     help="only read the config-3 pages in the decode order with loads only "
                          "(the attainable rate for the access pattern)")
+    ap.add_argument("--probe-order", default="head", choices=("head", "sequence"),
+                    help="--page-probe: unit order of the page list")
     ap.add_argument("--model-step", action="store_true",
                     help="a whole Llama-3-8B-shaped decode step (torch dense ops, library KV "
                          "path): the integrated flow against the reference's per-layer order")
@@ -910,7 +920,7 @@ def main():
         sys.exit(2)
 
     global PAGE_DTYPE, PAGE_BYTES, HQ, HKV, BATCH
-    PAGE_DTYPE, PAGE_BYTES = args.page_dtype, (2 if args.page_dtype == "bf16" else 4)
+    PAGE_DTYPE, PAGE_BYTES = args.page_dtype, {"bf16": 2, "fp8": 1}.get(args.page_dtype, 4)
     if args.layers is None:
         args.layers = 1 if args.config == 2 else LAYERS
     if args.config == 2:
@@ -920,7 +930,7 @@ def main():
         copy_probe()
         return
     if args.page_probe:
-        page_probe(args.seed)
+        page_probe(args.seed, order=args.probe_order)
         return
     if args.model_step:
         run_model_step(args)

@@ -144,7 +144,7 @@ class BlockManager:
         return a.value, b.value, c.value
 
 
-PAGE_DTYPES = {"f32": 0, "bf16": 1}
+PAGE_DTYPES = {"f32": 0, "bf16": 1, "fp8": 2}
 
 # ---------------------------------------------------------- prefix cache ----
 PREFIX_INSERTED, PREFIX_ALREADY_PRESENT, PREFIX_REJECTED_TOO_LARGE = 0, 1, 2
@@ -245,17 +245,27 @@ class PagedKvCache:
     """GPU paged KV pool (CudaPagedKvCache + the CPU cache's fork/bulk append)."""
 
     def __init__(self, layers, kv_heads, head_dimension, block_tokens, physical_blocks,
-                 device=0, page_dtype="f32"):
+                 device=0, page_dtype="f32", k_scale=1.0, v_scale=1.0):
         """``page_dtype`` "bf16" stores pages as bf16 (extension: appended
-        fp32 rows rounded to nearest even, gathers widen back to fp32)."""
+        fp32 rows rounded to nearest even, gathers widen back to fp32);
+        "fp8" stores OCP E4M3 codes of x / k_scale (keys) and x / v_scale
+        (values), rounded to nearest even and saturating at +-448; gathers
+        return decode(code) * scale."""
         h = ctypes.c_void_p()
         cfg = _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
         if page_dtype not in PAGE_DTYPES:
             raise HelixError(INVALID_ARGUMENT, f"page_dtype must be one of {sorted(PAGE_DTYPES)}")
-        check(_lib().helix_paged_cache_create_typed(ctypes.byref(cfg), device,
-                                                    PAGE_DTYPES[page_dtype], ctypes.byref(h)))
+        if page_dtype == "fp8":
+            check(_lib().helix_paged_cache_create_fp8(ctypes.byref(cfg), device, float(k_scale),
+                                                      float(v_scale), ctypes.byref(h)))
+        else:
+            check(_lib().helix_paged_cache_create_typed(ctypes.byref(cfg), device,
+                                                        PAGE_DTYPES[page_dtype], ctypes.byref(h)))
         self._h = h
         self.page_dtype = page_dtype
+        ks, vs = ctypes.c_float(), ctypes.c_float()
+        check(_lib().helix_paged_cache_fp8_scales(h, ctypes.byref(ks), ctypes.byref(vs)))
+        self.k_scale, self.v_scale = ks.value, vs.value
         self.layers, self.kv_heads, self.head_dimension = layers, kv_heads, head_dimension
         self.block_tokens, self.physical_blocks, self.device = block_tokens, physical_blocks, device
 
@@ -369,11 +379,11 @@ class PagedKvCache:
 
     def layer_pools(self, layer):
         """Device copies of layer `layer`'s pools [physical, kv_heads, block_tokens, dim]
-        (float32, or bfloat16 for a bf16 cache)."""
+        (float32, bfloat16 for a bf16 cache, uint8 E4M3 codes for an fp8 cache)."""
         import torch
         kp, vp = self.layer_pool_pointers(layer)
         shape = (self.physical_blocks, self.kv_heads, self.block_tokens, self.head_dimension)
-        dtype = torch.bfloat16 if self.page_dtype == "bf16" else torch.float32
+        dtype = {"bf16": torch.bfloat16, "fp8": torch.uint8}.get(self.page_dtype, torch.float32)
         out = []
         for p in (kp, vp):
             t = torch.empty(shape, dtype=dtype, device=f"cuda:{self.device}")

@@ -17,6 +17,7 @@ c_size = ctypes.c_size_t
 c_int = ctypes.c_int
 c_u32 = ctypes.c_uint32
 c_u64 = ctypes.c_uint64
+c_float = ctypes.c_float
 vp = ctypes.c_void_p
 
 
@@ -169,7 +170,9 @@ SIGNATURES = {
     "helix_decode_batch_shared_pages": (c_int, [vp, P(c_size)]),
     "helix_decode_batch_destroy": (None, [vp]),
     "helix_paged_cache_create_typed": (c_int, [P(Config), c_int, c_int, P(vp)]),
+    "helix_paged_cache_create_fp8": (c_int, [P(Config), c_int, c_float, c_float, P(vp)]),
     "helix_paged_cache_page_dtype": (c_int, [vp, P(c_int)]),
+    "helix_paged_cache_fp8_scales": (c_int, [vp, P(c_float), P(c_float)]),
     # prefix cache
     "helix_prefix_cache_create": (c_int, [vp, P(PrefixConfig), P(vp)]),
     "helix_prefix_cache_create_host": (c_int, [vp, P(PrefixConfig), P(vp)]),

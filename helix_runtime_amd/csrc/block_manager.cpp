@@ -32,8 +32,8 @@ std::size_t blocks_for(std::size_t tokens, std::size_t block_tokens) {
 // (src/kv_cache/paged.cpp:53-106).
 BlockManager::BlockManager(const PagedConfig& config, std::size_t element_bytes)
     : config_(config) {
-  check(element_bytes == 4 || element_bytes == 2, Status::kInvalidArgument,
-        "paged KV cache page elements are 4 (fp32) or 2 (bf16) bytes");
+  check(element_bytes == 4 || element_bytes == 2 || element_bytes == 1, Status::kInvalidArgument,
+        "paged KV cache page elements are 4 (fp32), 2 (bf16) or 1 (fp8) bytes");
   check(config.layers != 0, Status::kInvalidArgument, "paged KV cache layer count must be positive");
   check(config.kv_heads != 0, Status::kInvalidArgument, "paged KV cache head count must be positive");
   check(config.head_dimension != 0, Status::kInvalidArgument,

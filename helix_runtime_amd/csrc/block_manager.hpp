@@ -83,7 +83,7 @@ struct ForkPlan {
 
 class BlockManager {
 public:
-  // element_bytes: 4 for fp32 pages (the reference's), 2 for bf16 pages;
+  // element_bytes: 4 for fp32 pages (the reference's), 2 for bf16, 1 for fp8;
   // it scales the byte figures of the geometry and statistics only.
   explicit BlockManager(const PagedConfig& config, std::size_t element_bytes = 4);
 

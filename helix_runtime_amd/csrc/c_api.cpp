@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstring>
 #include <limits>
 #include <memory>
@@ -30,7 +31,7 @@ struct helix_block_manager {
 
 struct helix_paged_cache {
   helix_paged_cache(const helix::PagedConfig& c, int device,
-                    helix::hip::PageType type = helix::hip::PageType::kF32)
+                    helix::hip::PageFormat type = helix::hip::PageFormat())
       : cache(c, device, type) {}
   helix::DevicePagedCache cache;
 };
@@ -382,11 +383,26 @@ int helix_paged_cache_create_typed(const helix_paged_config* config, int device,
   return guarded([&] {
     require_out(out);
     *out = nullptr;
-    check(page_dtype == HELIX_PAGE_F32 || page_dtype == HELIX_PAGE_BF16,
-          Status::kInvalidArgument, "page dtype must be HELIX_PAGE_F32 or HELIX_PAGE_BF16");
+    check(page_dtype == HELIX_PAGE_F32 || page_dtype == HELIX_PAGE_BF16 ||
+              page_dtype == HELIX_PAGE_FP8_E4M3,
+          Status::kInvalidArgument,
+          "page dtype must be HELIX_PAGE_F32, HELIX_PAGE_BF16 or HELIX_PAGE_FP8_E4M3");
     *out = new helix_paged_cache(to_config(config), device,
-                                 page_dtype == HELIX_PAGE_BF16 ? helix::hip::PageType::kBF16
-                                                               : helix::hip::PageType::kF32);
+                                 static_cast<helix::hip::PageType>(page_dtype));
+  });
+}
+
+int helix_paged_cache_create_fp8(const helix_paged_config* config, int device, float key_scale,
+                                 float value_scale, helix_paged_cache** out) {
+  return guarded([&] {
+    require_out(out);
+    *out = nullptr;
+    check(std::isfinite(key_scale) && key_scale > 0.0f && std::isfinite(value_scale) &&
+              value_scale > 0.0f,
+          Status::kInvalidArgument, "fp8 page scales must be finite and positive");
+    *out = new helix_paged_cache(
+        to_config(config), device,
+        helix::hip::PageFormat(helix::hip::PageType::kFP8, key_scale, value_scale));
   });
 }
 
@@ -398,7 +414,17 @@ int helix_paged_cache_page_dtype(helix_paged_cache* cache, int* out) {
   return guarded([&] {
     REQUIRE_CACHE();
     require_out(out);
-    *out = cache->cache.state()->bf16() ? HELIX_PAGE_BF16 : HELIX_PAGE_F32;
+    *out = static_cast<int>(cache->cache.state()->page_type.type);
+  });
+}
+
+int helix_paged_cache_fp8_scales(helix_paged_cache* cache, float* key_scale, float* value_scale) {
+  return guarded([&] {
+    REQUIRE_CACHE();
+    require_out(key_scale);
+    require_out(value_scale);
+    *key_scale = cache->cache.state()->page_type.k_scale;
+    *value_scale = cache->cache.state()->page_type.v_scale;
   });
 }
 

@@ -9,6 +9,7 @@
 #include "kernels.hpp"
 
 #include "bf16.hpp"
+#include "fp8.hpp"
 #include "prefill_body.hpp"
 
 #include <hip/hip_runtime.h>
@@ -31,26 +32,27 @@ inline unsigned grid_for(std::size_t work, std::size_t per_block, std::size_t ca
 }
 
 // --------------------------------------------------------- page elements ----
-// Pages hold fp32 (the reference's format) or bf16 (bf16.hpp).  Rows passed
-// in and gather outputs are fp32 either way.
+// Pages hold fp32 (the reference's format), bf16 (bf16.hpp) or fp8 E4M3
+// codes (fp8.hpp).  Rows passed in and gather outputs are fp32 whatever the
+// type; `scale` is the fp8 scale of the pool (ignored by the other types).
 // W consecutive elements between fp32 rows and pages of element type S.
 template <typename S, int W>
 struct Elems;
 template <int W>
 struct Elems<float, W> {
-  static __device__ __forceinline__ void put(float* dst, const float* src) {
+  static __device__ __forceinline__ void copy(float* dst, const float* src) {
     if constexpr (W == 4) {
       *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
     } else {
       *dst = *src;
     }
   }
-  static __device__ __forceinline__ void get(float* dst, const float* src) { put(dst, src); }
-  static __device__ __forceinline__ void copy(float* dst, const float* src) { put(dst, src); }
+  static __device__ __forceinline__ void put(float* dst, const float* src, float) { copy(dst, src); }
+  static __device__ __forceinline__ void get(float* dst, const float* src, float) { copy(dst, src); }
 };
 template <int W>
 struct Elems<unsigned short, W> {
-  static __device__ __forceinline__ void put(unsigned short* dst, const float* src) {
+  static __device__ __forceinline__ void put(unsigned short* dst, const float* src, float) {
     if constexpr (W == 4) {
       const float4 v = *reinterpret_cast<const float4*>(src);
       *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pack(v.x, v.y), bf16_pack(v.z, v.w));
@@ -58,7 +60,7 @@ struct Elems<unsigned short, W> {
       *dst = bf16_round(*src);
     }
   }
-  static __device__ __forceinline__ void get(float* dst, const unsigned short* src) {
+  static __device__ __forceinline__ void get(float* dst, const unsigned short* src, float) {
     if constexpr (W == 4) {
       const uint2 p = *reinterpret_cast<const uint2*>(src);
       *reinterpret_cast<float4*>(dst) = bf16_widen(p.x, p.y);
@@ -75,6 +77,32 @@ struct Elems<unsigned short, W> {
   }
 };
 
+template <int W>
+struct Elems<unsigned char, W> {
+  static __device__ __forceinline__ void put(unsigned char* dst, const float* src, float scale) {
+    if constexpr (W == 4) {
+      *reinterpret_cast<unsigned*>(dst) =
+          fp8_pack4_scaled(*reinterpret_cast<const float4*>(src), scale);
+    } else {
+      *dst = static_cast<unsigned char>(fp8_code(*src / scale));
+    }
+  }
+  static __device__ __forceinline__ void get(float* dst, const unsigned char* src, float scale) {
+    if constexpr (W == 4) {
+      *reinterpret_cast<float4*>(dst) = fp8_widen4(*reinterpret_cast<const unsigned*>(src), scale);
+    } else {
+      *dst = fp8_value(*src, scale);
+    }
+  }
+  static __device__ __forceinline__ void copy(unsigned char* dst, const unsigned char* src) {
+    if constexpr (W == 4) {
+      *reinterpret_cast<unsigned*>(dst) = *reinterpret_cast<const unsigned*>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+};
+
 // ------------------------------------------------------------- append ----
 // Reference: CudaPagedKvCache::append issues 2 * layers * kv_heads
 // cudaMemcpyAsync D2D copies of one head vector (src/kv_cache/cuda_paged.cpp:
@@ -85,11 +113,12 @@ __global__ void append_token_kernel(const float* __restrict__ keys,
                                     const float* __restrict__ values, S* key_base, S* value_base,
                                     std::size_t layer_stride, std::size_t layers,
                                     std::size_t heads, std::size_t block_tokens, std::size_t dim,
-                                    std::uint32_t block, std::size_t offset) {
+                                    std::uint32_t block, std::size_t offset, float2 scale) {
   const std::size_t dv = dim / W;
   const std::size_t total = layers * heads * dv;
   const float* src = blockIdx.y == 0 ? keys : values;
   S* base = blockIdx.y == 0 ? key_base : value_base;
+  const float sc = blockIdx.y == 0 ? scale.x : scale.y;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t c = e % dv;
@@ -98,7 +127,7 @@ __global__ void append_token_kernel(const float* __restrict__ keys,
     const std::size_t l = lh / heads;
     S* dst = base + l * layer_stride +
              ((static_cast<std::size_t>(block) * heads + h) * block_tokens + offset) * dim + c * W;
-    Elems<S, W>::put(dst, src + e * W);
+    Elems<S, W>::put(dst, src + e * W, sc);
   }
 }
 
@@ -115,12 +144,13 @@ __global__ void append_bulk_kernel(LayerPointers src, S* key_base, S* value_base
                                    std::size_t heads, std::size_t block_tokens, std::size_t dim,
                                    const std::uint32_t* __restrict__ blocks,
                                    std::size_t first_block, std::size_t old_length,
-                                   std::size_t tokens) {
+                                   std::size_t tokens, float2 scale) {
   const std::size_t dv = dim / W;
   const std::size_t per_layer = heads * tokens * dv;
   const std::size_t total = layers * per_layer;
   S* base = blockIdx.y == 0 ? key_base : value_base;
   const float* const* layer_src = blockIdx.y == 0 ? src.keys : src.values;
+  const float sc = blockIdx.y == 0 ? scale.x : scale.y;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t l = e / per_layer;
@@ -133,7 +163,7 @@ __global__ void append_bulk_kernel(LayerPointers src, S* key_base, S* value_base
     const std::size_t phys = blocks[pos / block_tokens - first_block];
     S* dst = base + l * layer_stride +
              ((phys * heads + h) * block_tokens + pos % block_tokens) * dim + c * W;
-    Elems<S, W>::put(dst, layer_src[l] + r * W);
+    Elems<S, W>::put(dst, layer_src[l] + r * W, sc);
   }
 }
 
@@ -151,7 +181,7 @@ template <typename S, int W>
 __global__ __launch_bounds__(256) void append_slots_kernel(
     const float* __restrict__ keys, const float* __restrict__ values, S* key_pool, S* value_pool,
     std::size_t layer_stride, unsigned heads, unsigned block_tokens, unsigned dim,
-    const std::int64_t* __restrict__ slots, unsigned count, unsigned tokens) {
+    const std::int64_t* __restrict__ slots, unsigned count, unsigned tokens, float2 scale) {
   // Grid: x covers one row group's heads * dim / W vectors, y walks the
   // (sequence, token) rows, z = 2 * layer + (0: K, 1: V).  Everything but
   // the lane's (head, vector) pair is uniform across the workgroup.
@@ -163,6 +193,7 @@ __global__ __launch_bounds__(256) void append_slots_kernel(
   const bool is_value = (blockIdx.z & 1u) != 0;
   const std::size_t l = blockIdx.z >> 1;
   const float* src = is_value ? values : keys;
+  const float sc = is_value ? scale.y : scale.x;
   S* pool = (is_value ? value_pool : key_pool) + l * layer_stride;
   const unsigned rows = count * tokens;
   for (unsigned bt = blockIdx.y; bt < rows; bt += gridDim.y) {
@@ -173,7 +204,8 @@ __global__ __launch_bounds__(256) void append_slots_kernel(
     const std::size_t block = static_cast<std::size_t>(slot) / block_tokens;
     const std::size_t off = static_cast<std::size_t>(slot) % block_tokens;
     const std::size_t e = (((l * count + b) * heads + h) * tokens + t) * dv + c;
-    Elems<S, W>::put(pool + ((block * heads + h) * block_tokens + off) * dim + c * W, src + e * W);
+    Elems<S, W>::put(pool + ((block * heads + h) * block_tokens + off) * dim + c * W, src + e * W,
+                     sc);
   }
 }
 
@@ -232,11 +264,13 @@ template <typename S, int W>
 __global__ void gather_kernel(const S* __restrict__ key_pool, const S* __restrict__ value_pool,
                               std::size_t heads, std::size_t block_tokens, std::size_t dim,
                               const std::uint32_t* __restrict__ blocks, std::size_t length,
-                              float* keys_out, float* values_out, std::size_t dest_tokens) {
+                              float* keys_out, float* values_out, std::size_t dest_tokens,
+                              float2 scale) {
   const std::size_t dv = dim / W;
   const std::size_t total = heads * length * dv;
   const S* pool = blockIdx.y == 0 ? key_pool : value_pool;
   float* out = blockIdx.y == 0 ? keys_out : values_out;
+  const float sc = blockIdx.y == 0 ? scale.x : scale.y;
   for (std::size_t e = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
     const std::size_t c = e % dv;
@@ -245,7 +279,8 @@ __global__ void gather_kernel(const S* __restrict__ key_pool, const S* __restric
     const std::size_t h = ht / length;
     const std::size_t phys = blocks[t / block_tokens];
     Elems<S, W>::get(out + (h * dest_tokens + t) * dim + c * W,
-                     pool + ((phys * heads + h) * block_tokens + t % block_tokens) * dim + c * W);
+                     pool + ((phys * heads + h) * block_tokens + t % block_tokens) * dim + c * W,
+                     sc);
   }
 }
 
@@ -422,6 +457,10 @@ struct DecodeKernelArgs {
   float* append_key_pool;
   float* append_value_pool;
   int single_length;  // history of the one sequence when lengths is not used
+  // fp8 pages: scales of the key and value codes (the key scale is also
+  // folded into qscale).
+  float k_scale;
+  float v_scale;
 };
 
 __device__ __forceinline__ int clamp_length(int hist, int max_blocks) {
@@ -852,9 +891,13 @@ struct PageDesc {
   bool skip;
 };
 
-// BF16: pages hold bf16 (4 per 64-bit lane load) and are widened to fp32 in
-// registers.  The fp32 tail row is rounded to bf16 as it is read (it is the
-// value the page will hold once appended).
+// PF (page format, the PageType value): fp32 pages (0); bf16 pages (1, 4
+// per 64-bit lane load); fp8 E4M3 pages (2, 4 per 32-bit lane load).
+// Reduced-precision pages stay packed in registers and each row is widened
+// where it is used.  The fp32 tail row is rounded onto the page grid as it
+// is read (it is the value the page will hold once appended).  fp8 scales:
+// the key scale is folded into the score scale on the host and the value
+// scale is applied to each result, so rows widen to bare code values.
 // LDS of one stream wavefront.  Results are staged until the wavefront's
 // last page: on this architecture a store counts in the same in-order
 // counter as the loads, so a store issued between prefetches would make the
@@ -868,8 +911,17 @@ constexpr int kStreamStage = 4;
 // buffer never holds a widened copy of its page.
 __device__ __forceinline__ float4 page_row(const float4& x) { return x; }
 __device__ __forceinline__ float4 page_row(const uint2& x) { return bf16_widen(x.x, x.y); }
+__device__ __forceinline__ float4 page_row(const unsigned& x) { return fp8_widen4(x, 1.0f); }
 __device__ __forceinline__ float4 masked_row(const float4& x, bool keep) {
   return make_float4(keep ? x.x : 0.0f, keep ? x.y : 0.0f, keep ? x.z : 0.0f, keep ? x.w : 0.0f);
+}
+__device__ __forceinline__ unsigned masked_row(const unsigned& x, bool keep) { return keep ? x : 0u; }
+// A tail row as staged for its page write: fp32 and bf16 rows as values
+// (bf16-exact, repacked without rounding), fp8 rows as their codes in .x.
+__device__ __forceinline__ float4 staged_row(const float4& x) { return x; }
+__device__ __forceinline__ float4 staged_row(const uint2& x) { return page_row(x); }
+__device__ __forceinline__ float4 staged_row(const unsigned& x) {
+  return make_float4(__uint_as_float(x), 0.0f, 0.0f, 0.0f);
 }
 __device__ __forceinline__ uint2 masked_row(const uint2& x, bool keep) {
   return make_uint2(keep ? x.x : 0u, keep ? x.y : 0u);
@@ -928,7 +980,7 @@ __device__ __forceinline__ void stream_sync() {
 
 // The body of one stream wavefront: `wave` is its index among
 // a.stream_waves, `lane` its lane, `sh` its LDS.
-template <int G, bool APPEND, bool BF16, bool SHARED_BLOCK, bool SINGLE = false>
+template <int G, bool APPEND, int PF, bool SHARED_BLOCK, bool SINGLE = false>
 __device__ __forceinline__ void decode_stream_body(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
@@ -1083,9 +1135,11 @@ __device__ __forceinline__ void decode_stream_body(
   // arithmetic is needed.  The first page of a unit in this wavefront also
   // brings the unit's query rows, issued ahead of the page so that waiting
   // for the page covers them.
-  const int lane_off = lane * (BF16 ? 8 : 16);
+  constexpr bool BF16 = PF == 1;
+  constexpr bool FP8 = PF == 2;
+  const int lane_off = lane * (FP8 ? 4 : BF16 ? 8 : 16);
   const int row_off = j * 16;
-  using Raw = std::conditional_t<BF16, uint2, float4>;
+  using Raw = std::conditional_t<FP8, unsigned, std::conditional_t<BF16, uint2, float4>>;
   auto load_page = [&](const PageDesc& d, Raw (&k)[8], Raw (&v)[8], float4 (&q)[G], bool& bad) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
     const int kvh = __builtin_amdgcn_readfirstlane(d.kvh);
@@ -1106,7 +1160,10 @@ __device__ __forceinline__ void decode_stream_body(
         phys = 0;
       }
       const std::size_t off = (static_cast<std::size_t>(phys) * a.kv_heads + kvh) * page_elems;
-      if constexpr (BF16) {
+      if constexpr (FP8) {
+        kb = reinterpret_cast<const unsigned char*>(a.key_pool) + off;
+        vb = reinterpret_cast<const unsigned char*>(a.value_pool) + off;
+      } else if constexpr (BF16) {
         kb = reinterpret_cast<const unsigned short*>(a.key_pool) + off;
         vb = reinterpret_cast<const unsigned short*>(a.value_pool) + off;
       } else {
@@ -1125,12 +1182,29 @@ __device__ __forceinline__ void decode_stream_body(
     // range: its loads return zeros without touching memory, and the step
     // that consumes them does nothing.  The instruction stream is the same
     // either way, so the prefetch waits stay static.
-    const int bytes = d.skip ? 0 : (BF16 ? (tail ? D * 4 : P * D * 2) : P * D * 4);
+    const int bytes =
+        d.skip ? 0 : (tail ? D * 4 : P * D * static_cast<int>(sizeof(float) >> (FP8 ? 2 : BF16 ? 1 : 0)));
     const __amdgpu_buffer_rsrc_t kr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kb), 0, bytes, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vb), 0, bytes, kBufferWord3);
-    if constexpr (BF16) {
+    if constexpr (FP8) {
+      if (tail) {
+        // The fp32 row's 4 dims of this lane: four 32-bit words in slots 0-3.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          k[i] = __builtin_amdgcn_raw_buffer_load_b32(kr, row_off, i * 4, 0);
+          v[i] = __builtin_amdgcn_raw_buffer_load_b32(vr, row_off, i * 4, 0);
+        }
+#pragma unroll
+        for (int i = 4; i < 8; ++i) k[i] = v[i] = 0u;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = __builtin_amdgcn_raw_buffer_load_b32(kr, lane_off, i * 256, kStreamLoad);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b32(vr, lane_off, i * 256, kStreamLoad);
+      }
+    } else if constexpr (BF16) {
       if (tail) {
         // The fp32 row's 4 dims of this lane: two 64-bit halves in slots 0, 1.
 #pragma unroll
@@ -1247,7 +1321,13 @@ __device__ __forceinline__ void decode_stream_body(
     for (int r = 0; r < (APPEND ? napp : 0); ++r) {
       const long long dst = s_app_dst[r];
       if (parity == 0 && dst >= 0) {
-        if constexpr (BF16) {
+        if constexpr (FP8) {
+          // Staged rows hold the codes in .x.
+          reinterpret_cast<unsigned*>(reinterpret_cast<unsigned char*>(a.append_key_pool) + dst)[j] =
+              __float_as_uint(s_app_k[r][j].x);
+          reinterpret_cast<unsigned*>(reinterpret_cast<unsigned char*>(a.append_value_pool) + dst)[j] =
+              __float_as_uint(s_app_v[r][j].x);
+        } else if constexpr (BF16) {
           // Staged values are already bf16-exact: packing does not round.
           const float4 kk = s_app_k[r][j];
           const float4 vv = s_app_v[r][j];
@@ -1317,6 +1397,7 @@ __device__ __forceinline__ void decode_stream_body(
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float4 o = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        if constexpr (FP8) o = make_float4(o.x * a.v_scale, o.y * a.v_scale, o.z * a.v_scale, o.w * a.v_scale);
         if (complete) {
           const float mh = s_head[1][h];
           const float lh = s_head[2][h];
@@ -1371,8 +1452,8 @@ __device__ __forceinline__ void decode_stream_body(
         // The tail row is this step's new token: stage its page write.
         if (napp == kStage) flush();
         if (parity == 0) {
-          s_app_k[napp][j] = page_row(k[0]);
-          s_app_v[napp][j] = page_row(v[0]);
+          s_app_k[napp][j] = staged_row(k[0]);
+          s_app_v[napp][j] = staged_row(v[0]);
         }
         if (lane == 0) {
           const std::int64_t slot = a.append_slots[d.b];
@@ -1388,6 +1469,16 @@ __device__ __forceinline__ void decode_stream_body(
     if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
   };
   auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad) {
+    if constexpr (FP8) {
+      if (!d.skip && d.p == d.np - 1) {
+        // The tail row arrived as fp32 in slots 0-3: its codes (the values
+        // its page will hold) go to slot 0 like a page row.
+        kr[0] = fp8_pack4(__uint_as_float(kr[0]) / a.k_scale, __uint_as_float(kr[1]) / a.k_scale,
+                          __uint_as_float(kr[2]) / a.k_scale, __uint_as_float(kr[3]) / a.k_scale);
+        vr[0] = fp8_pack4(__uint_as_float(vr[0]) / a.v_scale, __uint_as_float(vr[1]) / a.v_scale,
+                          __uint_as_float(vr[2]) / a.v_scale, __uint_as_float(vr[3]) / a.v_scale);
+      }
+    }
     if constexpr (BF16) {
       if (!d.skip && d.p == d.np - 1) {
         // The tail row arrived as fp32 in slots 0 and 1: round it onto the
@@ -1427,7 +1518,7 @@ __device__ __forceinline__ void decode_stream_body(
   flush();
 }
 
-template <int G, bool APPEND, bool BF16, bool SINGLE = false>
+template <int G, bool APPEND, int PF, bool SINGLE = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
 void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
@@ -1444,7 +1535,7 @@ void decode_stream_kernel(
   __shared__ __align__(16) float4 s_app_k[kStreamStage][32];
   __shared__ __align__(16) float4 s_app_v[kStreamStage][32];
   __shared__ long long s_app_dst[kStreamStage];
-  decode_stream_body<G, APPEND, BF16, false, SINGLE>(
+  decode_stream_body<G, APPEND, PF, false, SINGLE>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
       StreamLds<G>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k, s_app_v,
                    s_app_dst});
@@ -1463,7 +1554,7 @@ union CascadeShared {
   prefill_detail::CascadePrefixShared prefill;
 };
 
-template <int G, bool APPEND, bool BF16>
+template <int G, bool APPEND, int PF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void cascade_decode_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
@@ -1474,7 +1565,7 @@ void cascade_decode_kernel(
   __shared__ __align__(16) unsigned char lds[sizeof(CascadeShared<G>)];
   auto& sh = *reinterpret_cast<CascadeShared<G>*>(lds);
   if (blockIdx.x < prefix_blocks) {
-    prefill_detail::prefill_body<G, true, BF16, 2>(prefix, tables, nullptr, blockIdx.x,
+    prefill_detail::prefill_body<G, true, PF, 2>(prefix, tables, nullptr, blockIdx.x,
                                                    sh.prefill);
     return;
   }
@@ -1482,7 +1573,7 @@ void cascade_decode_kernel(
   // The stream wavefronts issue ahead of the prefix wavefronts that share
   // their SIMDs (the prefix work is short and not on the critical path).
   __builtin_amdgcn_s_setprio(3);
-  decode_stream_body<G, APPEND, BF16, true>(
+  decode_stream_body<G, APPEND, PF, true>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots,
       static_cast<int>(blockIdx.x - prefix_blocks) * 4 + w, static_cast<int>(threadIdx.x & 63),
       stream_lds(sh.stream[w]));
@@ -1733,16 +1824,25 @@ __global__ __launch_bounds__(kThreads) void generic_attention_kernel(GenericArgs
 namespace {
 
 using Bf16 = unsigned short;
+using Fp8 = unsigned char;
+
+float2 scales(const PageFormat& f) { return make_float2(f.k_scale, f.v_scale); }
 
 // Runs body(S*, W) with the page element type of `type` and the widest
 // element group the geometry and the fp32 pointers allow.
 template <typename F>
-hipError_t with_page_type(PageType type, bool vec, F&& body) {
-  if (type == PageType::kBF16) {
+hipError_t with_page_type(const PageFormat& fmt, bool vec, F&& body) {
+  if (fmt.type == PageType::kBF16) {
     if (vec) {
       body(Bf16{}, std::integral_constant<int, 4>{});
     } else {
       body(Bf16{}, std::integral_constant<int, 1>{});
+    }
+  } else if (fmt.type == PageType::kFP8) {
+    if (vec) {
+      body(Fp8{}, std::integral_constant<int, 4>{});
+    } else {
+      body(Fp8{}, std::integral_constant<int, 1>{});
     }
   } else if (vec) {
     body(float{}, std::integral_constant<int, 4>{});
@@ -1766,7 +1866,7 @@ const S* as_pages(const void* p) {
 hipError_t launch_append_token(const float* keys, const float* values, void* key_base,
                                void* value_base, std::size_t layer_stride, std::size_t layers,
                                const PageGeometry& g, std::uint32_t block, std::size_t offset,
-                               hipStream_t stream, PageType type) {
+                               hipStream_t stream, PageFormat type) {
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
   const std::size_t work = layers * g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
   const dim3 grid(grid_for(work, kThreads), 2);
@@ -1774,7 +1874,7 @@ hipError_t launch_append_token(const float* keys, const float* values, void* key
     using S = decltype(s);
     append_token_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
         keys, values, as_pages<S>(key_base), as_pages<S>(value_base), layer_stride, layers,
-        g.kv_heads, g.block_tokens, g.head_dim, block, offset);
+        g.kv_heads, g.block_tokens, g.head_dim, block, offset, scales(type));
   });
 }
 
@@ -1783,7 +1883,7 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
                               std::size_t layers, const PageGeometry& g,
                               const std::uint32_t* blocks, std::size_t first_block,
                               std::size_t old_length, std::size_t tokens, hipStream_t stream,
-                              bool vec, PageType type) {
+                              bool vec, PageFormat type) {
   const std::size_t work = layers * g.kv_heads * tokens * (vec ? g.head_dim / 4 : g.head_dim);
   const dim3 grid(grid_for(work, kThreads), 2);
   const LayerPointers src{layer_keys, layer_values};
@@ -1791,14 +1891,14 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
     using S = decltype(s);
     append_bulk_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
         src, as_pages<S>(key_base), as_pages<S>(value_base), layer_stride, layers, g.kv_heads,
-        g.block_tokens, g.head_dim, blocks, first_block, old_length, tokens);
+        g.block_tokens, g.head_dim, blocks, first_block, old_length, tokens, scales(type));
   });
 }
 
 hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
                                void* value_pool, const PageGeometry& g, const std::int64_t* slots,
                                std::size_t count, hipStream_t stream, std::size_t tokens,
-                               PageType type, std::size_t layers, std::size_t layer_stride) {
+                               PageFormat type, std::size_t layers, std::size_t layer_stride) {
   if (count == 0 || tokens == 0 || layers == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys) && aligned16(values);
   const std::size_t per_row = g.kv_heads * (vec ? g.head_dim / 4 : g.head_dim);
@@ -1816,7 +1916,7 @@ hipError_t launch_append_slots(const float* keys, const float* values, void* key
         keys, values, as_pages<S>(key_pool), as_pages<S>(value_pool), layer_stride,
         static_cast<unsigned>(g.kv_heads), static_cast<unsigned>(g.block_tokens),
         static_cast<unsigned>(g.head_dim), slots, static_cast<unsigned>(count),
-        static_cast<unsigned>(tokens));
+        static_cast<unsigned>(tokens), scales(type));
   });
 }
 
@@ -1837,7 +1937,7 @@ hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t row
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
                          float* values_out, std::size_t dest_tokens, hipStream_t stream,
-                         PageType type) {
+                         PageFormat type) {
   if (length == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys_out) && aligned16(values_out);
   const std::size_t work = g.kv_heads * length * (vec ? g.head_dim / 4 : g.head_dim);
@@ -1846,14 +1946,14 @@ hipError_t launch_gather(const void* key_pool, const void* value_pool, const Pag
     using S = decltype(s);
     gather_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
         as_pages<S>(key_pool), as_pages<S>(value_pool), g.kv_heads, g.block_tokens, g.head_dim,
-        blocks, length, keys_out, values_out, dest_tokens);
+        blocks, length, keys_out, values_out, dest_tokens, scales(type));
   });
 }
 
 hipError_t launch_page_copy(void* key_base, void* value_base, std::size_t layer_stride,
                             std::size_t layers, const PageGeometry& g, std::uint32_t from,
                             std::uint32_t to, std::size_t tokens, hipStream_t stream,
-                            PageType type) {
+                            PageFormat type) {
   if (tokens == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0;
   const std::size_t work = layers * g.kv_heads * tokens * (vec ? g.head_dim / 4 : g.head_dim);
@@ -1959,7 +2059,9 @@ namespace {
 // (two per SIMD up to four query heads per kv head, one for eight, as the
 // kernels' register use allows), at most kMaxStreamWaves.  beside_prefix:
 // one per SIMD whatever the group, so the concurrent cascade prefix pass
-// finds registers on every SIMD.
+// finds registers on every SIMD.  fp8 pages at three per SIMD (the register
+// cap of 168 spills at four query heads) measured slower: 181 against
+// 140 us per config-3 layer.
 std::size_t stream_waves(std::size_t group, bool beside_prefix) {
   static int cus[64] = {0};
   int dev = 0;
@@ -1972,7 +2074,8 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix) {
     }
     cus[dev] = n;
   }
-  const std::size_t per_simd = group >= 8 || beside_prefix ? 1 : 2;
+  const std::size_t per_simd =
+      group >= 8 || beside_prefix ? 1 : 2;
   const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
   return w < kMaxStreamWaves ? w : kMaxStreamWaves;
 }
@@ -1981,53 +2084,56 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix) {
 
 namespace {
 
-template <int G, bool APPEND, bool BF16, bool SINGLE = false>
+template <int G, bool APPEND, int PF, bool SINGLE = false>
 void launch_stream_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k) {
-  decode_stream_kernel<G, APPEND, BF16, SINGLE><<<grid, 64, 0, stream>>>(
+  decode_stream_kernel<G, APPEND, PF, SINGLE><<<grid, 64, 0, stream>>>(
       k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
       APPEND ? k.append_slots : nullptr);
 }
 
-template <int G, bool APPEND, bool BF16>
+template <int G, bool APPEND, int PF>
 void launch_cascade_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k,
                             const prefill_detail::PrefillKernelArgs& prefix,
                             unsigned prefix_blocks) {
-  cascade_decode_kernel<G, APPEND, BF16><<<grid, 256, 0, stream>>>(
+  cascade_decode_kernel<G, APPEND, PF><<<grid, 256, 0, stream>>>(
       k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
       APPEND ? k.append_slots : nullptr, prefix, prefix_blocks);
+}
+
+// Runs body(APPEND, PF) with the compile-time forms of append and type.
+template <typename F>
+void with_stream_variant(bool append, PageType type, F&& body) {
+  using std::integral_constant;
+  const auto pick = [&](auto ap) {
+    switch (type) {
+      case PageType::kBF16: body(ap, integral_constant<int, 1>{}); break;
+      case PageType::kFP8: body(ap, integral_constant<int, 2>{}); break;
+      default: body(ap, integral_constant<int, 0>{}); break;
+    }
+  };
+  if (append) {
+    pick(integral_constant<bool, true>{});
+  } else {
+    pick(integral_constant<bool, false>{});
+  }
 }
 
 template <int G>
 void launch_cascade(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k,
                     const prefill_detail::PrefillKernelArgs& prefix, unsigned prefix_blocks,
-                    bool append, bool bf16) {
-  if (bf16) {
-    if (append) {
-      launch_cascade_variant<G, true, true>(grid, stream, k, prefix, prefix_blocks);
-    } else {
-      launch_cascade_variant<G, false, true>(grid, stream, k, prefix, prefix_blocks);
-    }
-  } else if (append) {
-    launch_cascade_variant<G, true, false>(grid, stream, k, prefix, prefix_blocks);
-  } else {
-    launch_cascade_variant<G, false, false>(grid, stream, k, prefix, prefix_blocks);
-  }
+                    bool append, PageType type) {
+  with_stream_variant(append, type, [&](auto ap, auto pf) {
+    launch_cascade_variant<G, decltype(ap)::value, decltype(pf)::value>(grid, stream, k, prefix,
+                                                                        prefix_blocks);
+  });
 }
 
 template <int G>
 void launch_stream(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k, bool append,
-                   bool bf16) {
-  if (bf16) {
-    if (append) {
-      launch_stream_variant<G, true, true>(grid, stream, k);
-    } else {
-      launch_stream_variant<G, false, true>(grid, stream, k);
-    }
-  } else if (append) {
-    launch_stream_variant<G, true, false>(grid, stream, k);
-  } else {
-    launch_stream_variant<G, false, false>(grid, stream, k);
-  }
+                   PageType type) {
+  with_stream_variant(append, type, [&](auto ap, auto pf) {
+    launch_stream_variant<G, decltype(ap)::value, decltype(pf)::value>(grid, stream, k);
+  });
 }
 
 }  // namespace
@@ -2055,11 +2161,15 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.pages_per_split = static_cast<int>(a.pages_per_split);
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
+  k.k_scale = a.page_type.k_scale;
+  k.v_scale = a.page_type.v_scale;
+  // fp8 keys widen to bare code values: their scale joins the score scale.
+  if (a.page_type.type == PageType::kFP8) k.qscale *= a.page_type.k_scale;
   if (a.lengths == nullptr) {
     // One sequence, history length passed by value, the caller's workspace
     // laid out for single_waves wavefronts.
     if (a.batch != 1 || !streamed || a.single_waves == 0 || a.shared_pages != 0 ||
-        a.append_slots != nullptr || a.page_type != PageType::kF32) {
+        a.append_slots != nullptr || a.page_type.type != PageType::kF32) {
       return hipErrorInvalidValue;
     }
     const WorkspaceLayout lay = stream_layout(1, a.q_heads, a.kv_heads, a.single_waves, 0);
@@ -2070,10 +2180,10 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     k.stream_waves = static_cast<int>(a.single_waves);
     const dim3 grid(static_cast<unsigned>(a.single_waves));
     switch (group) {
-      case 1: launch_stream_variant<1, false, false, true>(grid, stream, k); break;
-      case 2: launch_stream_variant<2, false, false, true>(grid, stream, k); break;
-      case 4: launch_stream_variant<4, false, false, true>(grid, stream, k); break;
-      case 8: launch_stream_variant<8, false, false, true>(grid, stream, k); break;
+      case 1: launch_stream_variant<1, false, 0, true>(grid, stream, k); break;
+      case 2: launch_stream_variant<2, false, 0, true>(grid, stream, k); break;
+      case 4: launch_stream_variant<4, false, 0, true>(grid, stream, k); break;
+      case 8: launch_stream_variant<8, false, 0, true>(grid, stream, k); break;
       default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
@@ -2101,7 +2211,10 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const bool overlap = !fused && a.shared_pages > 0 && a.side_stream != nullptr &&
                          a.fork_event != nullptr && a.join_event != nullptr;
     const std::size_t waves = stream_waves(group, overlap || fused);
-    if (a.compact_layout && a.shared_pages != 0) return hipErrorInvalidValue;
+    // The compact layout is sized for the fp32 kernel's wavefront count.
+    if (a.compact_layout && (a.shared_pages != 0 || a.page_type.type != PageType::kF32)) {
+      return hipErrorInvalidValue;
+    }
     const WorkspaceLayout lay =
         a.compact_layout ? stream_layout(a.batch, a.q_heads, a.kv_heads, waves, 0)
                          : stream_layout_for(a.batch, a.q_heads, a.kv_heads);
@@ -2136,12 +2249,12 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
         k.stream_waves = static_cast<int>(waves);
         const dim3 grid(static_cast<unsigned>(items + waves / 4));
         const bool append = k.append_slots != nullptr;
-        const bool bf16 = a.page_type == PageType::kBF16;
+        const PageType pt = a.page_type.type;
         const auto pb = static_cast<unsigned>(items);
         switch (group) {
-          case 1: launch_cascade<1>(grid, stream, k, pk, pb, append, bf16); break;
-          case 2: launch_cascade<2>(grid, stream, k, pk, pb, append, bf16); break;
-          case 4: launch_cascade<4>(grid, stream, k, pk, pb, append, bf16); break;
+          case 1: launch_cascade<1>(grid, stream, k, pk, pb, append, pt); break;
+          case 2: launch_cascade<2>(grid, stream, k, pk, pb, append, pt); break;
+          case 4: launch_cascade<4>(grid, stream, k, pk, pb, append, pt); break;
           default: return hipErrorInvalidValue;
         }
         hipError_t e = hipGetLastError();
@@ -2179,12 +2292,12 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     k.stream_waves = static_cast<int>(waves);
     const dim3 grid(static_cast<unsigned>(waves));
     const bool append = k.append_slots != nullptr;
-    const bool bf16 = a.page_type == PageType::kBF16;
+    const PageType pt = a.page_type.type;
     switch (group) {
-      case 1: launch_stream<1>(grid, stream, k, append, bf16); break;
-      case 2: launch_stream<2>(grid, stream, k, append, bf16); break;
-      case 4: launch_stream<4>(grid, stream, k, append, bf16); break;
-      case 8: launch_stream<8>(grid, stream, k, append, bf16); break;
+      case 1: launch_stream<1>(grid, stream, k, append, pt); break;
+      case 2: launch_stream<2>(grid, stream, k, append, pt); break;
+      case 4: launch_stream<4>(grid, stream, k, append, pt); break;
+      case 8: launch_stream<8>(grid, stream, k, append, pt); break;
       default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

@@ -26,12 +26,24 @@ struct PageGeometry {
   std::size_t head_dim;
 };
 
-// Element type of the pages: fp32 (the reference's format) or bf16 (the
-// appended fp32 value rounded to nearest even; NaN stays NaN).  Pool
-// pointers are untyped where either may be passed; strides and offsets are
-// in elements.  Rows appended and gather outputs are fp32 either way.
-enum class PageType : int { kF32 = 0, kBF16 = 1 };
-constexpr std::size_t page_element_bytes(PageType t) { return t == PageType::kBF16 ? 2 : 4; }
+// Element type of the pages: fp32 (the reference's format), bf16 (the
+// appended fp32 value rounded to nearest even; NaN stays NaN) or fp8 E4M3
+// with a key scale and a value scale (fp8.hpp).  Pool pointers are untyped
+// where several may be passed; strides and offsets are in elements.  Rows
+// appended and gather outputs are fp32 whatever the type.
+enum class PageType : int { kF32 = 0, kBF16 = 1, kFP8 = 2 };
+constexpr std::size_t page_element_bytes(PageType t) {
+  return t == PageType::kBF16 ? 2 : t == PageType::kFP8 ? 1 : 4;
+}
+// The page type with its fp8 scales (1 and ignored for the other types).
+struct PageFormat {
+  PageType type = PageType::kF32;
+  float k_scale = 1.0f;
+  float v_scale = 1.0f;
+  PageFormat() = default;
+  PageFormat(PageType t, float k = 1.0f, float v = 1.0f)  // NOLINT: implicit from the type
+      : type(t), k_scale(k), v_scale(v) {}
+};
 
 // One token for every layer.  src [layers, kv_heads, head_dim]; the token
 // lands at (block, offset) of every layer pool.  Layer l's key pool starts at
@@ -39,7 +51,7 @@ constexpr std::size_t page_element_bytes(PageType t) { return t == PageType::kBF
 hipError_t launch_append_token(const float* keys, const float* values, void* key_base,
                                void* value_base, std::size_t layer_stride, std::size_t layers,
                                const PageGeometry& g, std::uint32_t block, std::size_t offset,
-                               hipStream_t stream, PageType type = PageType::kF32);
+                               hipStream_t stream, PageFormat type = PageFormat());
 
 // Bulk layer-major append of `tokens` tokens.  layer_keys/layer_values are
 // device arrays of `layers` device pointers, each [kv_heads, tokens, dim].
@@ -51,7 +63,7 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
                               std::size_t layers, const PageGeometry& g,
                               const std::uint32_t* blocks, std::size_t first_block,
                               std::size_t old_length, std::size_t tokens, hipStream_t stream,
-                              bool vectorized, PageType type = PageType::kF32);
+                              bool vectorized, PageFormat type = PageFormat());
 
 // Batched append: src [layers, count, kv_heads, tokens, dim];
 // slots[i * tokens + t] is the flat slot block * block_tokens + offset of
@@ -60,7 +72,7 @@ hipError_t launch_append_bulk(const float* const* layer_keys, const float* const
 hipError_t launch_append_slots(const float* keys, const float* values, void* key_pool,
                                void* value_pool, const PageGeometry& g, const std::int64_t* slots,
                                std::size_t count, hipStream_t stream, std::size_t tokens = 1,
-                               PageType type = PageType::kF32, std::size_t layers = 1,
+                               PageFormat type = PageFormat(), std::size_t layers = 1,
                                std::size_t layer_stride = 0);
 
 // Rotary embedding (cpu::rope_out, bit-exact) of up to two tensors
@@ -80,14 +92,14 @@ hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t row
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
                          float* values_out, std::size_t dest_tokens, hipStream_t stream,
-                         PageType type = PageType::kF32);
+                         PageFormat type = PageFormat());
 
 // Copy the first `tokens` token rows of block `from` into block `to` for
 // every layer and head (copy-on-write of a partial shared page).
 hipError_t launch_page_copy(void* key_base, void* value_base, std::size_t layer_stride,
                             std::size_t layers, const PageGeometry& g, std::uint32_t from,
                             std::uint32_t to, std::size_t tokens, hipStream_t stream,
-                            PageType type = PageType::kF32);
+                            PageFormat type = PageFormat());
 
 // Scatter (row, column, value) triples into a [rows, cols] uint32 table.
 hipError_t launch_table_updates(std::uint32_t* tables, std::size_t cols,
@@ -130,10 +142,10 @@ struct DecodeArgs {
   // once for all sequences on the matrix cores and the stream kernel covers
   // the rest.  0: off.
   std::size_t shared_pages = 0;
-  // Element type of key_pool / value_pool (and the append pools): bf16 pages
-  // are read through the same pointers, typed nominally as float.  Stream
-  // mode only.
-  PageType page_type = PageType::kF32;
+  // Element type of key_pool / value_pool (and the append pools): bf16 and
+  // fp8 pages are read through the same pointers, typed nominally as float.
+  // Stream mode only for those types.
+  PageFormat page_type;
   // Optional second stream for the cascade prefix pass: when set (with the
   // two events), the prefix runs on side_stream concurrently with the
   // stream kernel, which then takes one wavefront per SIMD and leaves the
@@ -227,9 +239,9 @@ struct PrefillArgs {
   // Optional launch order of the batch * kv_heads * ceil(tokens / positions
   // per block) work items, packed (b * kv_heads + kvh) * blocks + block.
   const std::uint32_t* order = nullptr;
-  // bf16 pages: history keys/values are widened from bf16 and the chunk rows
-  // rounded to bf16 (the values their pages hold once appended).
-  PageType page_type = PageType::kF32;
+  // bf16 / fp8 pages: history keys/values are widened and the chunk rows
+  // rounded onto the page grid (the values their pages hold once appended).
+  PageFormat page_type;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of
@@ -244,7 +256,7 @@ struct CascadePrefixArgs {
   float* part_o;
   float* part_ml;
   std::size_t batch, q_heads, kv_heads, shared_pages, physical_blocks, prefix_slot0;
-  PageType page_type = PageType::kF32;
+  PageFormat page_type;
 };
 hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream);
 // The shared prefix is split into key chunks (each leaving its own partial

@@ -112,8 +112,8 @@ void synchronize_or_poison(CacheState& s, hipStream_t stream, const char* what) 
 
 }  // namespace
 
-CacheState::CacheState(const PagedConfig& config, int dev, hip::PageType type)
-    : manager(config, hip::page_element_bytes(type)), device((check_device(dev), dev)),
+CacheState::CacheState(const PagedConfig& config, int dev, hip::PageFormat type)
+    : manager(config, hip::page_element_bytes(type.type)), device((check_device(dev), dev)),
       page_type(type) {
   layer_elements = pool_elements(config);
   const std::size_t bytes = manager.stats().bytes_reserved;
@@ -143,7 +143,7 @@ void* CacheState::staging_bytes(std::size_t bytes) {
   return staging.data();
 }
 
-DevicePagedCache::DevicePagedCache(const PagedConfig& config, int device, hip::PageType page_type)
+DevicePagedCache::DevicePagedCache(const PagedConfig& config, int device, hip::PageFormat page_type)
     : state_(std::make_shared<CacheState>(config, device, page_type)) {}
 
 std::uint64_t DevicePagedCache::create_sequence() {
@@ -382,8 +382,8 @@ DecodeBatch::DecodeBatch(std::shared_ptr<CacheState> state, const std::uint64_t*
   }
   static_cast<void>(total_pages);
   pages_per_split_ = pages_per_split != 0 ? pages_per_split : hip::kDefaultPagesPerSplit;
-  check(!s.bf16() || pages_per_split_ == 0, Status::kUnsupported,
-        "decode batch: bf16 pages decode in stream mode only (pages_per_split 0)");
+  check(!s.reduced() || pages_per_split_ == 0, Status::kUnsupported,
+        "decode batch: bf16 and fp8 pages decode in stream mode only (pages_per_split 0)");
   check(hip::decode_max_splits(max_blocks_, pages_per_split_) <= hip::kMaxDecodeSplits,
         Status::kUnsupported, "decode batch: max_tokens / pages_per_split above 4096 splits");
   host_lengths_.assign(batch, 0);

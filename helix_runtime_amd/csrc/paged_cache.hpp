@@ -70,11 +70,11 @@ private:
 void hip_check(hipError_t e, const char* what);
 
 struct CacheState {
-  CacheState(const PagedConfig& config, int device, hip::PageType page_type = hip::PageType::kF32);
+  CacheState(const PagedConfig& config, int device, hip::PageFormat page_type = hip::PageFormat());
 
   BlockManager manager;
   int device;
-  hip::PageType page_type;
+  hip::PageFormat page_type;  // element type (and fp8 scales) of the pools
   DeviceBuffer slab;
   std::size_t layer_elements = 0;  // physical_blocks * kv_heads * block_tokens * head_dim
   std::mutex mutex;
@@ -85,15 +85,17 @@ struct CacheState {
   std::atomic<std::uint64_t> releases{0};
   DeviceBuffer staging;            // transient upload area (grown on demand)
 
-  // Layer pools: fp32 elements, or bf16 bits for a bf16 cache (the pointer
-  // type is nominal then; page_type says which).
+  // Layer pools: fp32 elements, or bf16 / fp8 bits for a reduced-precision
+  // cache (the pointer type is nominal then; page_type says which).
   [[nodiscard]] float* key_pool(std::size_t layer) const { return pool_at(2 * layer); }
   [[nodiscard]] float* value_pool(std::size_t layer) const { return pool_at(2 * layer + 1); }
   [[nodiscard]] float* pool_at(std::size_t index) const {
     return reinterpret_cast<float*>(static_cast<unsigned char*>(slab.data()) +
-                                    index * layer_elements * hip::page_element_bytes(page_type));
+                                    index * layer_elements * hip::page_element_bytes(page_type.type));
   }
-  [[nodiscard]] bool bf16() const noexcept { return page_type == hip::PageType::kBF16; }
+  [[nodiscard]] bool bf16() const noexcept { return page_type.type == hip::PageType::kBF16; }
+  [[nodiscard]] bool fp8() const noexcept { return page_type.type == hip::PageType::kFP8; }
+  [[nodiscard]] bool reduced() const noexcept { return page_type.type != hip::PageType::kF32; }
   [[nodiscard]] std::size_t layer_stride() const noexcept { return 2 * layer_elements; }
   [[nodiscard]] bool overlaps_pool(const void* p, std::size_t bytes) const;
   void require_healthy(const char* op) const;
@@ -108,7 +110,7 @@ struct CacheState {
 class DevicePagedCache {
 public:
   DevicePagedCache(const PagedConfig& config, int device,
-                   hip::PageType page_type = hip::PageType::kF32);
+                   hip::PageFormat page_type = hip::PageFormat());
 
   [[nodiscard]] const std::shared_ptr<CacheState>& state() const noexcept { return state_; }
   [[nodiscard]] std::uint64_t cache_id() const noexcept { return state_->manager.cache_id(); }

@@ -12,21 +12,27 @@ namespace {
 
 using namespace prefill_detail;
 
-template <int G, bool CASCADE, bool BF16, int RT>
+template <int G, bool CASCADE, int PF, int RT>
 __global__ __launch_bounds__(512 / RT, 6 - 2 * RT)
 void prefill_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ tables,
                     const std::uint32_t* __restrict__ order) {
   __shared__ PrefillShared sh;
-  prefill_body<G, CASCADE, BF16, RT>(a, tables, order, blockIdx.x, sh);
+  prefill_body<G, CASCADE, PF, RT>(a, tables, order, blockIdx.x, sh);
 }
 
 template <int G, bool CASCADE, int RT = kTilesPerWave>
 void launch_variant(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
                     const std::uint32_t* tables, const std::uint32_t* order, PageType type) {
-  if (type == PageType::kBF16) {
-    prefill_kernel<G, CASCADE, true, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
-  } else {
-    prefill_kernel<G, CASCADE, false, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
+  switch (type) {
+    case PageType::kBF16:
+      prefill_kernel<G, CASCADE, 1, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
+      break;
+    case PageType::kFP8:
+      prefill_kernel<G, CASCADE, 2, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
+      break;
+    default:
+      prefill_kernel<G, CASCADE, 0, RT><<<grid, 512 / RT, 0, stream>>>(k, tables, order);
+      break;
   }
 }
 
@@ -80,12 +86,14 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
   k.qscale = kLog2e / sqrtf(static_cast<float>(D));
   k.batch = static_cast<int>(a.batch);
+  k.k_scale = a.page_type.k_scale;
+  k.v_scale = a.page_type.v_scale;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   switch (group) {
-    case 1: launch_variant<1, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
-    case 2: launch_variant<2, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
-    case 4: launch_variant<4, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
-    case 8: launch_variant<8, false>(grid, stream, k, a.tables, a.order, a.page_type); break;
+    case 1: launch_variant<1, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;
+    case 2: launch_variant<2, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;
+    case 4: launch_variant<4, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;
+    case 8: launch_variant<8, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -112,6 +120,8 @@ prefill_detail::PrefillKernelArgs prefill_detail::cascade_prefix_args(const Casc
   k.part_o = a.part_o;
   k.part_ml = a.part_ml;
   k.prefix_slot0 = static_cast<long long>(a.prefix_slot0);
+  k.k_scale = a.page_type.k_scale;
+  k.v_scale = a.page_type.v_scale;
   const std::size_t chunks =
       (a.shared_pages + k.cascade_chunk_pages - 1) / k.cascade_chunk_pages;
   k.cascade_chunks = static_cast<int>(chunks);
@@ -126,10 +136,10 @@ hipError_t launch_cascade_prefix(const CascadePrefixArgs& a, hipStream_t stream)
   const PrefillKernelArgs k = cascade_prefix_args(a, &items);
   const dim3 grid(static_cast<unsigned>(items));
   switch (group) {
-    case 1: launch_variant<1, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 2: launch_variant<2, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 4: launch_variant<4, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
-    case 8: launch_variant<8, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type); break;
+    case 1: launch_variant<1, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type.type); break;
+    case 2: launch_variant<2, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type.type); break;
+    case 4: launch_variant<4, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type.type); break;
+    case 8: launch_variant<8, true, kCascadeTilesPerWave>(grid, stream, k, a.table, nullptr, a.page_type.type); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -38,6 +38,7 @@
 #include "kernels.hpp"
 
 #include "bf16.hpp"
+#include "fp8.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -92,6 +93,9 @@ struct PrefillKernelArgs {
   float* part_o;
   float* part_ml;
   long long prefix_slot0;
+  // fp8 pages: scales of the key and value codes.
+  float k_scale;
+  float v_scale;
 };
 
 // exp2(a - b), with a == b (also +inf == +inf, -inf == -inf) giving 1 and
@@ -128,16 +132,18 @@ __device__ __forceinline__ bool finite4(const float4& v) {
   return isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w);
 }
 
-// BF16: history pages hold bf16; staging widens them and rounds the fp32
-// chunk rows to bf16 (the values their pages will hold), so the math is the
-// fp32 kernel's on bf16-exact operands.
+// PF (page format, the PageType value): fp32 (0), bf16 (1) or fp8 E4M3 (2)
+// pages.  For bf16 and fp8 the staging widens history rows (fp8: times the
+// pool's scale) and rounds the fp32 chunk rows onto the same grid (the
+// values their pages will hold), so the math is the fp32 kernel's on
+// operands exact on that grid.
 // RT: 16-row tiles per wavefront (1 or 2); the workgroup has 8 / RT waves
 // and each SIMD runs 6 - 2 * RT of them.
 // LDS of one prefill workgroup.  fp32 pages: three K and three V stages
 // filled by direct global -> LDS loads; K rows unpadded with their 16-byte
 // chunks XOR-swizzled by row (chunk j of row r at j ^ (r & 15)), so the
-// MFMA operand reads (16 rows, one chunk) hit distinct banks.  bf16 pages:
-// two register-staged stages (the widening happens on the way), K rows
+// MFMA operand reads (16 rows, one chunk) hit distinct banks.  bf16 and fp8
+// pages: two register-staged stages (the widening happens on the way), K rows
 // padded to kKStride floats.
 constexpr int kDmaStages = 4;
 struct PrefillRegStages {
@@ -183,13 +189,15 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 
 // The body of one prefill (or cascade prefix) workgroup; `block` is its
 // work-item index (the block index of the standalone kernel).
-template <int G, bool CASCADE, bool BF16, int RT, class Shared>
+template <int G, bool CASCADE, int PF, int RT, class Shared>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
                                              const std::uint32_t* __restrict__ tables,
                                              const std::uint32_t* __restrict__ order,
                                              std::uint32_t block, Shared& sh) {
   constexpr int PW = kRows / G;  // chunk positions per workgroup
-  constexpr bool DMA = !BF16 && !CASCADE;
+  constexpr bool BF16 = PF == 1;
+  constexpr bool FP8 = PF == 2;
+  constexpr bool DMA = PF == 0 && !CASCADE;
   constexpr int kKRow = DMA ? D : kKStride;  // K row stride in LDS
   PrefillDmaStages* const ds = dma_stages(sh);  // null where DMA is off
   float (&s_k)[2][kKeys * kKStride] = sh.reg.k;
@@ -320,7 +328,21 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       const bool in_hist = key < hist;
       const bool valid = key < key_end && (!in_hist || page_ok);
       const int o = lane_off + RP * r * D;
-      if constexpr (BF16) {
+      if constexpr (FP8) {
+        // History rows: 4 fp8 codes in the low word; chunk rows: fp32.
+        stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        stv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (valid && in_hist) {
+          const std::size_t e = page_off + o;
+          stk[r].x = __uint_as_float(*reinterpret_cast<const unsigned*>(
+              reinterpret_cast<const unsigned char*>(a.key_pool) + e));
+          stv[r].x = __uint_as_float(*reinterpret_cast<const unsigned*>(
+              reinterpret_cast<const unsigned char*>(a.value_pool) + e));
+        } else if (valid) {
+          stk[r] = *reinterpret_cast<const float4*>(kchunk + o);
+          stv[r] = *reinterpret_cast<const float4*>(vchunk + o);
+        }
+      } else if constexpr (BF16) {
         // History rows: 4 bf16 in the low two words; chunk rows: fp32.
         stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
         stv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -354,7 +376,15 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       const int key = blk * kKeys + kr;
       float4 kv = stk[r];
       float4 vv = stv[r];
-      if constexpr (BF16) {
+      if constexpr (FP8) {
+        if (key < hist) {
+          kv = fp8_widen4(__float_as_uint(kv.x), a.k_scale);
+          vv = fp8_widen4(__float_as_uint(vv.x), a.v_scale);
+        } else {
+          kv = fp8_rounded(kv, a.k_scale);
+          vv = fp8_rounded(vv, a.v_scale);
+        }
+      } else if constexpr (BF16) {
         if (key < hist) {
           kv = bf16_widen(__float_as_uint(kv.x), __float_as_uint(kv.y));
           vv = bf16_widen(__float_as_uint(vv.x), __float_as_uint(vv.y));

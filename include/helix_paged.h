@@ -127,11 +127,28 @@ int helix_paged_cache_create(const helix_paged_config* config, int device,
  * step's fp32 tail rows rounded the same way.  Byte statistics count 2-byte
  * elements.  bf16 caches decode in stream mode only (pages_per_split 0), and
  * the pools helix_paged_cache_layer_pools / helix_decode_view_layer_pools
- * return then hold bf16 bits. */
-typedef enum helix_page_dtype { HELIX_PAGE_F32 = 0, HELIX_PAGE_BF16 = 1 } helix_page_dtype;
+ * return then hold bf16 bits.
+ * fp8 pages (HELIX_PAGE_FP8_E4M3) hold OCP FP8 E4M3 codes with one fp32
+ * scale for keys and one for values: an element is the code of x / scale
+ * rounded to nearest even, saturating at +-448 (NaN stays NaN), and its value
+ * is decode(code) * scale.  Gathers return those values; attention computes
+ * in fp32 on them, the step's tail and chunk rows rounded the same way; byte
+ * statistics count 1-byte elements; same stream-mode rule as bf16, and the
+ * pools hold the codes.  helix_paged_cache_create_typed with FP8 uses scales
+ * of 1. */
+typedef enum helix_page_dtype {
+  HELIX_PAGE_F32 = 0,
+  HELIX_PAGE_BF16 = 1,
+  HELIX_PAGE_FP8_E4M3 = 2
+} helix_page_dtype;
 int helix_paged_cache_create_typed(const helix_paged_config* config, int device, int page_dtype,
                                    helix_paged_cache** out);
+/* fp8 cache with its key and value scales (finite, positive). */
+int helix_paged_cache_create_fp8(const helix_paged_config* config, int device, float key_scale,
+                                 float value_scale, helix_paged_cache** out);
 int helix_paged_cache_page_dtype(helix_paged_cache* cache, int* out);
+/* The key and value scales of an fp8 cache (1 and 1 for the other types). */
+int helix_paged_cache_fp8_scales(helix_paged_cache* cache, float* key_scale, float* value_scale);
 void helix_paged_cache_destroy(helix_paged_cache* cache);
 int helix_paged_cache_create_sequence(helix_paged_cache* cache, helix_sequence* out);
 /* PagedKvCache::fork_sequence (paged.cpp:535-620); allow_cow != 0 copies a

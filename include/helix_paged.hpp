@@ -127,10 +127,10 @@ inline void check_hip(hipError_t status, const char* what) {
 
 // ------------------------------------------------------------------ tensor --
 
-enum class DType { kFloat32, kBFloat16, kInt32, kInt64, kUInt32 };
+enum class DType { kFloat32, kBFloat16, kInt32, kInt64, kUInt32, kFp8E4M3 };
 
 [[nodiscard]] constexpr std::size_t dtype_size(DType d) noexcept {
-  return d == DType::kBFloat16 ? 2 : (d == DType::kInt64 ? 8 : 4);
+  return d == DType::kFp8E4M3 ? 1 : d == DType::kBFloat16 ? 2 : (d == DType::kInt64 ? 8 : 4);
 }
 
 struct Device {
@@ -385,8 +385,20 @@ struct PagedKvCacheStats {
   }
 };
 
-/// Page storage type (extension: bf16 pages halve HBM bytes per token).
-enum class PageDType { kFloat32 = HELIX_PAGE_F32, kBFloat16 = HELIX_PAGE_BF16 };
+/// Page storage type (extension: bf16 pages halve HBM bytes per token, fp8
+/// E4M3 pages quarter them; fp8 scales as Fp8Scales, 1 and 1 by default).
+enum class PageDType {
+  kFloat32 = HELIX_PAGE_F32,
+  kBFloat16 = HELIX_PAGE_BF16,
+  kFp8E4M3 = HELIX_PAGE_FP8_E4M3
+};
+/// The key and value scales of an fp8 cache: a page element is the E4M3
+/// code of x / scale (nearest even, saturating at +-448), worth
+/// decode(code) * scale.
+struct Fp8Scales {
+  float key = 1.0F;
+  float value = 1.0F;
+};
 
 class HipPagedKvCache;
 class HipPagedPrefixCache;
@@ -598,14 +610,19 @@ class HipPagedKvCache final {
   };
 
   explicit HipPagedKvCache(PagedKvCacheConfig config, int device_index = 0,
-                           PageDType pages = PageDType::kFloat32)
+                           PageDType pages = PageDType::kFloat32, Fp8Scales scales = {})
       : impl_(std::make_shared<Impl>()) {
     detail::require(device_index >= 0, ErrorCode::kInvalidArgument,
                     "HipPagedKvCache: device index must be non-negative");
     const helix_paged_config c{config.layers, config.kv_heads, config.head_dimension,
                                config.block_tokens, config.physical_blocks};
-    detail::check(helix_paged_cache_create_typed(&c, device_index, static_cast<int>(pages),
+    if (pages == PageDType::kFp8E4M3) {
+      detail::check(helix_paged_cache_create_fp8(&c, device_index, scales.key, scales.value,
                                                  &impl_->cache));
+    } else {
+      detail::check(helix_paged_cache_create_typed(&c, device_index, static_cast<int>(pages),
+                                                   &impl_->cache));
+    }
     impl_->config = config;
     impl_->device = device_index;
     detail::check(helix_paged_cache_geometry(impl_->cache, &impl_->bytes_per_token,
@@ -715,7 +732,9 @@ class HipPagedKvCache final {
                      static_cast<Dimension>(c.head_dimension)};
     int dtype = HELIX_PAGE_F32;
     detail::check(helix_paged_cache_page_dtype(impl_->cache, &dtype));
-    const DType element = dtype == HELIX_PAGE_BF16 ? DType::kBFloat16 : DType::kFloat32;
+    const DType element = dtype == HELIX_PAGE_BF16      ? DType::kBFloat16
+                          : dtype == HELIX_PAGE_FP8_E4M3 ? DType::kFp8E4M3
+                                                         : DType::kFloat32;
     for (std::size_t l = 0; l < c.layers; ++l) {
       float* k = nullptr;
       float* vv = nullptr;

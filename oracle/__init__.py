@@ -166,6 +166,59 @@ def round_bf16(x):
     return (bf16_bits(x).astype(np.uint32) << 16).view(np.float32)
 
 
+# ------------------------------------------------------------- fp8 pages --
+# Extension (no reference counterpart, as bf16 above).  fp8 pages hold OCP
+# FP8 E4M3 ("e4m3fn": 1 sign, 4 exponent bits of bias 7, 3 mantissa bits; no
+# infinities; 0x7f / 0xff are NaN; largest finite 448) with one fp32 scale per
+# cache for keys and one for values.  The contract: a page element is the
+# code of x / scale (an fp32 division) rounded to nearest, ties to even,
+# saturating: values past 448 (infinities included) become +-448, NaN
+# stays NaN (0x7f with the sign).  Its value is decode(code) * scale (an
+# fp32 product).  Attention over fp8 pages is the fp32 reference evaluated
+# on those values; the step's fp32 tail rows and chunk rows go through the
+# same rounding (they are the values their pages hold once appended).
+FP8_MAX = 448.0
+
+
+def fp8_decode(codes):
+    """float32 values of E4M3 codes (uint8), from the format's definition."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+    return (sign * mag).astype(np.float32)
+
+
+_FP8_TABLE = fp8_decode(np.arange(128, dtype=np.uint8)[:127]).astype(np.float64)  # 0 .. 448
+
+
+def fp8_bits(x, scale=1.0):
+    """uint8 E4M3 codes of float32 values divided by ``scale`` (saturating,
+    ties to even), by nearest search over the 127 non-negative finite codes."""
+    with np.errstate(invalid="ignore"):
+        y = np.ascontiguousarray(x, dtype=np.float32) / np.float32(scale)
+    a = np.abs(y.astype(np.float64)).ravel()
+    nan = np.isnan(a)
+    a = np.where(nan, 0.0, np.minimum(a, FP8_MAX))
+    hi = np.searchsorted(_FP8_TABLE, a, side="left")          # first code >= a
+    hi = np.minimum(hi, 126)
+    lo = np.maximum(hi - 1, 0)
+    dlo = a - _FP8_TABLE[lo]
+    dhi = _FP8_TABLE[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(a == _FP8_TABLE[hi], hi, np.where(pick_hi, hi, lo))
+    code = np.where(nan, 0x7F, code)
+    sign = (y.view(np.uint32).ravel() >> 31).astype(np.int64) << 7
+    return (code | sign).astype(np.uint8).reshape(np.shape(y))
+
+
+def round_fp8(x, scale=1.0):
+    """float32 values moved onto the scaled fp8 grid: decode(code) * scale."""
+    return fp8_decode(fp8_bits(x, scale)) * np.float32(scale)
+
+
 def mt19937_64_nth(seed, n):
     return int(lib().oracle_mt19937_64_nth(seed, n))
 

@@ -266,7 +266,7 @@ def test_chunked_prefill_on_bf16_pages(device):
 
 def test_bf16_validation(device):
     with pytest.raises(hx.HelixError) as e:
-        hx.PagedKvCache(1, 1, D, P, 4, page_dtype="fp8")
+        hx.PagedKvCache(1, 1, D, P, 4, page_dtype="fp4")
     assert e.value.status == hx.INVALID_ARGUMENT
     cache = hx.PagedKvCache(1, 2, D, P, 8, page_dtype="bf16")
     s = cache.create_sequence()

@@ -632,3 +632,78 @@ def test_bf16_rounding_matches_torch():
     want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(oracle.bf16_bits(x), want)
     assert np.array_equal(oracle.round_bf16(x), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+# ------------------------------------------------------------- fp8 pages ----
+def test_fp8_decode_matches_torch_on_every_code():
+    """The E4M3 value table from the format's definition against torch's
+    float8_e4m3fn -> float32 widening, all 256 codes (NaN codes as NaN)."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.fp8_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))  # signed zeros too
+    assert np.isnan(got[[0x7F, 0xFF]]).all() and np.isnan(got).sum() == 2
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and got[0x08] == 2.0 ** -6
+
+
+def test_fp8_rounding_known_answers():
+    """Ties to even on the E4M3 grid, the subnormal step, saturation and NaN."""
+    f = np.float32
+    cases = [
+        (1.0, 0x38), (-2.0, 0xC0), (0.0, 0x00), (-0.0, 0x80),
+        (1.0625, 0x38),   # halfway 1.0 / 1.125: even (down)
+        (1.1875, 0x3A),   # halfway 1.125 / 1.25: even (up)
+        (1.0626, 0x39), (1.0624, 0x38),
+        (448.0, 0x7E), (449.0, 0x7E), (464.0, 0x7E), (465.0, 0x7E), (1e30, 0x7E),
+        (np.inf, 0x7E), (-np.inf, 0xFE),   # saturating: no infinities in E4M3
+        (2.0 ** -9, 0x01), (2.0 ** -10, 0x00),  # halfway 0 / 2^-9: even (zero)
+        (3 * 2.0 ** -10, 0x02),                 # halfway 2^-9 / 2^-8: even (up)
+        (2.0 ** -6, 0x08), (15 * 2.0 ** -10, 0x08),  # last subnormal step rounds up to 2^-6
+        (np.uint32(1).view(np.float32), 0x00),  # fp32 subnormal: zero
+    ]
+    for x, want in cases:
+        got = int(oracle.fp8_bits(np.array([x], f))[0])
+        assert got == want, (x, hex(got), hex(want))
+    nan = oracle.fp8_bits(np.array([np.nan, -np.nan], f))
+    assert nan.tolist() == [0x7F, 0xFF]
+
+
+def test_fp8_rounding_matches_torch_in_range():
+    """torch's float32 -> float8_e4m3fn conversion rounds to nearest even and
+    turns what rounds past 448 into NaN; this contract saturates instead.
+    Below that boundary (|x| < 464) the two agree bit for bit; above it
+    every value saturates."""
+    import torch
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 1 << 32, 300000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    x = np.concatenate([x, rng.standard_normal(100000).astype(np.float32),
+                        rng.standard_normal(50000).astype(np.float32) * 100,
+                        rng.standard_normal(50000).astype(np.float32) * 1e-3])
+    small = np.abs(x) < 464.0
+    want = torch.from_numpy(x[small]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.fp8_bits(x[small]), want)
+    big = x[~small]
+    assert big.size > 1000
+    assert np.array_equal(oracle.fp8_bits(big), np.where(big > 0, 0x7E, 0xFE).astype(np.uint8))
+
+
+def test_fp8_scale_divides_before_rounding():
+    """code = round(x / scale); value = decode(code) * scale, both in fp32."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(20000).astype(np.float32) * 7
+    for scale in (1.0, 0.25, 0.0371, 3.0):
+        s = np.float32(scale)
+        assert np.array_equal(oracle.fp8_bits(x, scale), oracle.fp8_bits(x / s))
+        want = oracle.fp8_decode(oracle.fp8_bits(x / s)) * s
+        assert np.array_equal(oracle.round_fp8(x, scale), want)
+        # relative error of the grid: at most half a mantissa step (2^-4) in range
+        v = oracle.round_fp8(x, scale)
+        normal = np.abs(x / s) >= 2.0 ** -6
+        inrange = np.abs(x / s) <= 448
+        m = normal & inrange
+        assert (np.abs(v[m] - x[m]) <= np.abs(x[m]) * 2.0 ** -4 * (1 + 1e-6)).all()
