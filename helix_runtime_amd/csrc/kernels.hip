@@ -1493,11 +1493,12 @@ __device__ __forceinline__ void decode_stream_body(
     step_body(d, kr, vr, qn, bad);
   };
 
-  // Two pages in flight, each in its own register buffer.  bf16 pages hold
-  // half the bytes, yet more bf16 pages in flight measured slower (3 pages:
-  // 130 against 125 us per config-3 layer, query rows moved to LDS to fit
-  // the registers; 4 pages: LDS-limited occupancy, 191 us): at two
-  // wavefronts per SIMD the bf16 kernel is held by its per-page math.
+  // Two pages in flight, each in its own register buffer.  More did not
+  // help the reduced-precision pages, whose kernels are held by their
+  // per-page instruction latency at two wavefronts per SIMD: bf16 with 3
+  // pages 130 against 125 us per config-3 layer (query rows moved to LDS to
+  // fit the registers), with 4 pages 191 us (LDS-limited occupancy); fp8
+  // with 3 and 4 pages 146 and 150 against 140 us.
   Raw ka[8], va[8], kb[8], vb[8];
   float4 qa[G], qb[G];
 #pragma unroll
