@@ -23,6 +23,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cmath>
 #include <array>
 #include <chrono>
 #include <cstring>
@@ -856,6 +857,73 @@ TEST_F(HipPagedKvCacheTest, Bf16PagesRoundOnAppendAndWidenOnGather) {
           const std::size_t src = (l * 2 + h) * 8 + d;
           EXPECT_EQ(hk[(h * 7 + t) * 8 + d], bf16_round(keys[t][src]));
           EXPECT_EQ(hv[(h * 7 + t) * 8 + d], bf16_round(values[t][src]));
+        }
+  }
+}
+
+// Extension: fp8 E4M3 pages with a key and a value scale.  The expected
+// value of x is the nearest code of x / scale (ties to the even code,
+// saturating at 448) decoded and times the scale, found here by search over
+// the format's value table.
+float fp8_expected(float x, float scale) {
+  const float y = x / scale;
+  double best = 0.0;
+  int best_code = 0;
+  const double a = std::fabs(static_cast<double>(y));
+  for (int c = 0; c < 127; ++c) {  // non-negative finite codes, increasing
+    const int e = c >> 3, m = c & 7;
+    const double v = e == 0 ? m * std::ldexp(1.0, -9) : (1.0 + m / 8.0) * std::ldexp(1.0, e - 7);
+    const double d = std::fabs(v - std::min(a, 448.0));
+    const double db = std::fabs(best - std::min(a, 448.0));
+    if (c == 0 || d < db || (d == db && (c & 1) == 0)) {
+      best = v;
+      best_code = c;
+    }
+  }
+  static_cast<void>(best_code);
+  const float mag = static_cast<float>(best);
+  return (std::signbit(y) ? -mag : mag) * scale;
+}
+
+TEST_F(HipPagedKvCacheTest, Fp8PagesRoundOnAppendAndWidenOnGather) {
+  const PagedKvCacheConfig config{2, 2, 8, 4, 8};
+  const Fp8Scales scales{0.05F, 0.02F};
+  HipPagedKvCache cache(config, 0, PageDType::kFp8E4M3, scales);
+  Stream stream;
+  const auto seq = cache.create_sequence();
+  std::vector<std::vector<float>> keys, values;  // per token [L, H, D]
+  for (std::size_t t = 0; t < 6; ++t) {
+    const Tensor k = random_uniform({2, 2, 8}, 1900 + t, -3, 3);
+    const Tensor v = random_uniform({2, 2, 8}, 1950 + t, -3, 3);
+    keys.emplace_back(k.data_as<float>(), k.data_as<float>() + k.numel());
+    values.emplace_back(v.data_as<float>(), v.data_as<float>() + v.numel());
+    cache.append(seq, k.to(kGpu), v.to(kGpu), stream);
+  }
+  // Past the largest code: saturates to 448 * scale.
+  const std::vector<float> big(32, 1e6F);
+  cache.append(seq, Tensor::from_values({2, 2, 8}, big, kGpu),
+               Tensor::from_values({2, 2, 8}, big, kGpu), stream);
+  keys.push_back(big);
+  values.push_back(big);
+  stream.synchronize();
+  EXPECT_EQ(fp8_expected(1e6F, 0.05F), 448.0F * 0.05F);
+  {
+    auto view = cache.read_sequence(seq);
+    EXPECT_TRUE(view.layer_key_blocks()[0].dtype() == DType::kFp8E4M3);
+    EXPECT_EQ(view.length(), 7U);
+  }
+  for (std::size_t l = 0; l < 2; ++l) {
+    Tensor gk = Tensor::empty({2, 7, 8}, DType::kFloat32, kGpu);
+    Tensor gv = Tensor::empty({2, 7, 8}, DType::kFloat32, kGpu);
+    cache.copy_layer_out(seq, l, gk, gv, stream);
+    stream.synchronize();
+    const auto hk = host_values(gk), hv = host_values(gv);
+    for (std::size_t h = 0; h < 2; ++h)
+      for (std::size_t t = 0; t < 7; ++t)
+        for (std::size_t d = 0; d < 8; ++d) {
+          const std::size_t src = (l * 2 + h) * 8 + d;
+          EXPECT_EQ(hk[(h * 7 + t) * 8 + d], fp8_expected(keys[t][src], scales.key));
+          EXPECT_EQ(hv[(h * 7 + t) * 8 + d], fp8_expected(values[t][src], scales.value));
         }
   }
 }
