@@ -906,10 +906,13 @@ struct PageDesc {
 // short units per wavefront).
 constexpr int kStreamStage = 4;
 
+
 // One token row's 4 dims of a page buffer as fp32: fp32 pages as loaded,
 // bf16 pages (4 per 64-bit lane load) widened where the row is used, so a
 // buffer never holds a widened copy of its page.
 __device__ __forceinline__ float4 page_row(const float4& x) { return x; }
+// First word of an fp8 page buffer row (the LDS query path orders on it).
+__device__ __forceinline__ unsigned first_word(const unsigned& x) { return x; }
 __device__ __forceinline__ float4 page_row(const uint2& x) { return bf16_widen(x.x, x.y); }
 __device__ __forceinline__ float4 page_row(const unsigned& x) { return fp8_widen4(x, 1.0f); }
 __device__ __forceinline__ float4 masked_row(const float4& x, bool keep) {
@@ -944,23 +947,39 @@ struct StreamShared {
 // them to separate __shared__ arrays: as distinct objects they are known not
 // to overlap, which the dynamically indexed fields of one struct are not
 // (the struct form cost 70 extra LDS reads and spills in the loop).
-template <int G>
+// S: results staged before a flush.  qslot: query rows loaded straight
+// into LDS, one area per page buffer (reduced-precision pages), or null.
+template <int G, int S = kStreamStage>
 struct StreamLds {
   float (&p)[2][8 * G];
   float (&head)[3][G];
-  float4 (&res_o)[kStreamStage][G][32];
-  float (&res_ml)[kStreamStage][G][2];
-  long long (&res_dst)[kStreamStage];
-  int2 (&seg)[kStreamStage];
-  int (&seg_unit)[kStreamStage];
-  float4 (&app_k)[kStreamStage][32];
-  float4 (&app_v)[kStreamStage][32];
-  long long (&app_dst)[kStreamStage];
+  float4 (&res_o)[S][G][32];
+  float (&res_ml)[S][G][2];
+  long long (&res_dst)[S];
+  int2 (&seg)[S];
+  int (&seg_unit)[S];
+  float4 (&app_k)[S][32];
+  float4 (&app_v)[S][32];
+  long long (&app_dst)[S];
+  float4 (*qslot)[G][32];
 };
 template <int G>
 __device__ __forceinline__ StreamLds<G> stream_lds(StreamShared<G>& s) {
   return StreamLds<G>{s.p, s.head, s.res_o, s.res_ml, s.res_dst,
-                      s.seg, s.seg_unit, s.app_k, s.app_v, s.app_dst};
+                      s.seg, s.seg_unit, s.app_k, s.app_v, s.app_dst, nullptr};
+}
+
+// fp8 pages in the stream kernel: query rows through LDS (not in a
+// register copy per page buffer), two results staged, three wavefronts per
+// SIMD, which their small page buffers then allow (137-150 VGPRs).  Config
+// 3, one box: 116.5 against 140.4 us per layer with two wavefronts.  bf16
+// pages stay at two: with the same change and the probabilities read from
+// LDS where used (167 VGPRs, no spills) they ran 129.8 against 125.8 us
+// (145 us with spills when the probabilities stayed in registers).
+constexpr bool stream_lds_query_type(PageType t) { return t == PageType::kFP8; }
+template <int PF, int G>
+constexpr bool stream_lds_query() {
+  return G <= 4 && stream_lds_query_type(static_cast<PageType>(PF));
 }
 
 // LDS hand-off inside one wavefront.  In the stream kernel a workgroup is a
@@ -980,12 +999,12 @@ __device__ __forceinline__ void stream_sync() {
 
 // The body of one stream wavefront: `wave` is its index among
 // a.stream_waves, `lane` its lane, `sh` its LDS.
-template <int G, bool APPEND, int PF, bool SHARED_BLOCK, bool SINGLE = false>
+template <int G, bool APPEND, int PF, bool SHARED_BLOCK, bool SINGLE = false, int S = kStreamStage>
 __device__ __forceinline__ void decode_stream_body(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
-    const std::int64_t* __restrict__ append_slots, int wave, int lane, StreamLds<G> sh) {
+    const std::int64_t* __restrict__ append_slots, int wave, int lane, StreamLds<G, S> sh) {
   // The block table and lengths are read-only here and do not alias the
   // outputs; with the restrict-qualified parameters their uniform reads
   // become scalar loads.
@@ -1001,7 +1020,8 @@ __device__ __forceinline__ void decode_stream_body(
   constexpr int R = G >= 4 ? G / 4 : 1;
   constexpr int DUPB = G >= 4 ? 0 : (G == 2 ? 1 : 2);
   constexpr int NV = 8 * G;
-  constexpr int kStage = kStreamStage;
+  constexpr int kStage = S;
+  constexpr bool QLDS = !SHARED_BLOCK && stream_lds_query<PF, G>();
   auto& s_p = sh.p;
   auto& s_head = sh.head;
   auto& s_res_o = sh.res_o;
@@ -1140,7 +1160,9 @@ __device__ __forceinline__ void decode_stream_body(
   const int lane_off = lane * (FP8 ? 4 : BF16 ? 8 : 16);
   const int row_off = j * 16;
   using Raw = std::conditional_t<FP8, unsigned, std::conditional_t<BF16, uint2, float4>>;
-  auto load_page = [&](const PageDesc& d, Raw (&k)[8], Raw (&v)[8], float4 (&q)[G], bool& bad) {
+  // slot: the buffer's LDS query area (query rows through LDS), else unused.
+  auto load_page = [&](const PageDesc& d, Raw (&k)[8], Raw (&v)[8], float4 (&q)[G], bool& bad,
+                       int slot) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
     const int kvh = __builtin_amdgcn_readfirstlane(d.kvh);
     const int p = __builtin_amdgcn_readfirstlane(d.p);
@@ -1172,11 +1194,25 @@ __device__ __forceinline__ void decode_stream_body(
       }
     }
     if (p == 0 || d.g == g0) {
-      const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<float*>(a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D),
-          0, d.skip ? 0 : G * D * 4, kBufferWord3);
+      const float* qsrc = a.query + (static_cast<std::size_t>(b) * a.q_heads + kvh * G) * D;
+      if constexpr (QLDS) {
+        // The G rows (G * 32 vectors of 16 bytes) straight into this
+        // buffer's LDS area, issued ahead of the page: the wait for the
+        // page's first key load covers them.
 #pragma unroll
-      for (int h = 0; h < G; ++h) q[h] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(qr, row_off, h * D * 4, 0));
+        for (int i = 0; i < (G * 32 + 63) / 64; ++i) {
+          if (i * 64 + lane < G * 32) {
+            prefill_detail::lds_load16(qsrc + (i * 64 + lane) * 4,
+                                       prefill_detail::lds_address(&sh.qslot[slot][0][0]) +
+                                           i * 1024);
+          }
+        }
+      } else {
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(qsrc), 0, d.skip ? 0 : G * D * 4, kBufferWord3);
+#pragma unroll
+        for (int h = 0; h < G; ++h) q[h] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(qr, row_off, h * D * 4, 0));
+      }
     }
     // A skip descriptor (past the end of the range) gets an empty buffer
     // range: its loads return zeros without touching memory, and the step
@@ -1427,7 +1463,7 @@ __device__ __forceinline__ void decode_stream_body(
   };
 
   float4 qc[G];  // query rows of the unit being processed
-  auto step_body = [&](const PageDesc& d, const auto& k, auto& v, const float4 (&qn)[G],
+  auto step_body = [&](const PageDesc& d, const auto& k, auto& v, const float4 (&qn)[G], int slot,
                        bool bad) {
     int valid = 0;
     if (!d.skip) {
@@ -1436,6 +1472,16 @@ __device__ __forceinline__ void decode_stream_body(
       if (d.p == 0 || d.g == g0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) qc[h] = qn[h];
+        if constexpr (QLDS) {
+          // Read the LDS area only once its direct loads have landed: the
+          // index depends (through an empty asm) on the page's first key
+          // word, so the read waits for that load, which was issued after
+          // the query loads.
+          int dep = 0;
+          asm volatile("" : "+v"(dep) : "v"(first_word(k[0])));
+#pragma unroll
+          for (int h = 0; h < G; ++h) qc[h] = sh.qslot[slot][h][j + dep];
+        }
       }
       if (d.p == 0) {
         // This wavefront holds the unit's first page: record which
@@ -1468,7 +1514,8 @@ __device__ __forceinline__ void decode_stream_body(
     process(k, v, qc, valid);
     if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
   };
-  auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad) {
+  auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad,
+                  int slot) {
     if constexpr (FP8) {
       if (!d.skip && d.p == d.np - 1) {
         // The tail row arrived as fp32 in slots 0-3: its codes (the values
@@ -1490,7 +1537,7 @@ __device__ __forceinline__ void decode_stream_body(
                            bf16_pack(__uint_as_float(vr[1].x), __uint_as_float(vr[1].y)));
       }
     }
-    step_body(d, kr, vr, qn, bad);
+    step_body(d, kr, vr, qn, slot, bad);
   };
 
   // Two pages in flight, each in its own register buffer.  More did not
@@ -1500,46 +1547,67 @@ __device__ __forceinline__ void decode_stream_body(
   // fit the registers), with 4 pages 191 us (LDS-limited occupancy); fp8
   // with 3 and 4 pages 146 and 150 against 140 us.
   Raw ka[8], va[8], kb[8], vb[8];
-  float4 qa[G], qb[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) qa[h] = qb[h] = qc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
   bool bada, badb;
-  PageDesc da = next_desc();
-  load_page(da, ka, va, qa, bada);
-  PageDesc db = next_desc();
-  load_page(db, kb, vb, qb, badb);
-  for (long long g = g0; g < g1; g += 2) {
-    step(da, ka, va, qa, bada);
-    da = next_desc();
-    load_page(da, ka, va, qa, bada);
-    step(db, kb, vb, qb, badb);
-    db = next_desc();
-    load_page(db, kb, vb, qb, badb);
+  if constexpr (QLDS) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) qc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    PageDesc da = next_desc();
+    load_page(da, ka, va, qc, bada, 0);
+    PageDesc db = next_desc();
+    load_page(db, kb, vb, qc, badb, 1);
+    for (long long g = g0; g < g1; g += 2) {
+      step(da, ka, va, qc, bada, 0);
+      da = next_desc();
+      load_page(da, ka, va, qc, bada, 0);
+      step(db, kb, vb, qc, badb, 1);
+      db = next_desc();
+      load_page(db, kb, vb, qc, badb, 1);
+    }
+  } else {
+    float4 qa[G], qb[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) qa[h] = qb[h] = qc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    PageDesc da = next_desc();
+    load_page(da, ka, va, qa, bada, 0);
+    PageDesc db = next_desc();
+    load_page(db, kb, vb, qb, badb, 1);
+    for (long long g = g0; g < g1; g += 2) {
+      step(da, ka, va, qa, bada, 0);
+      da = next_desc();
+      load_page(da, ka, va, qa, bada, 0);
+      step(db, kb, vb, qb, badb, 1);
+      db = next_desc();
+      load_page(db, kb, vb, qb, badb, 1);
+    }
   }
   flush();
 }
 
 template <int G, bool APPEND, int PF, bool SINGLE = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 2 : 1)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
+    G > 4 ? 1 : (stream_lds_query<PF, G>() ? 3 : 2))))
 void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
     const std::int64_t* __restrict__ append_slots) {
+  constexpr bool QLDS = stream_lds_query<PF, G>();
+  constexpr int S = QLDS ? 2 : kStreamStage;
   __shared__ __align__(16) float s_p[2][8 * G];
   __shared__ __align__(16) float s_head[3][G];
-  __shared__ __align__(16) float4 s_res_o[kStreamStage][G][32];
-  __shared__ float s_res_ml[kStreamStage][G][2];
-  __shared__ long long s_res_dst[kStreamStage];
-  __shared__ int2 s_seg[kStreamStage];
-  __shared__ int s_seg_unit[kStreamStage];
-  __shared__ __align__(16) float4 s_app_k[kStreamStage][32];
-  __shared__ __align__(16) float4 s_app_v[kStreamStage][32];
-  __shared__ long long s_app_dst[kStreamStage];
-  decode_stream_body<G, APPEND, PF, false, SINGLE>(
+  __shared__ __align__(16) float4 s_res_o[S][G][32];
+  __shared__ float s_res_ml[S][G][2];
+  __shared__ long long s_res_dst[S];
+  __shared__ int2 s_seg[S];
+  __shared__ int s_seg_unit[S];
+  __shared__ __align__(16) float4 s_app_k[S][32];
+  __shared__ __align__(16) float4 s_app_v[S][32];
+  __shared__ long long s_app_dst[S];
+  __shared__ __align__(16) float4 s_qslot[QLDS ? 2 : 1][G][32];
+  decode_stream_body<G, APPEND, PF, false, SINGLE, S>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
-      StreamLds<G>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k, s_app_v,
-                   s_app_dst});
+      StreamLds<G, S>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k,
+                      s_app_v, s_app_dst, QLDS ? s_qslot : nullptr});
 }
 
 // Cascade decode in one launch.  Blocks [0, prefix_blocks) are the cascade
@@ -2063,7 +2131,8 @@ namespace {
 // finds registers on every SIMD.  fp8 pages at three per SIMD (the register
 // cap of 168 spills at four query heads) measured slower: 181 against
 // 140 us per config-3 layer.
-std::size_t stream_waves(std::size_t group, bool beside_prefix) {
+std::size_t stream_waves(std::size_t group, bool beside_prefix,
+                         PageType type = PageType::kF32) {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -2076,7 +2145,7 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix) {
     cus[dev] = n;
   }
   const std::size_t per_simd =
-      group >= 8 || beside_prefix ? 1 : 2;
+      group >= 8 || beside_prefix ? 1 : (stream_lds_query_type(type) ? 3 : 2);
   const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
   return w < kMaxStreamWaves ? w : kMaxStreamWaves;
 }
@@ -2211,7 +2280,7 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const bool fused = a.shared_pages > 0 && group <= kCascadeFusedMaxGroup;
     const bool overlap = !fused && a.shared_pages > 0 && a.side_stream != nullptr &&
                          a.fork_event != nullptr && a.join_event != nullptr;
-    const std::size_t waves = stream_waves(group, overlap || fused);
+    const std::size_t waves = stream_waves(group, overlap || fused, a.page_type.type);
     // The compact layout is sized for the fp32 kernel's wavefront count.
     if (a.compact_layout && (a.shared_pages != 0 || a.page_type.type != PageType::kF32)) {
       return hipErrorInvalidValue;
