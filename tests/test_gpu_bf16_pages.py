@@ -273,3 +273,51 @@ def test_bf16_validation(device):
     with pytest.raises(hx.HelixError) as e:  # the split path reads fp32 pages only
         hx.DecodeBatch(cache, [s], 8, max_tokens=64, pages_per_split=4)
     assert e.value.status == hx.UNSUPPORTED
+
+
+@pytest.mark.parametrize("hq", [8, 32])
+def test_decode_with_infinite_keys_matches_oracle(device, hq):
+    """Keys of +-inf in bf16 pages: a page holding one takes fp32 dot
+    products, so scores are +-inf (or NaN) exactly as in the oracle; pages
+    without one are unaffected."""
+    L, H = 1, 8
+    rng = np.random.default_rng(61 + hq)
+    lengths = [40, 70, 5]
+    N = sum((n + 8) // P + 2 for n in lengths) + 4
+    cache = hx.PagedKvCache(L, H, D, P, N, page_dtype="bf16")
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for i, n in enumerate(lengths):
+        s, so = cache.create_sequence(), pool.create_sequence()
+        k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+        if i == 0:
+            k[0, 1, 5, 3] = np.inf      # one +inf dim: score +-inf by the query's sign
+            k[0, 2, 20, 7] = -np.inf
+        if i == 1:
+            k[0, 0, 33, :] = np.inf     # a whole +inf row
+            k[0, 5, 64, 0] = np.inf
+            k[0, 5, 64, 1] = -np.inf    # inf - inf: NaN score
+        cache.append_layer_major(s, [dev(k[0])], [dev(v[0])])
+        pool.append_layer_major(so, R(k), R(v))
+        seqs.append((s, so))
+    B = len(seqs)
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], hq, max_tokens=200)
+    batch.prepare()
+    q = rng.standard_normal((B, hq, D), dtype=np.float32)
+    tk = rng.standard_normal((B, H, D), dtype=np.float32)
+    tv = rng.standard_normal((B, H, D), dtype=np.float32)
+    out = torch.empty(B, hq, D, device=device)
+    batch.attention_layer(0, dev(q), dev(tk), dev(tv), out)
+    torch.cuda.synchronize()
+    kp, vp = pool.layer_pages(0)
+    hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+    tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+    for b, (_, so) in enumerate(seqs):
+        t = pool.block_table(so)
+        tables[b, : len(t)] = t
+    ref = oracle.batched_decode(q, kp, vp, tables, hist, R(tk), R(tv), threads=8)
+    got = host(out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+    batch.close()
