@@ -83,13 +83,15 @@ def run_steps(cache, seqs, hq, steps, seed, expect_shared=None):
                 out = torch.empty(B, hq, D, device="cuda:0")
                 batch.append_attention_layer(layer, dev(q), dev(tk), dev(tv), out)
                 torch.cuda.synchronize()
-                ref = oracle.batched_decode(q, kp, vp, tables, hist, tk, tv, threads=16)
+                rtk = workloads.round_rows(cache, tk, cache.k_scale)
+                rtv = workloads.round_rows(cache, tv, cache.v_scale)
+                ref = oracle.batched_decode(q, kp, vp, tables, hist, rtk, rtv, threads=16)
                 close(out, ref)
                 # The fused append wrote the token into its slot.
                 for b in (0, B - 1):
                     gk, gv = cache.retrieve_layer(seqs[b], layer)
-                    np.testing.assert_array_equal(gk[:, -1].cpu().numpy(), tk[b])
-                    np.testing.assert_array_equal(gv[:, -1].cpu().numpy(), tv[b])
+                    np.testing.assert_array_equal(gk[:, -1].cpu().numpy(), rtk[b])
+                    np.testing.assert_array_equal(gv[:, -1].cpu().numpy(), rtv[b])
                 del kp, vp
     finally:
         batch.close()
@@ -101,14 +103,19 @@ def test_config2_mha_full_size(device):
     cache.close()
 
 
-def test_config3_gqa_full_size(device):
-    cache, seqs, hq = workloads.config3(layers=1)
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16", "fp8"])
+def test_config3_gqa_full_size(device, page_dtype):
+    """fp32 pages, and the reduced-precision extensions (bf16, fp8 E4M3 at
+    scale 1): the oracle reads the pages' own values and the step rows
+    rounded onto the page grid."""
+    cache, seqs, hq = workloads.config3(layers=1, page_dtype=page_dtype)
     run_steps(cache, seqs, hq, steps=1, seed=30)
     cache.close()
 
 
-def test_config4_prefix_sharing_full_size(device):
-    cache, seqs, hq = workloads.config4(layers=1, steps=2)
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16", "fp8"])
+def test_config4_prefix_sharing_full_size(device, page_dtype):
+    cache, seqs, hq = workloads.config4(layers=1, steps=2, page_dtype=page_dtype)
     st = cache.stats()
     assert st["shared_blocks"] == 64
     run_steps(cache, seqs, hq, steps=2, seed=40, expect_shared=64)

@@ -69,13 +69,13 @@ def config2(layers=1, seed=2):
     return cache, seqs, 32
 
 
-def config3(layers=1, seed=3, batch=64):
+def config3(layers=1, seed=3, batch=64, page_dtype="f32"):
     """Llama-3-8B GQA: 64 sequences, 32/8 heads, contexts log-uniform in
     [512, 8192], shuffled pages."""
     rng = np.random.default_rng(seed)
     lengths = np.exp(rng.uniform(math.log(512), math.log(8192), size=batch)).astype(np.int64)
     need = int(((lengths + P) // P + 2).sum()) + 16
-    cache = shuffled_cache(layers, 8, need, seed)
+    cache = shuffled_cache(layers, 8, need, seed, page_dtype=page_dtype)
     gen = generator(seed)
     seqs = []
     for n in lengths:
@@ -85,7 +85,7 @@ def config3(layers=1, seed=3, batch=64):
     return cache, seqs, 32
 
 
-def config4(layers=1, seed=4, steps=2):
+def config4(layers=1, seed=4, steps=2, page_dtype="f32"):
     """Prefix sharing: 128 forks of a root of 1024 + 8 tokens (64 full pages
     shared at refcount 128, the 8-token partial page copied on write by
     every fork), then unique suffixes of U[64, 512] tokens; 32/8 heads."""
@@ -93,7 +93,8 @@ def config4(layers=1, seed=4, steps=2):
     batch, prefix, partial = 128, 1024, 8
     suffix = rng.integers(64, 513, size=batch)
     own = (partial + suffix + steps + P - 1) // P + 1
-    cache = shuffled_cache(layers, 8, int((prefix + partial) // P + 1 + own.sum() + 16), seed)
+    cache = shuffled_cache(layers, 8, int((prefix + partial) // P + 1 + own.sum() + 16), seed,
+                           page_dtype=page_dtype)
     gen = generator(seed)
     root = cache.create_sequence()
     fill(cache, root, prefix + partial, gen)
@@ -104,9 +105,35 @@ def config4(layers=1, seed=4, steps=2):
     return cache, seqs, 32
 
 
+def page_values(cache, pool, scale):
+    """fp32 values of a host copy of a raw pool: the pool itself for fp32
+    pages, bf16 bits widened, fp8 codes decoded times the cache's scale."""
+    import oracle
+    if cache.page_dtype == "bf16":
+        return (pool.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if cache.page_dtype == "fp8":
+        return oracle.fp8_decode(pool) * np.float32(scale)
+    return pool
+
+
+def round_rows(cache, rows, scale):
+    """Step rows (tail / chunk) on the cache's page grid."""
+    import oracle
+    if cache.page_dtype == "bf16":
+        return oracle.round_bf16(rows)
+    if cache.page_dtype == "fp8":
+        return oracle.round_fp8(rows, scale)
+    return rows
+
+
 def oracle_inputs(cache, seqs, layer):
-    """Host copies of one layer's pools and the batch's tables and lengths."""
-    kp, vp = (x.cpu().numpy() for x in cache.layer_pools(layer))
+    """Host copies of one layer's pools (as fp32 values) and the batch's
+    tables and lengths."""
+    kr, vr = cache.layer_pools(layer)
+    if cache.page_dtype == "bf16":
+        kr, vr = kr.view(torch.int16), vr.view(torch.int16)
+    kp = page_values(cache, kr.cpu().numpy(), cache.k_scale)
+    vp = page_values(cache, vr.cpu().numpy(), cache.v_scale)
     tabs = [cache.block_table(s) for s in seqs]
     tables = np.zeros((len(seqs), max(len(t) for t in tabs) + 1), np.uint32)
     for b, t in enumerate(tabs):
