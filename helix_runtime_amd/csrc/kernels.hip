@@ -905,6 +905,10 @@ struct PageDesc {
 // global store after the last load.  A full stage is flushed early (many
 // short units per wavefront).
 constexpr int kStreamStage = 4;
+// fp8 stream wavefronts: four per SIMD with a one-deep result stage (the
+// extra wavefront hides more per-page latency than its spills cost).
+constexpr int kFp8StreamWaves = 4;
+constexpr int kFp8StreamStage = 1;
 
 
 // One token row's 4 dims of a page buffer as fp32: fp32 pages as loaded,
@@ -970,9 +974,10 @@ __device__ __forceinline__ StreamLds<G> stream_lds(StreamShared<G>& s) {
 }
 
 // fp8 pages in the stream kernel: query rows through LDS (not in a
-// register copy per page buffer), two results staged, three wavefronts per
-// SIMD, which their small page buffers then allow (137-150 VGPRs).  Config
-// 3, one box: 116.5 against 140.4 us per layer with two wavefronts.  bf16
+// register copy per page buffer), one result staged, four wavefronts per
+// SIMD, which their small page buffers then allow (128 VGPRs, 6-14 spilled).
+// Config 3, one box: 110.7 us per layer against 116.3 with three wavefronts
+// and two staged results (137-150 VGPRs, no spills) and 140.4 with two.  bf16
 // pages stay at two: with the same change and the probabilities read from
 // LDS where used (167 VGPRs, no spills) they ran 129.8 against 125.8 us
 // (145 us with spills when the probabilities stayed in registers).
@@ -1585,14 +1590,14 @@ __device__ __forceinline__ void decode_stream_body(
 
 template <int G, bool APPEND, int PF, bool SINGLE = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
-    G > 4 ? 1 : (stream_lds_query<PF, G>() ? 3 : 2))))
+    G > 4 ? 1 : (stream_lds_query<PF, G>() ? kFp8StreamWaves : 2))))
 void decode_stream_kernel(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ segments,
     const std::int64_t* __restrict__ append_slots) {
   constexpr bool QLDS = stream_lds_query<PF, G>();
-  constexpr int S = QLDS ? 2 : kStreamStage;
+  constexpr int S = QLDS ? kFp8StreamStage : kStreamStage;
   __shared__ __align__(16) float s_p[2][8 * G];
   __shared__ __align__(16) float s_head[3][G];
   __shared__ __align__(16) float4 s_res_o[S][G][32];
@@ -2145,7 +2150,7 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix,
     cus[dev] = n;
   }
   const std::size_t per_simd =
-      group >= 8 || beside_prefix ? 1 : (stream_lds_query_type(type) ? 3 : 2);
+      group >= 8 || beside_prefix ? 1 : (stream_lds_query_type(type) ? kFp8StreamWaves : 2);
   const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
   return w < kMaxStreamWaves ? w : kMaxStreamWaves;
 }
