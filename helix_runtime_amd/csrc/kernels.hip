@@ -1036,11 +1036,11 @@ __device__ __forceinline__ void decode_stream_body(
   constexpr int NV = 8 * G;
   constexpr int kStage = S;
   constexpr bool QLDS = !SHARED_BLOCK && stream_lds_query<PF, G>();
-  // bf16 and fp8 pages, and stream wavefronts beside prefix workgroups: the
-  // raw exp2 and a ballot for the rescale test (measured: config 3 bf16
-  // 130.7 -> 125.4 us, fp8 110.7 -> 108.4 us per layer, config 4 fused
-  // cascade 79.9 -> 79.3 us; the plain fp32 stream kernel, bound by HBM,
-  // showed no gain and keeps exp2f).
+  // fp8 and bf16 pages, and stream wavefronts beside prefix workgroups: the
+  // raw exp2 and a ballot for the rescale test (measured: config 3 fp8
+  // 110.7 -> 108.4 us per layer, config 4 fused cascade 79.9 -> 79.3 us;
+  // bf16 within its box-to-box spread; the plain fp32 stream kernel, bound
+  // by HBM, showed no gain and keeps exp2f).
   constexpr bool LEAN = PF != 0 || SHARED_BLOCK;
   auto& s_p = sh.p;
   auto& s_head = sh.head;
