@@ -255,6 +255,8 @@ class PagedKvCache:
         cfg = _cfg(layers, kv_heads, head_dimension, block_tokens, physical_blocks)
         if page_dtype not in PAGE_DTYPES:
             raise HelixError(INVALID_ARGUMENT, f"page_dtype must be one of {sorted(PAGE_DTYPES)}")
+        if page_dtype != "fp8" and (k_scale != 1.0 or v_scale != 1.0):
+            raise HelixError(INVALID_ARGUMENT, "k_scale and v_scale apply to fp8 pages only")
         if page_dtype == "fp8":
             check(_lib().helix_paged_cache_create_fp8(ctypes.byref(cfg), device, float(k_scale),
                                                       float(v_scale), ctypes.byref(h)))

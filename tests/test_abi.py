@@ -82,3 +82,45 @@ def test_batched_entry_points_reject_other_geometries_before_launch():
                                                block_tokens, None, 8, None, None, None, None,
                                                None)
         assert rc == hx.UNSUPPORTED
+
+
+def test_cache_creation_rejects_bad_page_formats_before_any_allocation():
+    """helix_paged_cache_create_fp8 refuses zero, negative and non-finite
+    scales and helix_paged_cache_create_typed an unknown element type with
+    HELIX_INVALID_ARGUMENT, leaving *out NULL; both checks run before the
+    device is touched (no GPU here)."""
+    lib = hx.load()
+    cfg = _native.Config(layers=2, kv_heads=8, head_dimension=128, block_tokens=16,
+                         physical_blocks=64)
+    out = ctypes.c_void_p(12345)
+    for ks, vs in ((0.0, 1.0), (1.0, -2.0), (float("inf"), 1.0), (1.0, float("nan")),
+                   (-0.0, 1.0)):
+        rc = lib.helix_paged_cache_create_fp8(ctypes.byref(cfg), 0, ks, vs, ctypes.byref(out))
+        assert rc == hx.INVALID_ARGUMENT, (ks, vs)
+        assert out.value is None
+        assert b"fp8 page scales must be finite and positive" in lib.helix_last_error()
+        out = ctypes.c_void_p(12345)
+    for dtype in (-1, 3, 4):
+        rc = lib.helix_paged_cache_create_typed(ctypes.byref(cfg), 0, dtype, ctypes.byref(out))
+        assert rc == hx.INVALID_ARGUMENT, dtype
+        assert out.value is None
+        assert b"page dtype must be" in lib.helix_last_error()
+        out = ctypes.c_void_p(12345)
+    rc = lib.helix_paged_cache_create_fp8(ctypes.byref(cfg), 0, 1.0, 1.0, None)
+    assert rc == hx.INVALID_ARGUMENT
+
+
+def test_python_cache_rejects_bad_page_formats_before_any_allocation():
+    """The Python PagedKvCache refuses an unknown page type, scales on a
+    page type without them, and bad fp8 scales (the C check) with
+    INVALID_ARGUMENT before the device is touched."""
+    import pytest
+    geometry = dict(layers=2, kv_heads=8, head_dimension=128, block_tokens=16,
+                    physical_blocks=64)
+    cases = (dict(page_dtype="fp4"), dict(page_dtype="bf16", k_scale=2.0),
+             dict(page_dtype="f32", v_scale=0.5), dict(page_dtype="fp8", k_scale=0.0),
+             dict(page_dtype="fp8", v_scale=float("inf")))
+    for kw in cases:
+        with pytest.raises(hx.HelixError) as e:
+            hx.PagedKvCache(**geometry, **kw)
+        assert e.value.status == hx.INVALID_ARGUMENT, kw
