@@ -982,14 +982,15 @@ __device__ __forceinline__ StreamLds<G> stream_lds(StreamShared<G>& s) {
                       s.seg, s.seg_unit, s.app_k, s.app_v, s.app_dst, nullptr};
 }
 
-// fp8 pages in the stream kernel: query rows through LDS (not in a
-// register copy per page buffer), one result staged, four wavefronts per
-// SIMD, which their small page buffers then allow (128 VGPRs, 6-14 spilled).
-// Config 3, one box: 110.7 us per layer against 116.3 with three wavefronts
-// and two staged results (137-150 VGPRs, no spills) and 140.4 with two.  bf16
-// pages stay at two: with the same change and the probabilities read from
-// LDS where used (167 VGPRs, no spills) they ran 129.8 against 125.8 us
-// (145 us with spills when the probabilities stayed in registers).
+// fp8 pages in the stream kernel: query rows loaded straight into LDS (one
+// area per live unit) and read from there at every page, with no register
+// copy; one result staged; four wavefronts per SIMD, which their small page
+// buffers then allow (119-127 VGPRs, at most 2 spilled).  Config 3, one
+// box: 104.0 us per layer against 108.5 with a register copy per unit
+// (6-13 spilled), 116.3 with three wavefronts and two staged results and
+// 140.4 with two wavefronts.  bf16 pages stay at two wavefronts: with the
+// same arrangement three ran 128.4-128.8 against 125.4 us (161 VGPRs, no
+// spills) and four 161.6 us (21-27 spilled).
 constexpr bool stream_lds_query_type(PageType t) { return t == PageType::kFP8; }
 template <int PF, int G>
 constexpr bool stream_lds_query() {
@@ -1180,7 +1181,15 @@ __device__ __forceinline__ void decode_stream_body(
   const int lane_off = lane * (FP8 ? 4 : BF16 ? 8 : 16);
   const int row_off = j * 16;
   using Raw = std::conditional_t<FP8, unsigned, std::conditional_t<BF16, uint2, float4>>;
-  // slot: the buffer's LDS query area (query rows through LDS), else unused.
+  // Query rows through LDS: a unit's rows go to area (kvh * batch + b) % 3.
+  // Units are visited in that flat order and every unit has a page (its
+  // tail), so with two pages in flight the three units that can be live at
+  // once (one being processed, up to two loading) have distinct areas.
+  auto query_area = [&](const PageDesc& d) {
+    return static_cast<int>(
+        static_cast<unsigned>(__builtin_amdgcn_readfirstlane(d.kvh * a.batch + d.b)) % 3u);
+  };
+  // slot: the page buffer (0 or 1).
   auto load_page = [&](const PageDesc& d, Raw (&k)[8], Raw (&v)[8], float4 (&q)[G], bool& bad,
                        int slot) {
     const int b = __builtin_amdgcn_readfirstlane(d.b);
@@ -1223,7 +1232,7 @@ __device__ __forceinline__ void decode_stream_body(
         for (int i = 0; i < (G * 32 + 63) / 64; ++i) {
           if (i * 64 + lane < G * 32) {
             prefill_detail::lds_load16(qsrc + (i * 64 + lane) * 4,
-                                       prefill_detail::lds_address(&sh.qslot[slot][0][0]) +
+                                       prefill_detail::lds_address(&sh.qslot[query_area(d)][0][0]) +
                                            i * 1024);
           }
         }
@@ -1497,18 +1506,10 @@ __device__ __forceinline__ void decode_stream_body(
     if (!d.skip) {
       valid = d.p == d.np - 1 ? 1 : min(P, d.hist - (d.p + a.first_page) * P);
       unit_bad = unit_bad || bad;
-      if (d.p == 0 || d.g == g0) {
+      if constexpr (!QLDS) {
+        if (d.p == 0 || d.g == g0) {
 #pragma unroll
-        for (int h = 0; h < G; ++h) qc[h] = qn[h];
-        if constexpr (QLDS) {
-          // Read the LDS area only once its direct loads have landed: the
-          // index depends (through an empty asm) on the page's first key
-          // word, so the read waits for that load, which was issued after
-          // the query loads.
-          int dep = 0;
-          asm volatile("" : "+v"(dep) : "v"(first_word(k[0])));
-#pragma unroll
-          for (int h = 0; h < G; ++h) qc[h] = sh.qslot[slot][h][j + dep];
+          for (int h = 0; h < G; ++h) qc[h] = qn[h];
         }
       }
       if (d.p == 0) {
@@ -1539,7 +1540,21 @@ __device__ __forceinline__ void decode_stream_body(
         stream_sync<SHARED_BLOCK>();
       }
     }
-    process(k, v, qc, valid);
+    if constexpr (QLDS) {
+      // The query rows are read from the unit's LDS area at every page, so
+      // no register copy lives across the unit's pages.  The index depends
+      // (through an empty asm) on the page's first key word, so the read
+      // waits for that load, which was issued after the unit's query loads.
+      int dep = 0;
+      asm volatile("" : "+v"(dep) : "v"(first_word(k[0])));
+      float4 qv[G];
+      const int qa = query_area(d);
+#pragma unroll
+      for (int h = 0; h < G; ++h) qv[h] = sh.qslot[qa][h][j + dep];
+      process(k, v, qv, valid);
+    } else {
+      process(k, v, qc, valid);
+    }
     if (!d.skip && (d.p == d.np - 1 || d.g == g1 - 1)) finalize(d);
   };
   auto step = [&](const PageDesc& d, Raw (&kr)[8], Raw (&vr)[8], const float4 (&qn)[G], bool bad,
@@ -1631,7 +1646,7 @@ void decode_stream_kernel(
   __shared__ __align__(16) float4 s_app_k[S][32];
   __shared__ __align__(16) float4 s_app_v[S][32];
   __shared__ long long s_app_dst[S];
-  __shared__ __align__(16) float4 s_qslot[QLDS ? 2 : 1][G][32];
+  __shared__ __align__(16) float4 s_qslot[QLDS ? 3 : 1][G][32];
   decode_stream_body<G, APPEND, PF, false, SINGLE, S>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
       StreamLds<G, S>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k,
