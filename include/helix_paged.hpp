@@ -614,6 +614,9 @@ class HipPagedKvCache final {
       : impl_(std::make_shared<Impl>()) {
     detail::require(device_index >= 0, ErrorCode::kInvalidArgument,
                     "HipPagedKvCache: device index must be non-negative");
+    detail::require(pages == PageDType::kFp8E4M3 || (scales.key == 1.0F && scales.value == 1.0F),
+                    ErrorCode::kInvalidArgument,
+                    "HipPagedKvCache: fp8 scales apply to fp8 pages only");
     const helix_paged_config c{config.layers, config.kv_heads, config.head_dimension,
                                config.block_tokens, config.physical_blocks};
     if (pages == PageDType::kFp8E4M3) {

@@ -177,6 +177,24 @@ TEST_F(HostContractTest, InvalidArgumentsFailBeforeDeviceWork) {
        ErrorCode::kInvalidArgument},
       {"negative device index", [] { HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, -1); },
        ErrorCode::kInvalidArgument},
+      {"fp8 scales on bf16 pages",
+       [] {
+         HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, 0, PageDType::kBFloat16,
+                           Fp8Scales{2.0F, 1.0F});
+       },
+       ErrorCode::kInvalidArgument},
+      {"zero fp8 key scale",
+       [] {
+         HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, 0, PageDType::kFp8E4M3,
+                           Fp8Scales{0.0F, 1.0F});
+       },
+       ErrorCode::kInvalidArgument},
+      {"infinite fp8 value scale",
+       [] {
+         HipPagedKvCache c(PagedKvCacheConfig{1, 1, 1, 1, 1}, 0, PageDType::kFp8E4M3,
+                           Fp8Scales{1.0F, std::numeric_limits<float>::infinity()});
+       },
+       ErrorCode::kInvalidArgument},
       {"reshape changing the count",
        [] { static_cast<void>(Tensor::zeros({2, 3}).reshape({4, 2})); },
        ErrorCode::kInvalidArgument},
