@@ -982,8 +982,8 @@ __device__ __forceinline__ StreamLds<G> stream_lds(StreamShared<G>& s) {
                       s.seg, s.seg_unit, s.app_k, s.app_v, s.app_dst, nullptr};
 }
 
-// fp8 pages in the stream kernel: query rows loaded straight into LDS (one
-// area per live unit) and read from there at every page, with no register
+// fp8 pages in the stream kernel: query rows loaded straight into LDS (three
+// areas used by units in turn) and read from there at every page, with no register
 // copy; one result staged; four wavefronts per SIMD, which their small page
 // buffers then allow (119-127 VGPRs, at most 2 spilled).  Config 3, one
 // box: 104.0 us per layer against 108.5 with a register copy per unit
@@ -1182,9 +1182,12 @@ __device__ __forceinline__ void decode_stream_body(
   const int row_off = j * 16;
   using Raw = std::conditional_t<FP8, unsigned, std::conditional_t<BF16, uint2, float4>>;
   // Query rows through LDS: a unit's rows go to area (kvh * batch + b) % 3.
-  // Units are visited in that flat order and every unit has a page (its
-  // tail), so with two pages in flight the three units that can be live at
-  // once (one being processed, up to two loading) have distinct areas.
+  // Units are visited in that flat order, every unit has a page (its
+  // tail) and loads run two pages ahead, so the unit that reuses an area
+  // (three units later) starts loading at least one page after the last
+  // read of the area's previous rows.  (Two areas would already reload an
+  // area only after its last read in program order; the third adds a page
+  // of margin.)
   auto query_area = [&](const PageDesc& d) {
     return static_cast<int>(
         static_cast<unsigned>(__builtin_amdgcn_readfirstlane(d.kvh * a.batch + d.b)) % 3u);

@@ -228,6 +228,49 @@ def test_decode_steps_match_oracle_on_rounded_values(device, hq, fused):
     batch.close()
 
 
+@pytest.mark.parametrize("hq", [8, 32])
+def test_decode_over_many_short_units_matches_oracle(device, hq):
+    """1024 sequences of 0-40 tokens (a quarter of them empty, so their
+    unit is the tail alone): each stream wavefront runs through several
+    one- and two-page units in a row, so the query rows of up to three units
+    are in LDS at once (one being attended, two loading) and every area is
+    reused many times (about 16 K pages over the 4096 fp8 stream wavefronts
+    of a 256-CU GPU: four pages each)."""
+    L, H, B = 1, 8, 1024
+    rng = np.random.default_rng(29 + hq)
+    lengths = rng.integers(0, 41, size=B)
+    lengths[rng.random(B) < 0.25] = 0
+    N = int(sum((n + P - 1) // P + 1 for n in lengths)) + 8
+    cache = fp8_cache(L, H, N)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for n in lengths:
+        s, so = cache.create_sequence(), pool.create_sequence()
+        if n:
+            k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            cache.append_layer_major(s, [dev(k[0])], [dev(v[0])])
+            pool.append_layer_major(so, RK(k), RV(v))
+        seqs.append((s, so))
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], hq, max_tokens=64)
+    batch.prepare()
+    hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+    tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+    for b, (_, so) in enumerate(seqs):
+        t = pool.block_table(so)
+        tables[b, : len(t)] = t
+    keys = rng.standard_normal((B, H, D), dtype=np.float32)
+    values = rng.standard_normal((B, H, D), dtype=np.float32)
+    q = rng.standard_normal((B, hq, D), dtype=np.float32)
+    out = torch.empty(B, hq, D, device=device)
+    batch.attention_layer(0, dev(q), dev(keys), dev(values), out)
+    torch.cuda.synchronize()
+    kp, vp = pool.layer_pages(0)
+    ref = oracle.batched_decode(q, kp, vp, tables, hist, RK(keys), RV(values), threads=8)
+    np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+    batch.close()
+
+
 @pytest.mark.parametrize("hq", [16, 32])
 def test_cascade_decode_on_fp8_pages(device, hq):
     """Forks of one prompt share its pages; the decode step attends them once
