@@ -471,3 +471,75 @@ def test_step_calls_on_other_streams(device):
         for b, (_, so) in enumerate(seqs):
             pool.append(so, keys[:, b], values[:, b])
     batch.close()
+
+
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hq", [8, 32])
+def test_decode_over_many_short_sequences(device, hq, page_dtype):
+    """1024 sequences of 0-40 tokens (a quarter empty: their unit is the
+    tail alone).  Past 256 sequences the stream kernel finds each
+    wavefront's first unit by scanning the lengths chunk by chunk beyond its
+    preloaded four, and each wavefront runs through several short units."""
+    L, H, B = 1, 8, 1024
+    rnd = (lambda x: x) if page_dtype == "f32" else oracle.round_bf16
+    rng = np.random.default_rng(31 + hq)
+    lengths = rng.integers(0, 41, size=B)
+    lengths[rng.random(B) < 0.25] = 0
+    N = int(sum((n + P - 1) // P + 1 for n in lengths)) + 8
+    cache = hx.PagedKvCache(L, H, D, P, N, page_dtype=page_dtype)
+    pool = oracle.PagedPool(L, H, D, P, N)
+    seqs = []
+    for n in lengths:
+        s, so = cache.create_sequence(), pool.create_sequence()
+        if n:
+            k = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            v = rng.standard_normal((L, H, n, D), dtype=np.float32)
+            cache.append_layer_major(s, [dev(k[0])], [dev(v[0])])
+            pool.append_layer_major(so, rnd(k), rnd(v))
+        seqs.append((s, so))
+    batch = hx.DecodeBatch(cache, [s for s, _ in seqs], hq, max_tokens=64)
+    batch.prepare()
+    hist = np.array([pool.length(so) for _, so in seqs], np.int32)
+    tables = np.zeros((B, batch.device_state()["max_blocks"]), np.uint32)
+    for b, (_, so) in enumerate(seqs):
+        t = pool.block_table(so)
+        tables[b, : len(t)] = t
+    keys = rng.standard_normal((B, H, D), dtype=np.float32)
+    values = rng.standard_normal((B, H, D), dtype=np.float32)
+    q = rng.standard_normal((B, hq, D), dtype=np.float32)
+    out = torch.empty(B, hq, D, device=device)
+    batch.attention_layer(0, dev(q), dev(keys), dev(values), out)
+    torch.cuda.synchronize()
+    kp, vp = pool.layer_pages(0)
+    ref = oracle.batched_decode(q, kp, vp, tables, hist, rnd(keys), rnd(values), threads=8)
+    np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
+    batch.close()
+
+
+def test_stateless_decode_of_1000_sequences(device):
+    """The batched C-ABI entry (caller workspace) at 1000 sequences, not a
+    multiple of the 64-sequence scan chunk, with ragged contexts."""
+    rng = np.random.default_rng(41)
+    B, hkv, hq = 1000, 8, 32
+    lengths = rng.integers(0, 300, size=B).astype(np.int32)
+    pages = (lengths + P - 1) // P
+    phys = int(pages.sum()) + 4
+    perm = rng.permutation(phys).astype(np.uint32)
+    max_blocks = int(pages.max()) + 1
+    tables = np.zeros((B, max_blocks), np.uint32)
+    at = 0
+    for b, n in enumerate(pages):
+        tables[b, :n] = perm[at: at + n]
+        at += n
+    kp = rng.standard_normal((phys, hkv, P, D), dtype=np.float32)
+    vp = rng.standard_normal((phys, hkv, P, D), dtype=np.float32)
+    q = rng.standard_normal((B, hq, D), dtype=np.float32)
+    tk = rng.standard_normal((B, hkv, D), dtype=np.float32)
+    tv = rng.standard_normal((B, hkv, D), dtype=np.float32)
+    out = torch.empty(B, hq, D, device=device)
+    ws = hx.decode_workspace(B, hq, hkv, max_blocks)
+    hx.paged_decode_attention(dev(q), dev(kp), dev(vp), dev(tables.view(np.int32)), dev(lengths),
+                              dev(tk), dev(tv), out, ws)
+    torch.cuda.synchronize()
+    ref = oracle.batched_decode(q, kp, vp, tables, lengths, tk, tv, threads=8)
+    np.testing.assert_allclose(host(out), ref, atol=ATOL, rtol=RTOL)
