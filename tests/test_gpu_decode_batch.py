@@ -230,7 +230,7 @@ def test_prefix_sharing_decode_with_cow_forks(device):
 
 
 @pytest.mark.parametrize("mode", ["separate", "fused", "commit"])
-@pytest.mark.parametrize("hq", [8, 32])
+@pytest.mark.parametrize("hq", [4, 8, 32])
 def test_cascade_shared_prefix_decode(device, hq, mode):
     """Sequences forked from one root share its full leading pages; the decode
     step attends them once for the batch (cascade) and the per-sequence rest
