@@ -12,6 +12,7 @@
 #include "fp8.hpp"
 #include "prefill_body.hpp"
 
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -2171,28 +2172,28 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 namespace {
 
 // Wavefronts the stream kernel launches: every resident slot of the device
-// (two per SIMD up to four query heads per kv head, one for eight, as the
-// kernels' register use allows), at most kMaxStreamWaves.  beside_prefix:
-// one per SIMD whatever the group, so the concurrent cascade prefix pass
-// finds registers on every SIMD.  fp8 pages at three per SIMD (the register
-// cap of 168 spills at four query heads) measured slower: 181 against
-// 140 us per config-3 layer.
+// (fp32 and bf16 pages: two per SIMD up to four query heads per kv head, one
+// for eight; fp8 pages: four per SIMD up to four query heads, as the
+// kernels' register and LDS use allows), at most kMaxStreamWaves.
+// beside_prefix: one per SIMD whatever the group, so the concurrent cascade
+// prefix pass finds registers on every SIMD.
 std::size_t stream_waves(std::size_t group, bool beside_prefix,
                          PageType type = PageType::kF32) {
-  static int cus[64] = {0};
+  // CU count per device, looked up once; host threads may launch at once.
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0) {
       n = 256;
     }
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
   const std::size_t per_simd =
       group >= 8 || beside_prefix ? 1 : (stream_lds_query_type(type) ? kFp8StreamWaves : 2);
-  const std::size_t w = static_cast<std::size_t>(cus[dev]) * 4 * per_simd;
+  const std::size_t w = static_cast<std::size_t>(n) * 4 * per_simd;
   return w < kMaxStreamWaves ? w : kMaxStreamWaves;
 }
 
