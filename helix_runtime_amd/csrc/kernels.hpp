@@ -242,6 +242,11 @@ struct PrefillArgs {
   // bf16 / fp8 pages: history keys/values are widened and the chunk rows
   // rounded onto the page grid (the values their pages hold once appended).
   PageFormat page_type;
+  // bf16 / fp8 pages: one word per launched work item.  Given, the launch
+  // runs on the bf16 matrix cores and redoes exactly the items that met a
+  // special value (a NaN score, a non-finite value row that some row
+  // masks); the words are written by the launch itself.
+  std::uint32_t* redo = nullptr;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of

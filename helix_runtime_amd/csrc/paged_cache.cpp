@@ -449,7 +449,8 @@ const std::int64_t* DecodeBatch::slots() const {
 // [B, tokens] int64, up to B * max_blocks table updates of 3 words (a step
 // uploads the entries a member gained since the previous step, inside or
 // outside the batch), and for chunks the prefill work-item order, in one
-// device buffer and two pinned staging copies.
+// device buffer and two pinned staging copies; after them, device only, one
+// redo word per prefill work item (written by the bf16 / fp8 prefill).
 std::size_t DecodeBatch::order_offset(std::size_t tokens) const {
   const std::size_t B = batch();
   const std::size_t max_updates = B * max_blocks_;
@@ -464,7 +465,8 @@ std::size_t DecodeBatch::prefill_items(std::size_t tokens) const {
 
 void DecodeBatch::reserve_step(std::size_t tokens) {
   if (tokens <= step_capacity_) return;
-  const std::size_t bytes = order_offset(tokens) + prefill_items(tokens) * sizeof(std::uint32_t);
+  const std::size_t bytes =
+      order_offset(tokens) + 2 * prefill_items(tokens) * sizeof(std::uint32_t);
   for (hipEvent_t e : uploaded_) hip_check(hipEventSynchronize(e), "decode batch staging wait");
   DeviceGuard guard(state_->device);
   // The device buffer may still be read by queued kernels of earlier steps.
@@ -760,6 +762,9 @@ void DecodeBatch::prefill_layer(std::size_t layer, const float* query, const flo
     a.order = reinterpret_cast<const std::uint32_t*>(
         static_cast<const unsigned char*>(step_.data()) + order_offset(step_tokens_));
   }
+  a.redo = reinterpret_cast<std::uint32_t*>(
+      static_cast<unsigned char*>(step_.data()) + order_offset(step_tokens_) +
+      prefill_items(step_tokens_) * sizeof(std::uint32_t));
   DeviceGuard guard(state_->device);
   begin_call(stream, "decode batch prefill");
   hip_check(hip::launch_prefill(a, stream), "decode batch prefill launch");

@@ -2,6 +2,7 @@
 // standalone kernel and its launches.  The workgroup code, its design notes
 // and the special-value rules are in prefill_body.hpp.
 #include "prefill_body.hpp"
+#include "prefill_bmma.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -18,6 +19,44 @@ void prefill_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ table
                     const std::uint32_t* __restrict__ order) {
   __shared__ PrefillShared sh;
   prefill_body<G, CASCADE, PF, RT>(a, tables, order, blockIdx.x, sh);
+}
+
+// The exact kernel over the blocks the matrix-core launch flagged (every
+// other block returns at once).
+template <int G, int PF, int RT>
+__global__ __launch_bounds__(512 / RT, 6 - 2 * RT)
+void prefill_redo_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ tables,
+                         const std::uint32_t* __restrict__ order,
+                         const std::uint32_t* __restrict__ redo) {
+  if (redo[blockIdx.x] == 0) return;
+  __shared__ PrefillShared sh;
+  prefill_body<G, false, PF, RT>(a, tables, order, blockIdx.x, sh);
+}
+
+// Tiles per wavefront of the bf16 matrix-core prefill: one (8 wavefronts
+// of 16 rows) keeps the three-term query operand and the accumulators of a
+// wavefront within 128 VGPRs, four wavefronts per SIMD.
+constexpr int kBmmaTilesPerWave = 1;
+
+template <int G, int PF, int RT>
+__global__ __launch_bounds__(512 / RT, 6 - 2 * RT)
+void prefill_bmma_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ tables,
+                         const std::uint32_t* __restrict__ order,
+                         std::uint32_t* __restrict__ redo) {
+  __shared__ PrefillBmmaShared sh;
+  prefill_body_bmma<G, PF, RT>(a, tables, order, redo, blockIdx.x, sh);
+}
+
+// bf16 / fp8 pages with a redo array: the bf16 matrix-core kernel, then the
+// exact kernel over the work items it flagged.
+template <int G, int PF>
+void launch_bmma(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
+                 const std::uint32_t* tables, const std::uint32_t* order,
+                 std::uint32_t* redo) {
+  constexpr int BRT = kBmmaTilesPerWave;
+  prefill_bmma_kernel<G, PF, BRT><<<grid, 512 / BRT, 0, stream>>>(k, tables, order, redo);
+  prefill_redo_kernel<G, PF, kTilesPerWave><<<grid, 512 / kTilesPerWave, 0, stream>>>(
+      k, tables, order, redo);
 }
 
 template <int G, bool CASCADE, int RT = kTilesPerWave>
@@ -89,6 +128,21 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.k_scale = a.page_type.k_scale;
   k.v_scale = a.page_type.v_scale;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
+  if (a.redo != nullptr && a.page_type.type != PageType::kF32) {
+    const bool fp8 = a.page_type.type == PageType::kFP8;
+    switch (group) {
+      case 1: fp8 ? launch_bmma<1, 2>(grid, stream, k, a.tables, a.order, a.redo)
+                  : launch_bmma<1, 1>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 2: fp8 ? launch_bmma<2, 2>(grid, stream, k, a.tables, a.order, a.redo)
+                  : launch_bmma<2, 1>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 4: fp8 ? launch_bmma<4, 2>(grid, stream, k, a.tables, a.order, a.redo)
+                  : launch_bmma<4, 1>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 8: fp8 ? launch_bmma<8, 2>(grid, stream, k, a.tables, a.order, a.redo)
+                  : launch_bmma<8, 1>(grid, stream, k, a.tables, a.order, a.redo); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   switch (group) {
     case 1: launch_variant<1, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;
     case 2: launch_variant<2, false>(grid, stream, k, a.tables, a.order, a.page_type.type); break;

@@ -1,0 +1,385 @@
+// Chunked-prefill attention for bf16 and fp8 pages on the bf16 matrix cores.
+//
+// The decomposition, masks, online softmax and special-value rules are those
+// of prefill_body (one workgroup of 4 wavefronts per (sequence, kv head) and
+// 128 query rows, two 16-row tiles per wavefront, scores computed transposed
+// so each lane holds 4 keys of one query row).  What differs is the matrix
+// arithmetic.  A bf16 page element is exact in bf16, and so is the bare code
+// value of an fp8 element (the key scale joins the score scale and the value
+// scale multiplies the output, as in the decode kernel).  The fp32 operand
+// of each product (the scaled query, the probabilities) is split by
+// truncation into three bf16 terms, hi + mid + lo, which hold its 24
+// significant bits exactly.  Every product term is then exact in fp32, and
+// three v_mfma_f32_16x16x32_bf16 (scores) or v_mfma_f32_16x16x16_bf16 (P.V)
+// replace the fp32 instructions at about five times the matrix throughput;
+// only the order of the fp32 accumulation differs from the fp32 kernel.
+//
+// Special values.  A non-finite operand keeps only its hi term.  The split
+// can only go wrong by giving NaN (a zero query term times an infinite key,
+// where the fp32 product is inf), and a value row that some row masks must
+// not reach that row (0 * inf).  Exact paths for these cases would cost the
+// kernel its occupancy (they need registers the hot loop cannot spare), so
+// a work item that meets a NaN score or such a value row is flagged in
+// redo[block] instead; the launcher then runs prefill_body, which handles
+// both exactly, over the flagged items only.
+//
+// LDS: K rows as bf16, padded to kBKStride elements (16 bytes) so the 16
+// rows one operand read touches start in distinct banks; V transposed,
+// [dim][key] with rows of kVtStride keys, so one 8-byte read gives a lane the
+// 4 keys of one dim that the P.V operand needs.
+#pragma once
+
+#include "prefill_body.hpp"
+
+namespace helix::hip::prefill_detail {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+constexpr int kBKStride = D + 8;  // bf16 elements per K row in LDS
+constexpr int kVtStride = 20;     // bf16 elements per transposed V row (16 keys + pad)
+
+struct PrefillBmmaShared {
+  __align__(16) unsigned short k[2][kKeys * kBKStride];
+  __align__(16) unsigned short vt[2][D * kVtStride];
+};
+
+// x = hi + mid + lo exactly (truncating splits of a finite fp32); a
+// non-finite x is hi alone.  Results are bf16 bit patterns.
+__device__ __forceinline__ void split3(float x, short& hi, short& mid, short& lo) {
+  const unsigned u = __float_as_uint(x);
+  hi = static_cast<short>(u >> 16);
+  if (!isfinite(x)) {
+    mid = 0;
+    lo = 0;
+    return;
+  }
+  const float r1 = x - __uint_as_float(u & 0xffff0000u);
+  const unsigned u1 = __float_as_uint(r1);
+  mid = static_cast<short>(u1 >> 16);
+  const float r2 = r1 - __uint_as_float(u1 & 0xffff0000u);
+  lo = static_cast<short>(__float_as_uint(r2) >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_value(unsigned short h) {
+  return __uint_as_float(static_cast<unsigned>(h) << 16);
+}
+
+// PF: 1 bf16 pages, 2 fp8 pages.  Standalone prefill only (no cascade).
+// RT: 16-row tiles per wavefront; the workgroup has 8 / RT wavefronts.
+// redo[block] is written for every block: 1 when the item must be redone
+// exactly.
+template <int G, int PF, int RT>
+__device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
+                                                  const std::uint32_t* __restrict__ tables,
+                                                  const std::uint32_t* __restrict__ order,
+                                                  std::uint32_t* __restrict__ redo,
+                                                  std::uint32_t block, PrefillBmmaShared& sh) {
+  static_assert(PF == 1 || PF == 2, "bf16 matrix-core prefill is for bf16 and fp8 pages");
+  constexpr int RP = 16 / RT;  // key rows per staging pass
+  constexpr int PW = kRows / G;
+  constexpr bool FP8 = PF == 2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+
+  std::uint32_t item = block;
+  if (order != nullptr) {
+    item = order[block];
+  } else {
+    const std::uint32_t x = item % a.pos_blocks;
+    item = item - x + (a.pos_blocks - 1 - x);
+  }
+  const int pb = static_cast<int>(item % a.pos_blocks);
+  const int kvh = static_cast<int>((item / a.pos_blocks) % a.kv_heads);
+  const int b = static_cast<int>(item / a.pos_blocks / a.kv_heads);
+  const int T = a.tokens;
+  const int pos0 = pb * PW;
+
+  int hist = a.lengths[b];
+  bool bad = hist < 0 || hist > a.max_blocks * P;
+  if (bad) hist = 0;
+  const int key_end = hist + min(T, pos0 + PW);
+  const std::uint32_t* __restrict__ table = tables + static_cast<std::size_t>(b) * a.max_blocks;
+  const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
+  // fp8: keys are bare code values, their scale joins the score scale.
+  const float qs = FP8 ? a.qscale * a.k_scale : a.qscale;
+
+  // Query operand: tile t, step s covers dims 32 s + 8 grp .. + 7 of row
+  // t * 16 + col (B operand of S^T = K Q^T), as three bf16 terms.
+  int qpos[RT];
+  std::size_t qrow[RT];
+  v8s qv[RT][3][4];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int r = wave * (16 * RT) + t * 16 + col;
+    const int head = kvh * G + r / PW;
+    qpos[t] = pos0 + r % PW;
+    const bool valid = qpos[t] < T;
+    qrow[t] = ((static_cast<std::size_t>(b) * a.q_heads + head) * T + qpos[t]) * D;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+      if (valid) {
+        x0 = *reinterpret_cast<const float4*>(a.query + qrow[t] + 32 * s + 8 * grp);
+        x1 = *reinterpret_cast<const float4*>(a.query + qrow[t] + 32 * s + 8 * grp + 4);
+      }
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        short h, m, l;
+        split3(xs[j] * qs, h, m, l);
+        qv[t][0][s][j] = h;
+        qv[t][1][s][j] = m;
+        qv[t][2][s][j] = l;
+      }
+    }
+  }
+
+  v4f o[RT][8];  // O^T tiles: o[t][dt][i] = O[row t*16 + col][dim 16 dt + 4 grp + i]
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[t][dt] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m[RT], l[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.f;
+  }
+
+  // Staging: thread tid moves dims 4 scol .. + 3 of key rows srow + RP r
+  // (r < RT) of a 16-key block, for K and V (as loaded: bf16 words, fp8
+  // code words or fp32 chunk rows).
+  const int srow = tid >> 5;
+  const int scol = tid & 31;
+  const int lane_off = srow * D + scol * 4;
+  float4 stk[RT], stv[RT];
+  auto stage_load = [&](int blk) {
+    const int key0 = blk * kKeys;
+    std::size_t page_off = 0;
+    bool page_ok = false;
+    if (key0 < hist) {
+      const std::uint32_t page = table[blk];
+      page_ok = page < a.physical_blocks;
+      bad = bad || !page_ok;
+      page_off = page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
+    }
+    const long long crow = static_cast<long long>(chunk_row0) + key0 - hist;
+    const float* kchunk = a.chunk_key + crow * D;
+    const float* vchunk = a.chunk_value + crow * D;
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const int key = key0 + srow + RP * r;
+      const bool in_hist = key < hist;
+      const bool valid = key < key_end && (!in_hist || page_ok);
+      const int off = lane_off + RP * r * D;
+      stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      stv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (valid && in_hist) {
+        const std::size_t e = page_off + off;
+        if constexpr (FP8) {
+          stk[r].x = __uint_as_float(*reinterpret_cast<const unsigned*>(
+              reinterpret_cast<const unsigned char*>(a.key_pool) + e));
+          stv[r].x = __uint_as_float(*reinterpret_cast<const unsigned*>(
+              reinterpret_cast<const unsigned char*>(a.value_pool) + e));
+        } else {
+          const uint2 kw = *reinterpret_cast<const uint2*>(
+              reinterpret_cast<const unsigned short*>(a.key_pool) + e);
+          const uint2 vw = *reinterpret_cast<const uint2*>(
+              reinterpret_cast<const unsigned short*>(a.value_pool) + e);
+          stk[r] = make_float4(__uint_as_float(kw.x), __uint_as_float(kw.y), 0.f, 0.f);
+          stv[r] = make_float4(__uint_as_float(vw.x), __uint_as_float(vw.y), 0.f, 0.f);
+        }
+      } else if (valid) {
+        stk[r] = *reinterpret_cast<const float4*>(kchunk + off);
+        stv[r] = *reinterpret_cast<const float4*>(vchunk + off);
+      }
+    }
+  };
+  // Stores a staged block as bf16 (K rows, V transposed).  Returns whether
+  // a value row that some query row masks is non-finite.
+  auto stage_store = [&](int buf, int blk) {
+    bool nonfinite = false;
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const int kr = srow + RP * r;
+      const int key = blk * kKeys + kr;
+      uint2 kb, vb;  // 4 bf16 each, low half first
+      float4 vf;     // the value row's 4 dims as fp32 (non-finite check)
+      float4 kf;     // fp8: the key row's bare code values
+      if (key < hist) {
+        if constexpr (FP8) {
+          kf = fp8_widen4(__float_as_uint(stk[r].x), 1.0f);
+          vf = fp8_widen4(__float_as_uint(stv[r].x), 1.0f);
+          kb = make_uint2((__float_as_uint(kf.x) >> 16) | (__float_as_uint(kf.y) & 0xffff0000u),
+                          (__float_as_uint(kf.z) >> 16) | (__float_as_uint(kf.w) & 0xffff0000u));
+          vb = make_uint2((__float_as_uint(vf.x) >> 16) | (__float_as_uint(vf.y) & 0xffff0000u),
+                          (__float_as_uint(vf.z) >> 16) | (__float_as_uint(vf.w) & 0xffff0000u));
+        } else {
+          kb = make_uint2(__float_as_uint(stk[r].x), __float_as_uint(stk[r].y));
+          vb = make_uint2(__float_as_uint(stv[r].x), __float_as_uint(stv[r].y));
+          vf = bf16_widen(vb.x, vb.y);
+        }
+      } else {
+        // Chunk rows (zeros past the key range): onto the page grid.
+        if constexpr (FP8) {
+          kf = fp8_widen4(fp8_pack4_scaled(stk[r], a.k_scale), 1.0f);
+          vf = fp8_widen4(fp8_pack4_scaled(stv[r], a.v_scale), 1.0f);
+          kb = make_uint2((__float_as_uint(kf.x) >> 16) | (__float_as_uint(kf.y) & 0xffff0000u),
+                          (__float_as_uint(kf.z) >> 16) | (__float_as_uint(kf.w) & 0xffff0000u));
+          vb = make_uint2((__float_as_uint(vf.x) >> 16) | (__float_as_uint(vf.y) & 0xffff0000u),
+                          (__float_as_uint(vf.z) >> 16) | (__float_as_uint(vf.w) & 0xffff0000u));
+        } else {
+          kb = make_uint2(bf16_pack(stk[r].x, stk[r].y), bf16_pack(stk[r].z, stk[r].w));
+          vb = make_uint2(bf16_pack(stv[r].x, stv[r].y), bf16_pack(stv[r].z, stv[r].w));
+          vf = bf16_widen(vb.x, vb.y);
+        }
+      }
+      *reinterpret_cast<uint2*>(&sh.k[buf][kr * kBKStride + scol * 4]) = kb;
+      unsigned short* vt = &sh.vt[buf][(scol * 4) * kVtStride + kr];
+      vt[0] = static_cast<unsigned short>(vb.x & 0xffffu);
+      vt[kVtStride] = static_cast<unsigned short>(vb.x >> 16);
+      vt[2 * kVtStride] = static_cast<unsigned short>(vb.y & 0xffffu);
+      vt[3 * kVtStride] = static_cast<unsigned short>(vb.y >> 16);
+      if (key >= hist + pos0 + 1 && key < key_end && !finite4(vf)) nonfinite = true;
+    }
+    return nonfinite;
+  };
+  // Only a block holding chunk rows past the workgroup's first position can
+  // carry a masked value row; every other block needs a plain barrier.
+  auto staged_barrier = [&](bool nonfinite, int blk) -> int {
+    if (blk * kKeys + kKeys > hist + pos0 + 1) return __syncthreads_or(nonfinite);
+    __syncthreads();
+    return 0;
+  };
+
+  __shared__ int s_redo;
+  if (tid == 0) s_redo = 0;  // published by the first barrier below
+  const int nblocks = (key_end + kKeys - 1) / kKeys;
+  int exact_pv = 0;
+  if (nblocks > 0) {
+    stage_load(0);
+    exact_pv = staged_barrier(stage_store(0, 0), 0);
+  }
+  for (int n = 0; n < nblocks; ++n) {
+    const int buf = n & 1;
+    if (n + 1 < nblocks) stage_load(n + 1);
+    const unsigned short* K = sh.k[buf];
+    const unsigned short* VT = sh.vt[buf];
+
+    // S^T = K Q^T on the bf16 matrix cores: st[t] holds keys 4 grp + i of
+    // query row t * 16 + col.
+    v4f st[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) st[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const v8bf kop = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const v8s*>(&K[col * kBKStride + 32 * s + 8 * grp]));
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+          for (int term = 2; term >= 0; --term) {
+            st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                kop, __builtin_bit_cast(v8bf, qv[t][term][s]), st[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+    bool nan_score = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nan_score = nan_score || isnan(st[t][i]);
+    if (__ballot(nan_score) != 0 && lane == 0) s_redo = 1;
+
+    float p[RT][4];
+    const bool full = (n + 1) * kKeys <= min(key_end, hist + pos0 + 1);
+    auto softmax = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        float x[4];
+        bool vis[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = n * kKeys + 4 * grp + i;
+          vis[i] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
+          x[i] = vis[i] ? st[t][i] : -INFINITY;
+        }
+        const float mx = row_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+        const float mn = fmaxf(m[t], mx);
+        const float alpha = exp2_ratio(m[t], mn);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[t][i] = vis[i] ? exp2_ratio(x[i], mn) : 0.f;
+        const float sum = row_sum((p[t][0] + p[t][1]) + (p[t][2] + p[t][3]));
+        l[t] = l[t] * alpha + sum;
+        m[t] = mn;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
+      }
+    };
+    if (full) {
+      softmax(std::true_type{});
+    } else {
+      softmax(std::false_type{});
+    }
+
+    if (exact_pv && tid == 0) s_redo = 1;
+    {
+      // O^T += V^T P^T: A = V^T rows (dims 16 dt + col) at keys 4 grp .. + 3,
+      // B = the lane's own 4 probabilities of row col, as three bf16 terms.
+      v4s pv[RT][3];
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          short h, mm, lo;
+          split3(p[t][i], h, mm, lo);
+          pv[t][0][i] = h;
+          pv[t][1][i] = mm;
+          pv[t][2][i] = lo;
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const v4s vop = *reinterpret_cast<const v4s*>(&VT[(16 * dt + col) * kVtStride + 4 * grp]);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+          for (int term = 2; term >= 0; --term) {
+            o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pv[t][term], o[t][dt], 0,
+                                                                 0, 0);
+          }
+        }
+      }
+    }
+
+    if (n + 1 < nblocks) exact_pv = staged_barrier(stage_store(buf ^ 1, n + 1), n + 1);
+  }
+
+  const int any_bad = __syncthreads_or(bad);
+  if (tid == 0) redo[block] = s_redo != 0 ? 1u : 0u;
+  const float vscale = FP8 ? a.v_scale : 1.0f;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    if (qpos[t] >= T) continue;
+    const bool nan_row = any_bad || m[t] == -INFINITY;
+    const float inv = nan_row ? NAN : vscale / l[t];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      float4 r = make_float4(o[t][dt][0] * inv, o[t][dt][1] * inv, o[t][dt][2] * inv,
+                             o[t][dt][3] * inv);
+      if (nan_row) r = make_float4(NAN, NAN, NAN, NAN);
+      *reinterpret_cast<float4*>(a.out + qrow[t] + 16 * dt + 4 * grp) = r;
+    }
+  }
+}
+
+}  // namespace helix::hip::prefill_detail
