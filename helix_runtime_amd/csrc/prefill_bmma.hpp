@@ -15,13 +15,15 @@
 // only the order of the fp32 accumulation differs from the fp32 kernel.
 //
 // Special values.  A non-finite operand keeps only its hi term.  The split
-// can only go wrong by giving NaN (a zero query term times an infinite key,
-// where the fp32 product is inf), and a value row that some row masks must
-// not reach that row (0 * inf).  Exact paths for these cases would cost the
-// kernel its occupancy (they need registers the hot loop cannot spare), so
-// a work item that meets a NaN score or such a value row is flagged in
-// redo[block] instead; the launcher then runs prefill_body, which handles
-// both exactly, over the flagged items only.
+// can only go wrong by giving NaN where fp32 does not: a zero term of one
+// operand times an infinite element of the other (a query term against an
+// infinite key, a probability of exactly 1 against an infinite value), and
+// a value row that some row masks reaching that row (0 * inf).  Each such
+// NaN reaches the row's accumulators or sum, so a work item whose rows end
+// with a NaN there is flagged in redo[block], and the launcher runs
+// prefill_body (fp32 operands, exact paths for these cases) over the
+// flagged items only.  An item whose exact result is NaN anyway is just
+// computed twice.
 //
 // LDS: K rows as bf16, padded to kBKStride elements (16 bytes) so the 16
 // rows one operand read touches start in distinct banks; V transposed,
@@ -201,17 +203,14 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       }
     }
   };
-  // Stores a staged block as bf16 (K rows, V transposed).  Returns whether
-  // a value row that some query row masks is non-finite.
+  // Stores a staged block as bf16 (K rows, V transposed).
   auto stage_store = [&](int buf, int blk) {
-    bool nonfinite = false;
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
       const int kr = srow + RP * r;
       const int key = blk * kKeys + kr;
       uint2 kb, vb;  // 4 bf16 each, low half first
-      float4 vf;     // the value row's 4 dims as fp32 (non-finite check)
-      float4 kf;     // fp8: the key row's bare code values
+      float4 kf, vf;  // fp8: the rows' bare code values
       if (key < hist) {
         if constexpr (FP8) {
           kf = fp8_widen4(__float_as_uint(stk[r].x), 1.0f);
@@ -223,7 +222,6 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         } else {
           kb = make_uint2(__float_as_uint(stk[r].x), __float_as_uint(stk[r].y));
           vb = make_uint2(__float_as_uint(stv[r].x), __float_as_uint(stv[r].y));
-          vf = bf16_widen(vb.x, vb.y);
         }
       } else {
         // Chunk rows (zeros past the key range): onto the page grid.
@@ -237,7 +235,6 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         } else {
           kb = make_uint2(bf16_pack(stk[r].x, stk[r].y), bf16_pack(stk[r].z, stk[r].w));
           vb = make_uint2(bf16_pack(stv[r].x, stv[r].y), bf16_pack(stv[r].z, stv[r].w));
-          vf = bf16_widen(vb.x, vb.y);
         }
       }
       *reinterpret_cast<uint2*>(&sh.k[buf][kr * kBKStride + scol * 4]) = kb;
@@ -246,26 +243,17 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       vt[kVtStride] = static_cast<unsigned short>(vb.x >> 16);
       vt[2 * kVtStride] = static_cast<unsigned short>(vb.y & 0xffffu);
       vt[3 * kVtStride] = static_cast<unsigned short>(vb.y >> 16);
-      if (key >= hist + pos0 + 1 && key < key_end && !finite4(vf)) nonfinite = true;
     }
-    return nonfinite;
-  };
-  // Only a block holding chunk rows past the workgroup's first position can
-  // carry a masked value row; every other block needs a plain barrier.
-  auto staged_barrier = [&](bool nonfinite, int blk) -> int {
-    if (blk * kKeys + kKeys > hist + pos0 + 1) return __syncthreads_or(nonfinite);
-    __syncthreads();
-    return 0;
   };
 
   __shared__ int s_redo;
   if (tid == 0) s_redo = 0;  // published by the first barrier below
   const int nblocks = (key_end + kKeys - 1) / kKeys;
-  int exact_pv = 0;
   if (nblocks > 0) {
     stage_load(0);
-    exact_pv = staged_barrier(stage_store(0, 0), 0);
+    stage_store(0, 0);
   }
+  __syncthreads();
   for (int n = 0; n < nblocks; ++n) {
     const int buf = n & 1;
     if (n + 1 < nblocks) stage_load(n + 1);
@@ -292,13 +280,6 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         }
       }
     }
-    bool nan_score = false;
-#pragma unroll
-    for (int t = 0; t < RT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) nan_score = nan_score || isnan(st[t][i]);
-    if (__ballot(nan_score) != 0 && lane == 0) s_redo = 1;
-
     float p[RT][4];
     const bool full = (n + 1) * kKeys <= min(key_end, hist + pos0 + 1);
     auto softmax = [&](auto full_tag) {
@@ -331,7 +312,6 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       softmax(std::false_type{});
     }
 
-    if (exact_pv && tid == 0) s_redo = 1;
     {
       // O^T += V^T P^T: A = V^T rows (dims 16 dt + col) at keys 4 grp .. + 3,
       // B = the lane's own 4 probabilities of row col, as three bf16 terms.
@@ -361,9 +341,20 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       }
     }
 
-    if (n + 1 < nblocks) exact_pv = staged_barrier(stage_store(buf ^ 1, n + 1), n + 1);
+    if (n + 1 < nblocks) stage_store(buf ^ 1, n + 1);
+    __syncthreads();
   }
 
+  bool nan_row = false;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    nan_row = nan_row || isnan(l[t]);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nan_row = nan_row || isnan(o[t][dt][i]);
+  }
+  if (__ballot(nan_row) != 0 && lane == 0) s_redo = 1;
   const int any_bad = __syncthreads_or(bad);
   if (tid == 0) redo[block] = s_redo != 0 ? 1u : 0u;
   const float vscale = FP8 ? a.v_scale : 1.0f;

@@ -101,13 +101,17 @@ def test_prefill_every_group_matches_oracle(device, page_dtype, hq):
 
 @pytest.mark.parametrize("page_dtype", ["bf16", "fp8"])
 def test_prefill_special_values_are_redone_exactly(device, page_dtype):
-    """NaN key rows in a history (every row's scores NaN there) and
-    non-finite value rows at chunk positions 7 and 25 (rows before them must
-    not see them: 0 * inf would leak NaN)."""
+    """NaN key rows in a history (every row's scores NaN there), non-finite
+    value rows at chunk positions 7 and 25 (rows before them must not see
+    them: 0 * inf would leak NaN) and, on bf16 pages, one value dim infinite
+    over a whole history page (every row's first maximum there has p = 1,
+    whose middle and low bf16 terms are 0: the split gives 0 * inf = NaN
+    where fp32 gives inf)."""
     bad = np.float32("inf") if page_dtype == "bf16" else np.float32("nan")
 
     def edit(ks, vs, ck, cv, q):
         ks[2][0, 1, 33, 5] = np.float32("nan")
+        vs[1][0, 3, :16, 77] = bad
         cv[1, 0, 7, 100] = bad
         cv[3, 2, 25, :4] = bad
 
