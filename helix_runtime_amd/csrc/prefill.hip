@@ -47,6 +47,27 @@ void prefill_bmma_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ 
   prefill_body_bmma<G, PF, RT>(a, tables, order, redo, blockIdx.x, sh);
 }
 
+// fp32 pages with a redo array: the fast variant of the fp32 kernel (no
+// exact paths, one tile per wavefront, four wavefronts per SIMD), then the
+// exact kernel over the work items it flagged.
+constexpr int kFastTilesPerWave = 1;
+template <int G>
+__global__ __launch_bounds__(512 / kFastTilesPerWave, 6 - 2 * kFastTilesPerWave)
+void prefill_fast_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ tables,
+                         const std::uint32_t* __restrict__ order,
+                         std::uint32_t* __restrict__ redo) {
+  __shared__ PrefillShared sh;
+  prefill_body<G, false, 0, kFastTilesPerWave, true>(a, tables, order, blockIdx.x, sh, redo);
+}
+
+template <int G>
+void launch_fast(const dim3& grid, hipStream_t stream, const PrefillKernelArgs& k,
+                 const std::uint32_t* tables, const std::uint32_t* order, std::uint32_t* redo) {
+  prefill_fast_kernel<G><<<grid, 512 / kFastTilesPerWave, 0, stream>>>(k, tables, order, redo);
+  prefill_redo_kernel<G, 0, kTilesPerWave><<<grid, 512 / kTilesPerWave, 0, stream>>>(
+      k, tables, order, redo);
+}
+
 // bf16 / fp8 pages with a redo array: the bf16 matrix-core kernel, then the
 // exact kernel over the work items it flagged.
 template <int G, int PF>
@@ -128,7 +149,17 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.k_scale = a.page_type.k_scale;
   k.v_scale = a.page_type.v_scale;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
-  if (a.redo != nullptr && a.page_type.type != PageType::kF32) {
+  if (a.redo != nullptr && a.page_type.type == PageType::kF32) {
+    switch (group) {
+      case 1: launch_fast<1>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 2: launch_fast<2>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 4: launch_fast<4>(grid, stream, k, a.tables, a.order, a.redo); break;
+      case 8: launch_fast<8>(grid, stream, k, a.tables, a.order, a.redo); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  if (a.redo != nullptr) {
     const bool fp8 = a.page_type.type == PageType::kFP8;
     switch (group) {
       case 1: fp8 ? launch_bmma<1, 2>(grid, stream, k, a.tables, a.order, a.redo)

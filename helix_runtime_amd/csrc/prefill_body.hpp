@@ -189,11 +189,19 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 
 // The body of one prefill (or cascade prefix) workgroup; `block` is its
 // work-item index (the block index of the standalone kernel).
-template <int G, bool CASCADE, int PF, int RT, class Shared>
+// FAST (standalone prefill with a redo array): no exact P.V path and no
+// non-finite check per block; a work item whose rows end with a NaN in
+// their accumulators or sum (where a masked non-finite value row met a zero
+// probability, or the exact result is NaN anyway) is flagged in
+// redo[block] for the exact kernel.  Without the exact path the kernel
+// fits one 16-row tile per wavefront at four wavefronts per SIMD.
+template <int G, bool CASCADE, int PF, int RT, bool FAST = false, class Shared>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
                                              const std::uint32_t* __restrict__ tables,
                                              const std::uint32_t* __restrict__ order,
-                                             std::uint32_t block, Shared& sh) {
+                                             std::uint32_t block, Shared& sh,
+                                             std::uint32_t* __restrict__ redo = nullptr) {
+  static_assert(!FAST || !CASCADE, "the fast prefill is the standalone one");
   constexpr int PW = kRows / G;  // chunk positions per workgroup
   constexpr bool BF16 = PF == 1;
   constexpr bool FP8 = PF == 2;
@@ -406,7 +414,9 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   // carry a masked value row; every other block needs a plain barrier
   // (__syncthreads_or costs two more).
   auto staged_barrier = [&](bool nonfinite, int blk) -> int {
-    if (!CASCADE && blk * kKeys + kKeys > hist + pos0 + 1) return __syncthreads_or(nonfinite);
+    if (!FAST && !CASCADE && blk * kKeys + kKeys > hist + pos0 + 1) {
+      return __syncthreads_or(nonfinite);
+    }
     __syncthreads();
     return 0;
   };
@@ -504,7 +514,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       // Only a block holding chunk rows past the workgroup's first
       // position can carry a masked value row.
       exact_pv = 0;
-      if (!CASCADE && n * kKeys + kKeys > hist + pos0 + 1) {
+      if (!FAST && !CASCADE && n * kKeys + kKeys > hist + pos0 + 1) {
         exact_pv = __syncthreads_or(dma_nonfinite(n));
       }
       // The stage of block n - 1 is free: every wave has passed the barrier.
@@ -574,7 +584,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       softmax(std::false_type{});
     }
 
-    if (!exact_pv) {
+    if (FAST || !exact_pv) {
       // O^T += V^T P^T: k step i covers keys 4*g + i over the four lane
       // groups g; A = V rows of those keys at dims 64h + 4*col + c.
 #pragma unroll
@@ -635,6 +645,23 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
     }
   }
 
+  if constexpr (FAST) {
+    bool nan_row = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      nan_row = nan_row || isnan(l[t]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) nan_row = nan_row || isnan(o[t][h][c][i]);
+    }
+    // Any NaN row of the workgroup; bad (NaN rows by design) is folded in
+    // by the barrier below anyway.
+    const int nan_any = __syncthreads_or(nan_row);
+    if (threadIdx.x == 0) redo[block] = nan_any != 0 ? 1u : 0u;
+  }
   const int any_bad = __syncthreads_or(bad);
   if constexpr (CASCADE) {
     // Partial (m, l, o) per row; lanes of the four k groups hold the row's

@@ -1,8 +1,10 @@
-"""Chunked prefill over bf16 and fp8 pages through DecodeBatch, which runs it
-on the bf16 matrix cores (the fp32 operand of each product split into three
-exact bf16 terms) and redoes exactly, with the fp32 kernel, every work item
-that meets a special value.  Checked against the fp32 oracle on the rounded
-values within the fp32 tolerance (2e-5 abs + 1e-4 rel):
+"""Chunked prefill through DecodeBatch, which runs a fast kernel and then
+redoes exactly, with the fp32 kernel, every work item that met a special
+value: on bf16 and fp8 pages the bf16 matrix-core kernel (the fp32 operand
+of each product split into three exact bf16 terms), on fp32 pages the fp32
+kernel without its exact paths (one tile per wavefront).  Checked against
+the fp32 oracle on the rounded values within the fp32 tolerance (2e-5 abs +
+1e-4 rel):
 - every query group (1, 2, 4, 8 query heads per kv head), ragged histories;
 - the two special cases the matrix-core kernel hands to the exact kernel:
   a NaN score (here from NaN key rows, and from an infinite bf16 key whose
@@ -34,6 +36,8 @@ def host(t):
 
 
 def rounder(page_dtype):
+    if page_dtype == "f32":
+        return (lambda x: x), (lambda x: x)
     if page_dtype == "bf16":
         return oracle.round_bf16, oracle.round_bf16
     return (lambda x: oracle.round_fp8(x, KS)), (lambda x: oracle.round_fp8(x, VS))
@@ -92,22 +96,22 @@ def check(got, wants):
         np.testing.assert_allclose(got[b], want, atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("page_dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16", "fp8"])
 @pytest.mark.parametrize("hq", [4, 8, 16, 32])
 def test_prefill_every_group_matches_oracle(device, page_dtype, hq):
     got, wants = run_prefill(page_dtype, hq, [0, 5, 16, 70, 300], 40, 11 + hq)
     check(got, wants)
 
 
-@pytest.mark.parametrize("page_dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16", "fp8"])
 def test_prefill_special_values_are_redone_exactly(device, page_dtype):
     """NaN key rows in a history (every row's scores NaN there), non-finite
     value rows at chunk positions 7 and 25 (rows before them must not see
-    them: 0 * inf would leak NaN) and, on bf16 pages, one value dim infinite
-    over a whole history page (every row's first maximum there has p = 1,
+    them: 0 * inf would leak NaN) and one value dim infinite (fp8: NaN) over
+    a whole history page (every row's first maximum there has p = 1,
     whose middle and low bf16 terms are 0: the split gives 0 * inf = NaN
     where fp32 gives inf)."""
-    bad = np.float32("inf") if page_dtype == "bf16" else np.float32("nan")
+    bad = np.float32("nan") if page_dtype == "fp8" else np.float32("inf")
 
     def edit(ks, vs, ck, cv, q):
         ks[2][0, 1, 33, 5] = np.float32("nan")
@@ -145,7 +149,7 @@ def test_prefill_infinite_bf16_key_with_zero_middle_query_term(device):
     check(got, wants)
 
 
-@pytest.mark.parametrize("page_dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("page_dtype", ["f32", "bf16", "fp8"])
 def test_prefill_config5_shaped_chunk(device, page_dtype):
     """512-token chunks over histories of ~1000 tokens, 32 query and 8 kv
     heads: four position blocks per (sequence, kv head) in longest-first
