@@ -426,6 +426,14 @@ int helix_decode_batch_rope(helix_decode_batch* b, float* query, float* key,
 int helix_decode_batch_attention_layer(helix_decode_batch* b, size_t layer, const float* query,
                                        const float* tail_key, const float* tail_value,
                                        float* output, helix_stream stream);
+/* The chunk attention of a prepare_chunk() step.  fp32 pages: the fp32
+ * matrix cores, one 16-row tile per wavefront.  bf16 and fp8 pages: the bf16
+ * matrix cores, page values exact in bf16 and the fp32 operand of each
+ * product split into three exact bf16 terms (every product exact, fp32
+ * accumulation).  Either way a work item that meets a special value (a NaN
+ * in a row's accumulators or sum) is recomputed by the exact kernel in a
+ * second launch, so the results follow the reference's special-value rules
+ * within the fp32 tolerance.  The flags live in the batch's step buffer. */
 int helix_decode_batch_prefill_layer(helix_decode_batch* b, size_t layer, const float* query,
                                      const float* chunk_key, const float* chunk_value,
                                      float* output, helix_stream stream);
