@@ -53,10 +53,12 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int D = 128;
 constexpr int P = 16;
 constexpr int kRows = 128;      // query rows per workgroup
-// 16-row tiles per wavefront: 2 (4 waves per workgroup, 256 VGPRs, two
-// workgroups per CU).  The kernel also builds with 1 (8 waves, 128 VGPRs,
-// four waves per SIMD): at config 5 that spills (21 VGPRs even with the
-// direct-load staging) and measured 103.7 against 113.1 TFLOP/s.
+// 16-row tiles per wavefront of the exact kernel: 2 (4 waves per workgroup,
+// 256 VGPRs, two workgroups per CU).  With its exact paths the kernel also
+// builds with 1 (8 waves, 128 VGPRs, four waves per SIMD), but then spills
+// (21 VGPRs even with the direct-load staging) and measured 103.7 against
+// 113.1 TFLOP/s at config 5; the fast variant (FAST below) drops those paths
+// and runs one tile per wave at 118 VGPRs.
 constexpr int kTilesPerWave = 2;
 // The cascade prefix pass has few keys per work item and runs beside the
 // stream decode kernel: 8 waves of one tile (108 VGPRs, no spills) fit two
