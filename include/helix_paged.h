@@ -388,7 +388,12 @@ int helix_paged_append_chunk(const float* keys, const float* values, float* key_
  * pages), append_layer() writes it, attention_layer() attends over the
  * history before the step plus the tail.  prepare_chunk() reserves `tokens`
  * slots per sequence instead; append_layer() then takes [batch, kv_heads,
- * tokens, head_dim] rows and prefill_layer() runs the chunk attention. */
+ * tokens, head_dim] rows and prefill_layer() runs the chunk attention.
+ * Streams: any call may use any stream (it waits for the step's upload, and
+ * the next prepare() waits for the last call's stream), but the calls of one
+ * step share the batch's workspace and step buffers, so two attention or
+ * prefill calls that overlap in time on different streams race; order them
+ * (one stream, or events between streams), as a layer loop does. */
 int helix_decode_batch_create(helix_paged_cache* cache, const helix_sequence* sequences,
                               size_t batch, size_t q_heads, size_t max_tokens,
                               size_t pages_per_split, helix_decode_batch** out);
