@@ -947,7 +947,10 @@ using PagedPrefixCache = HipPagedPrefixCache;
 /// tables and lengths; each layer then attends over the pages plus the
 /// step's tail rows and, in either order, commits them.  Shapes: query
 /// [B, q_heads, D], step keys/values [B, kv_heads, D] (chunk forms take
-/// [B, heads, T, D]), all-layer commit [layers, B, kv_heads, D].
+/// [B, heads, T, D]), all-layer commit [layers, B, kv_heads, D].  The calls
+/// of one step share the batch's workspace and step buffers: calls that
+/// overlap in time on different streams race, so order them (one stream or
+/// events), as a layer loop does.
 class DecodeBatch final {
  public:
   DecodeBatch(HipPagedKvCache& cache, std::span<const HipPagedSequenceHandle> sequences,
