@@ -1,17 +1,17 @@
 // Chunked-prefill attention for bf16 and fp8 pages on the bf16 matrix cores.
 //
 // The decomposition, masks, online softmax and special-value rules are those
-// of prefill_body (one workgroup of 4 wavefronts per (sequence, kv head) and
-// 128 query rows, two 16-row tiles per wavefront, scores computed transposed
-// so each lane holds 4 keys of one query row).  What differs is the matrix
+// of prefill_body (one workgroup per (sequence, kv head) and 128 query rows,
+// 16-row tiles, scores computed transposed so each lane holds keys of one
+// query row).  What differs is the matrix
 // arithmetic.  A bf16 page element is exact in bf16, and so is the bare code
 // value of an fp8 element (the key scale joins the score scale and the value
 // scale multiplies the output, as in the decode kernel).  The fp32 operand
 // of each product (the scaled query, the probabilities) is split by
 // truncation into three bf16 terms, hi + mid + lo, which hold its 24
 // significant bits exactly.  Every product term is then exact in fp32, and
-// three v_mfma_f32_16x16x32_bf16 (scores) or v_mfma_f32_16x16x16_bf16 (P.V)
-// replace the fp32 instructions at about five times the matrix throughput;
+// three v_mfma_f32_16x16x32_bf16 replace each fp32 instruction (scores and
+// P.V) at about five times the matrix throughput;
 // only the order of the fp32 accumulation differs from the fp32 kernel.
 //
 // Special values.  A non-finite operand keeps only its hi term.  The split
@@ -25,10 +25,18 @@
 // flagged items only.  An item whose exact result is NaN anyway is just
 // computed twice.
 //
+// Blocks of 32 keys (two pages) per LDS stage, so that both products run on
+// the K = 32 instruction.  Scores come out as two 16-key tiles, keys
+// 4 g + i and 16 + 4 g + i of row col in lane (g = lane / 16, col = lane %
+// 16).  P.V contracts over the keys in any order, so its 32-key operand
+// takes them in the order the scores left them: contraction index 8 g + j
+// is key 4 g + j for j < 4 and key 16 + 4 g + j - 4 otherwise, and V is
+// staged in the same order.
+//
 // LDS: K rows as bf16, padded to kBKStride elements (16 bytes) so the 16
 // rows one operand read touches start in distinct banks; V transposed,
-// [dim][key] with rows of kVtStride keys, so one 8-byte read gives a lane the
-// 4 keys of one dim that the P.V operand needs.
+// [dim][contraction index] with rows of kVtStride elements, so one 16-byte
+// read gives a lane the 8 keys of one dim that the P.V operand needs.
 #pragma once
 
 #include "prefill_body.hpp"
@@ -36,16 +44,25 @@
 namespace helix::hip::prefill_detail {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
-constexpr int kBKStride = D + 8;  // bf16 elements per K row in LDS
-constexpr int kVtStride = 20;     // bf16 elements per transposed V row (16 keys + pad)
+constexpr int kBKeys = 2 * P;          // keys per LDS stage
+constexpr int kBKStride = D + 8;       // bf16 elements per K row in LDS
+constexpr int kVtStride = kBKeys + 8;  // bf16 elements per transposed V row
 
 struct PrefillBmmaShared {
-  __align__(16) unsigned short k[2][kKeys * kBKStride];
+  __align__(16) unsigned short k[2][kBKeys * kBKStride];
   __align__(16) unsigned short vt[2][D * kVtStride];
+  // The low bf16 term of each lane's query operand, [wave][step][lane]:
+  // kept here rather than in registers, which the other two terms, the
+  // accumulators and the staging fill.
+  __align__(16) uint4 qlo[kRows / 16][4][64];
 };
+
+// Position of key kr (0 .. 31 within a stage) on the P.V contraction axis.
+__device__ __forceinline__ int bmma_key_slot(int kr) {
+  return 8 * ((kr & 15) >> 2) + 4 * (kr >> 4) + (kr & 3);
+}
 
 // x = hi + mid + lo exactly (truncating splits of a finite fp32); a
 // non-finite x is hi alone.  Results are bf16 bit patterns.
@@ -62,6 +79,43 @@ __device__ __forceinline__ void split3(float x, short& hi, short& mid, short& lo
   mid = static_cast<short>(u1 >> 16);
   const float r2 = r1 - __uint_as_float(u1 & 0xffff0000u);
   lo = static_cast<short>(__float_as_uint(r2) >> 16);
+}
+
+// split3 for a probability (in [0, 1], or NaN): no finiteness test.  For
+// a finite p the terms are split3's.  A NaN p still gives a NaN middle term,
+// so the row's accumulators end NaN as they must (the item is redone).
+__device__ __forceinline__ void split3_prob(float x, short& hi, short& mid, short& lo) {
+  const unsigned u = __float_as_uint(x);
+  hi = static_cast<short>(u >> 16);
+  const float r1 = x - __uint_as_float(u & 0xffff0000u);
+  const unsigned u1 = __float_as_uint(r1);
+  mid = static_cast<short>(u1 >> 16);
+  const float r2 = r1 - __uint_as_float(u1 & 0xffff0000u);
+  lo = static_cast<short>(__float_as_uint(r2) >> 16);
+}
+
+// Maxima without the compiler's NaN quieting of each operand (the matrix
+// results it cannot prove canonical).  Where a NaN score meets them the
+// row's probabilities come out NaN whichever operand is kept, and the item
+// is redone exactly.
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Maximum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row).
+__device__ __forceinline__ float row_max_raw(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = max_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return max_raw(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 
 __device__ __forceinline__ float bf16_bits_value(unsigned short h) {
@@ -115,7 +169,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
   // t * 16 + col (B operand of S^T = K Q^T), as three bf16 terms.
   int qpos[RT];
   std::size_t qrow[RT];
-  v8s qv[RT][3][4];
+  v8s qv[RT][2][4];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     const int r = wave * (16 * RT) + t * 16 + col;
@@ -131,14 +185,16 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         x1 = *reinterpret_cast<const float4*>(a.query + qrow[t] + 32 * s + 8 * grp + 4);
       }
       const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      v8s lo;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         short h, m, l;
         split3(xs[j] * qs, h, m, l);
         qv[t][0][s][j] = h;
         qv[t][1][s][j] = m;
-        qv[t][2][s][j] = l;
+        lo[j] = l;
       }
+      sh.qlo[wave * RT + t][s][lane] = __builtin_bit_cast(uint4, lo);
     }
   }
 
@@ -155,31 +211,30 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
   }
 
   // Staging: thread tid moves dims 4 scol .. + 3 of key rows srow + RP r
-  // (r < RT) of a 16-key block, for K and V (as loaded: bf16 words, fp8
-  // code words or fp32 chunk rows).
+  // (r < NR) of one 16-key half (one page) of a 32-key block, for K and V
+  // (as loaded: bf16 words, fp8 code words or fp32 chunk rows).  The two
+  // halves of the next block are staged one after the other, so only one
+  // page is held in registers.
+  constexpr int NR = P / RP;
   const int srow = tid >> 5;
   const int scol = tid & 31;
-  const int lane_off = srow * D + scol * 4;
-  float4 stk[RT], stv[RT];
-  auto stage_load = [&](int blk) {
-    const int key0 = blk * kKeys;
+  float4 stk[NR], stv[NR];
+  auto stage_load = [&](int blk, int half) {
+    const int pkey0 = blk * kBKeys + half * P;
     std::size_t page_off = 0;
     bool page_ok = false;
-    if (key0 < hist) {
-      const std::uint32_t page = table[blk];
+    if (pkey0 < hist) {
+      const std::uint32_t page = table[pkey0 / P];
       page_ok = page < a.physical_blocks;
       bad = bad || !page_ok;
       page_off = page_ok ? (static_cast<std::size_t>(page) * a.kv_heads + kvh) * P * D : 0;
     }
-    const long long crow = static_cast<long long>(chunk_row0) + key0 - hist;
-    const float* kchunk = a.chunk_key + crow * D;
-    const float* vchunk = a.chunk_value + crow * D;
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      const int key = key0 + srow + RP * r;
+    for (int r = 0; r < NR; ++r) {
+      const int key = pkey0 + srow + RP * r;
       const bool in_hist = key < hist;
       const bool valid = key < key_end && (!in_hist || page_ok);
-      const int off = lane_off + RP * r * D;
+      const int off = (srow + RP * r) * D + scol * 4;
       stk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
       stv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (valid && in_hist) {
@@ -198,17 +253,18 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
           stv[r] = make_float4(__uint_as_float(vw.x), __uint_as_float(vw.y), 0.f, 0.f);
         }
       } else if (valid) {
-        stk[r] = *reinterpret_cast<const float4*>(kchunk + off);
-        stv[r] = *reinterpret_cast<const float4*>(vchunk + off);
+        const std::size_t crow = chunk_row0 + static_cast<std::size_t>(key - hist);
+        stk[r] = *reinterpret_cast<const float4*>(a.chunk_key + crow * D + scol * 4);
+        stv[r] = *reinterpret_cast<const float4*>(a.chunk_value + crow * D + scol * 4);
       }
     }
   };
-  // Stores a staged block as bf16 (K rows, V transposed).
-  auto stage_store = [&](int buf, int blk) {
+  // Stores a staged half as bf16 (K rows, V transposed in contraction order).
+  auto stage_store = [&](int buf, int blk, int half) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      const int kr = srow + RP * r;
-      const int key = blk * kKeys + kr;
+    for (int r = 0; r < NR; ++r) {
+      const int kr = half * P + srow + RP * r;
+      const int key = blk * kBKeys + kr;
       uint2 kb, vb;  // 4 bf16 each, low half first
       float4 kf, vf;  // fp8: the rows' bare code values
       if (key < hist) {
@@ -238,7 +294,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         }
       }
       *reinterpret_cast<uint2*>(&sh.k[buf][kr * kBKStride + scol * 4]) = kb;
-      unsigned short* vt = &sh.vt[buf][(scol * 4) * kVtStride + kr];
+      unsigned short* vt = &sh.vt[buf][(scol * 4) * kVtStride + bmma_key_slot(kr)];
       vt[0] = static_cast<unsigned short>(vb.x & 0xffffu);
       vt[kVtStride] = static_cast<unsigned short>(vb.x >> 16);
       vt[2 * kVtStride] = static_cast<unsigned short>(vb.y & 0xffffu);
@@ -248,62 +304,81 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
 
   __shared__ int s_redo;
   if (tid == 0) s_redo = 0;  // published by the first barrier below
-  const int nblocks = (key_end + kKeys - 1) / kKeys;
+  const int nblocks = (key_end + kBKeys - 1) / kBKeys;
   if (nblocks > 0) {
-    stage_load(0);
-    stage_store(0, 0);
+    stage_load(0, 0);
+    stage_store(0, 0, 0);
+    stage_load(0, 1);
+    stage_store(0, 0, 1);
   }
   __syncthreads();
   for (int n = 0; n < nblocks; ++n) {
     const int buf = n & 1;
-    if (n + 1 < nblocks) stage_load(n + 1);
+    const bool next = n + 1 < nblocks;
+    if (next) stage_load(n + 1, 0);
     const unsigned short* K = sh.k[buf];
     const unsigned short* VT = sh.vt[buf];
 
-    // S^T = K Q^T on the bf16 matrix cores: st[t] holds keys 4 grp + i of
-    // query row t * 16 + col.
-    v4f st[RT];
+    // S^T = K Q^T on the bf16 matrix cores: st[t][h] holds keys
+    // 16 h + 4 grp + i of query row t * 16 + col.
+    v4f st[RT][2];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) st[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    {
+    for (int t = 0; t < RT; ++t) st[t][0] = st[t][1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const v8bf kop = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const v8s*>(&K[col * kBKStride + 32 * s + 8 * grp]));
+    for (int s = 0; s < 4; ++s) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t) {
+      for (int t = 0; t < RT; ++t) {
+        const v8bf qlo = __builtin_bit_cast(v8bf, sh.qlo[wave * RT + t][s][lane]);
 #pragma unroll
-          for (int term = 2; term >= 0; --term) {
-            st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                kop, __builtin_bit_cast(v8bf, qv[t][term][s]), st[t], 0, 0, 0);
+        for (int h = 0; h < 2; ++h) {
+          const v8bf kop = __builtin_bit_cast(
+              v8bf,
+              *reinterpret_cast<const v8s*>(&K[(16 * h + col) * kBKStride + 32 * s + 8 * grp]));
+          st[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo, st[t][h], 0, 0, 0);
+#pragma unroll
+          for (int term = 1; term >= 0; --term) {
+            st[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                kop, __builtin_bit_cast(v8bf, qv[t][term][s]), st[t][h], 0, 0, 0);
           }
         }
       }
     }
-    float p[RT][4];
-    const bool full = (n + 1) * kKeys <= min(key_end, hist + pos0 + 1);
+    float p[RT][8];  // p[t][4 h + i]: key 16 h + 4 grp + i
+    const bool full = (n + 1) * kBKeys <= min(key_end, hist + pos0 + 1);
     auto softmax = [&](auto full_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        float x[4];
-        bool vis[4];
+        float x[8];
+        bool vis[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = n * kKeys + 4 * grp + i;
-          vis[i] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
-          x[i] = vis[i] ? st[t][i] : -INFINITY;
+        for (int j = 0; j < 8; ++j) {
+          const int key = n * kBKeys + 16 * (j >> 2) + 4 * grp + (j & 3);
+          vis[j] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
+          x[j] = vis[j] ? st[t][j >> 2][j & 3] : -INFINITY;
         }
-        const float mx = row_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-        const float mn = fmaxf(m[t], mx);
-        const float alpha = exp2_ratio(m[t], mn);
+        const float mx = row_max_raw(max3_raw(max3_raw(x[0], x[1], x[2]),
+                                              max3_raw(x[3], x[4], x[5]), max_raw(x[6], x[7])));
+        const float mn = max_raw(m[t], mx);
+        // alpha is exactly 1 when the maximum holds, so the accumulators
+        // are only rescaled when some row of the wavefront moved.
+        float alpha = 1.f;
+        if (true) {
+          alpha = exp2_ratio(m[t], mn);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[t][i] = vis[i] ? exp2_ratio(x[i], mn) : 0.f;
-        const float sum = row_sum((p[t][0] + p[t][1]) + (p[t][2] + p[t][3]));
+          for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
+        }
+        if (FULL && __ballot(!(fabsf(mn) < INFINITY)) == 0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) p[t][j] = __builtin_amdgcn_exp2f(x[j] - mn);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) p[t][j] = vis[j] ? exp2_ratio(x[j], mn) : 0.f;
+        }
+        const float sum = row_sum(((p[t][0] + p[t][1]) + (p[t][2] + p[t][3])) +
+                                  ((p[t][4] + p[t][5]) + (p[t][6] + p[t][7])));
         l[t] = l[t] * alpha + sum;
         m[t] = mn;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
       }
     };
     if (full) {
@@ -312,36 +387,43 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       softmax(std::false_type{});
     }
 
+    if (next) {
+      stage_store(buf ^ 1, n + 1, 0);
+      stage_load(n + 1, 1);
+    }
+
     {
-      // O^T += V^T P^T: A = V^T rows (dims 16 dt + col) at keys 4 grp .. + 3,
-      // B = the lane's own 4 probabilities of row col, as three bf16 terms.
-      v4s pv[RT][3];
+      // O^T += V^T P^T: A = V^T rows (dims 16 dt + col) at contraction
+      // indices 8 grp .. + 7, B = the lane's own 8 probabilities of row col
+      // in the same order, as three bf16 terms.
+      v8s pv[RT][3];
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int j = 0; j < 8; ++j) {
           short h, mm, lo;
-          split3(p[t][i], h, mm, lo);
-          pv[t][0][i] = h;
-          pv[t][1][i] = mm;
-          pv[t][2][i] = lo;
+          split3_prob(p[t][j], h, mm, lo);
+          pv[t][0][j] = h;
+          pv[t][1][j] = mm;
+          pv[t][2][j] = lo;
         }
       }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const v4s vop = *reinterpret_cast<const v4s*>(&VT[(16 * dt + col) * kVtStride + 4 * grp]);
+        const v8bf vop = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const v8s*>(&VT[(16 * dt + col) * kVtStride + 8 * grp]));
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
 #pragma unroll
           for (int term = 2; term >= 0; --term) {
-            o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pv[t][term], o[t][dt], 0,
-                                                                 0, 0);
+            o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                vop, __builtin_bit_cast(v8bf, pv[t][term]), o[t][dt], 0, 0, 0);
           }
         }
       }
     }
 
-    if (n + 1 < nblocks) stage_store(buf ^ 1, n + 1);
+    if (next) stage_store(buf ^ 1, n + 1, 1);
     __syncthreads();
   }
 
