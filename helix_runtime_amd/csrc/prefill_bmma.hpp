@@ -118,6 +118,15 @@ __device__ __forceinline__ float row_max_raw(float v) {
   return max_raw(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 
+// Four fp8 code values (one word, lowest byte first) as four bf16 bit
+// patterns, lowest first, two to a word.  Exact: every E4M3 value is a bf16
+// value, and the scale is 1.
+__device__ __forceinline__ uint2 fp8_codes_bf16(unsigned w) {
+  const auto lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  const auto hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  return make_uint2(__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi));
+}
+
 __device__ __forceinline__ float bf16_bits_value(unsigned short h) {
   return __uint_as_float(static_cast<unsigned>(h) << 16);
 }
@@ -265,16 +274,11 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
     for (int r = 0; r < NR; ++r) {
       const int kr = half * P + srow + RP * r;
       const int key = blk * kBKeys + kr;
-      uint2 kb, vb;  // 4 bf16 each, low half first
-      float4 kf, vf;  // fp8: the rows' bare code values
+      uint2 kb, vb;  // 4 bf16 each, low half first (fp8: the bare code values)
       if (key < hist) {
         if constexpr (FP8) {
-          kf = fp8_widen4(__float_as_uint(stk[r].x), 1.0f);
-          vf = fp8_widen4(__float_as_uint(stv[r].x), 1.0f);
-          kb = make_uint2((__float_as_uint(kf.x) >> 16) | (__float_as_uint(kf.y) & 0xffff0000u),
-                          (__float_as_uint(kf.z) >> 16) | (__float_as_uint(kf.w) & 0xffff0000u));
-          vb = make_uint2((__float_as_uint(vf.x) >> 16) | (__float_as_uint(vf.y) & 0xffff0000u),
-                          (__float_as_uint(vf.z) >> 16) | (__float_as_uint(vf.w) & 0xffff0000u));
+          kb = fp8_codes_bf16(__float_as_uint(stk[r].x));
+          vb = fp8_codes_bf16(__float_as_uint(stv[r].x));
         } else {
           kb = make_uint2(__float_as_uint(stk[r].x), __float_as_uint(stk[r].y));
           vb = make_uint2(__float_as_uint(stv[r].x), __float_as_uint(stv[r].y));
@@ -282,12 +286,8 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       } else {
         // Chunk rows (zeros past the key range): onto the page grid.
         if constexpr (FP8) {
-          kf = fp8_widen4(fp8_pack4_scaled(stk[r], a.k_scale), 1.0f);
-          vf = fp8_widen4(fp8_pack4_scaled(stv[r], a.v_scale), 1.0f);
-          kb = make_uint2((__float_as_uint(kf.x) >> 16) | (__float_as_uint(kf.y) & 0xffff0000u),
-                          (__float_as_uint(kf.z) >> 16) | (__float_as_uint(kf.w) & 0xffff0000u));
-          vb = make_uint2((__float_as_uint(vf.x) >> 16) | (__float_as_uint(vf.y) & 0xffff0000u),
-                          (__float_as_uint(vf.z) >> 16) | (__float_as_uint(vf.w) & 0xffff0000u));
+          kb = fp8_codes_bf16(fp8_pack4_scaled(stk[r], a.k_scale));
+          vb = fp8_codes_bf16(fp8_pack4_scaled(stv[r], a.v_scale));
         } else {
           kb = make_uint2(bf16_pack(stk[r].x, stk[r].y), bf16_pack(stk[r].z, stk[r].w));
           vb = make_uint2(bf16_pack(stv[r].x, stv[r].y), bf16_pack(stv[r].z, stv[r].w));

@@ -156,3 +156,24 @@ def test_prefill_config5_shaped_chunk(device, page_dtype):
     order."""
     got, wants = run_prefill(page_dtype, 32, [1000, 777, 1210], 512, 23, H=8)
     check(got, wants)
+
+
+def test_prefill_every_fp8_code_in_history(device):
+    """Every finite E4M3 code (subnormals, the largest values and both signs)
+    in the history keys and values, each at several dims and heads: the
+    staging moves the page codes to bf16 in hardware, which must keep every
+    code value exact."""
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)  # 254 codes
+    vals = oracle.fp8_decode(codes)
+
+    def edit(ks, vs, ck, cv, q):
+        for b, (k, v) in enumerate(zip(ks, vs)):
+            _, H, n, _ = k.shape
+            idx = (np.arange(H)[:, None, None] * 7 + np.arange(n)[None, :, None] * D
+                   + np.arange(D)[None, None, :] + 13 * b)
+            k[0] = vals[idx % len(codes)] * np.float32(KS)
+            v[0] = vals[(idx + 101) % len(codes)] * np.float32(VS)
+        q *= np.float32(0.05)  # keys reach 448 * KS: keep the scores moderate
+
+    got, wants = run_prefill("fp8", 16, [254, 300], 24, 31, edit)
+    check(got, wants)
