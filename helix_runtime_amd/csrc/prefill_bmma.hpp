@@ -324,6 +324,10 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
     v4f st[RT][2];
 #pragma unroll
     for (int t = 0; t < RT; ++t) st[t][0] = st[t][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    // Raised wave priority over the matrix instructions: the waves of one
+    // workgroup reach them together (barriers), and the softmax and staging
+    // of the other workgroup on the CU fill the gaps.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -343,6 +347,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     float p[RT][8];  // p[t][4 h + i]: key 16 h + 4 grp + i
     const bool full = (n + 1) * kBKeys <= min(key_end, hist + pos0 + 1);
     auto softmax = [&](auto full_tag) {
@@ -408,6 +413,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
           pv[t][2][j] = lo;
         }
       }
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const v8bf vop = __builtin_bit_cast(
@@ -423,6 +429,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
       }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     if (next) stage_store(buf ^ 1, n + 1, 1);
     __syncthreads();
   }
