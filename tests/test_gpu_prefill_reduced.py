@@ -177,3 +177,13 @@ def test_prefill_every_fp8_code_in_history(device):
 
     got, wants = run_prefill("fp8", 16, [254, 300], 24, 31, edit)
     check(got, wants)
+
+
+@pytest.mark.parametrize("page_dtype", ["bf16", "fp8"])
+@pytest.mark.parametrize("T", [1, 31, 33, 64])
+def test_prefill_chunk_lengths_across_key_blocks(device, page_dtype, T):
+    """Chunks of 1, 31, 33 and 64 tokens over histories that end just before,
+    on and just after a 32-key staging block (and one that ends mid-page),
+    so the last block of each work item is partial in every way."""
+    got, wants = run_prefill(page_dtype, 8, [31, 32, 33, 47, 64], T, 40 + T)
+    check(got, wants)
