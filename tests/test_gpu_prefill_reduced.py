@@ -11,7 +11,10 @@ the fp32 oracle on the rounded values within the fp32 tolerance (2e-5 abs +
   query term splits with a zero middle part, where the split alone would
   give NaN instead of inf) and a non-finite value row in a chunk position
   that earlier rows mask;
-- a config-5-shaped chunk (512 tokens over histories of ~1000)."""
+- a config-5-shaped chunk (512 tokens over histories of ~1000);
+- every finite fp8 code in a history (the staging's hardware fp8-to-bf16
+  move);
+- chunk lengths and histories around the 32-key staging blocks."""
 
 import numpy as np
 import pytest
