@@ -34,8 +34,9 @@ void prefill_redo_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ 
 }
 
 // Tiles per wavefront of the bf16 matrix-core prefill: one (8 wavefronts
-// of 16 rows) keeps the three-term query operand and the accumulators of a
-// wavefront within 128 VGPRs, four wavefronts per SIMD.
+// of 16 rows) keeps two of the query operand's three terms (the third is
+// in LDS), the accumulators and the staging of a wavefront within 128
+// VGPRs, four wavefronts per SIMD.
 constexpr int kBmmaTilesPerWave = 1;
 
 template <int G, int PF, int RT>
