@@ -20,7 +20,8 @@
 // infinite key, a probability of exactly 1 against an infinite value), and
 // a value row that some row masks reaching that row (0 * inf).  Each such
 // NaN reaches the row's accumulators or sum, so a work item whose rows end
-// with a NaN there is flagged in redo[block], and the launcher runs
+// with a NaN there (or with a sum that is not finite) is flagged in
+// redo[block], and the launcher runs
 // prefill_body (fp32 operands, exact paths for these cases) over the
 // flagged items only.  An item whose exact result is NaN anyway is just
 // computed twice.
@@ -92,30 +93,6 @@ __device__ __forceinline__ void split3_prob(float x, short& hi, short& mid, shor
   mid = static_cast<short>(u1 >> 16);
   const float r2 = r1 - __uint_as_float(u1 & 0xffff0000u);
   lo = static_cast<short>(__float_as_uint(r2) >> 16);
-}
-
-// Maxima without the compiler's NaN quieting of each operand (the matrix
-// results it cannot prove canonical).  Where a NaN score meets them the
-// row's probabilities come out NaN whichever operand is kept, and the item
-// is redone exactly.
-__device__ __forceinline__ float max_raw(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float max3_raw(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-// Maximum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row).
-__device__ __forceinline__ float row_max_raw(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  v = max_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return max_raw(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 
 // Four fp8 code values (one word, lowest byte first) as four bf16 bit
@@ -362,17 +339,13 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
           vis[j] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
           x[j] = vis[j] ? st[t][j >> 2][j & 3] : -INFINITY;
         }
-        const float mx = row_max_raw(max3_raw(max3_raw(x[0], x[1], x[2]),
-                                              max3_raw(x[3], x[4], x[5]), max_raw(x[6], x[7])));
-        const float mn = max_raw(m[t], mx);
-        // alpha is exactly 1 when the maximum holds, so the accumulators
-        // are only rescaled when some row of the wavefront moved.
-        float alpha = 1.f;
-        if (true) {
-          alpha = exp2_ratio(m[t], mn);
+        const float mx = row_max(fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]))));
+        const float mn = fmaxf(m[t], mx);
+        // Branch-free rescale (alpha is 1 for rows whose maximum held).
+        const float alpha = exp2_ratio(m[t], mn);
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
-        }
+        for (int dt = 0; dt < 8; ++dt) o[t][dt] *= alpha;
         if (FULL && __ballot(!(fabsf(mn) < INFINITY)) == 0) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) p[t][j] = __builtin_amdgcn_exp2f(x[j] - mn);
@@ -437,7 +410,7 @@ __device__ __forceinline__ void prefill_body_bmma(PrefillKernelArgs a,
   bool nan_row = false;
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    nan_row = nan_row || isnan(l[t]);
+    nan_row = nan_row || !(l[t] < INFINITY);  // NaN, or a sum that overflowed
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll

@@ -651,7 +651,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
     bool nan_row = false;
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      nan_row = nan_row || isnan(l[t]);
+      nan_row = nan_row || !(l[t] < INFINITY);  // NaN, or a sum that overflowed
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
