@@ -214,101 +214,7 @@ TEST_F(HostContractTest, InvalidArgumentsFailBeforeDeviceWork) {
   EXPECT_FALSE(static_cast<bool>(HipPagedSequenceHandle{}));
 }
 
-// Host page bookkeeping under contention: eight threads run random programs
-// (create, append, forks of a shared source, releases) on one block manager
-// through the C ABI.  Every call is serialised by the manager: each
-// sequence ends at the length its own successful appends give it, every
-// invariant holds (helix_block_manager_validate), each page's reference count
-// equals the number of live tables holding it, and releasing everything
-// returns every page.
-TEST_F(HostContractTest, BlockManagerSerialisesConcurrentPrograms) {
-  const helix_paged_config config{1, 1, 4, 4, 64};
-  helix_block_manager* m = nullptr;
-  ASSERT_EQ(helix_block_manager_create(&config, &m), HELIX_OK);
-  helix_sequence source{};
-  ASSERT_EQ(helix_block_manager_create_sequence(m, &source), HELIX_OK);
-  ASSERT_EQ(helix_block_manager_append(m, source, 8, nullptr), HELIX_OK);
-  constexpr int kThreads = 8;
-  struct Owned {
-    helix_sequence seq;
-    std::size_t length;
-  };
-  std::vector<std::vector<Owned>> owned(kThreads);
-  std::vector<int> unexpected(kThreads, 0);
-  std::vector<std::thread> threads;
-  for (int t = 0; t < kThreads; ++t) {
-    threads.emplace_back([&, t] {
-      std::mt19937_64 rng(1000 + t);
-      auto& mine = owned[static_cast<std::size_t>(t)];
-      for (int i = 0; i < 400; ++i) {
-        const int op = static_cast<int>(rng() % 6);
-        if (op == 0 || mine.empty()) {
-          helix_sequence s{};
-          if (helix_block_manager_create_sequence(m, &s) != HELIX_OK) ++unexpected[t];
-          mine.push_back({s, 0});
-        } else if (op == 1) {
-          helix_sequence s{};
-          const int rc = helix_block_manager_fork_sequence(m, source, 8, 0, &s, nullptr);
-          if (rc == HELIX_OK) {
-            mine.push_back({s, 8});
-          } else if (rc != HELIX_RESOURCE_EXHAUSTED) {
-            ++unexpected[t];
-          }
-        } else if (op <= 4) {
-          Owned& o = mine[rng() % mine.size()];
-          const std::size_t n = 1 + rng() % 9;
-          const int rc = helix_block_manager_append(m, o.seq, n, nullptr);
-          if (rc == HELIX_OK) {
-            o.length += n;
-          } else if (rc != HELIX_RESOURCE_EXHAUSTED) {
-            ++unexpected[t];
-          }
-        } else {
-          const std::size_t k = rng() % mine.size();
-          if (helix_block_manager_release_sequence(m, mine[k].seq) != HELIX_OK) ++unexpected[t];
-          mine.erase(mine.begin() + static_cast<std::ptrdiff_t>(k));
-        }
-      }
-    });
-  }
-  for (auto& th : threads) th.join();
-  for (int t = 0; t < kThreads; ++t) EXPECT_EQ(unexpected[static_cast<std::size_t>(t)], 0);
-  EXPECT_EQ(helix_block_manager_validate(m), HELIX_OK);
-  std::map<std::uint32_t, std::size_t> holders;
-  std::size_t live = 1;
-  auto count_table = [&](helix_sequence s) {
-    std::vector<std::uint32_t> ids(64);
-    std::size_t n = 0;
-    EXPECT_EQ(helix_block_manager_block_table(m, s, ids.data(), ids.size(), &n), HELIX_OK);
-    for (std::size_t i = 0; i < n; ++i) ++holders[ids[i]];
-  };
-  count_table(source);
-  for (const auto& mine : owned)
-    for (const Owned& o : mine) {
-      std::size_t len = 0;
-      EXPECT_EQ(helix_block_manager_length(m, o.seq, &len), HELIX_OK);
-      EXPECT_EQ(len, o.length);
-      count_table(o.seq);
-      ++live;
-    }
-  helix_paged_stats st{};
-  EXPECT_EQ(helix_block_manager_stats(m, &st), HELIX_OK);
-  EXPECT_EQ(st.active_sequence_count, live);
-  EXPECT_EQ(st.used_blocks, holders.size());
-  for (const auto& [block, count] : holders) {
-    std::size_t refs = 0, tokens = 0;
-    EXPECT_EQ(helix_block_manager_block_info(m, block, &refs, &tokens), HELIX_OK);
-    EXPECT_EQ(refs, count);
-  }
-  for (const auto& mine : owned)
-    for (const Owned& o : mine) EXPECT_EQ(helix_block_manager_release_sequence(m, o.seq), HELIX_OK);
-  EXPECT_EQ(helix_block_manager_release_sequence(m, source), HELIX_OK);
-  EXPECT_EQ(helix_block_manager_stats(m, &st), HELIX_OK);
-  EXPECT_EQ(st.used_blocks, 0U);
-  EXPECT_EQ(st.free_blocks, 64U);
-  EXPECT_EQ(helix_block_manager_validate(m), HELIX_OK);
-  helix_block_manager_destroy(m);
-}
+#include "host_programs.hpp"
 
 // ------------------------------------------------ golden fixture replay ----
 // tests/golden/paged_cache_scenarios.json: op programs with the reference's
