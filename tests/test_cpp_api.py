@@ -29,4 +29,4 @@ def test_api_binary_runs_host_cases_and_skips_gpu_cases():
     env = dict(os.environ, HIP_VISIBLE_DEVICES="")  # no device here; make it explicit
     r = subprocess.run([BINARY], capture_output=True, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "3 ran, 15 skipped, 0 failed" in r.stdout, r.stdout[-2000:]
+    assert "5 ran, 15 skipped, 0 failed" in r.stdout, r.stdout[-2000:]

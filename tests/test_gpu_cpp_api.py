@@ -23,4 +23,4 @@ def test_cpp_api_suite_passes_on_gpu():
     print(r.stdout[-4000:])
     print(r.stderr[-4000:])
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
-    assert "18 ran, 0 skipped, 0 failed" in r.stdout
+    assert "20 ran, 0 skipped, 0 failed" in r.stdout
