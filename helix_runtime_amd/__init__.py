@@ -507,10 +507,10 @@ def paged_attention_out(query, key_blocks, value_blocks, block_table, kv_tokens,
 def paged_attention_with_tail_out(query, key_blocks, value_blocks, block_table, history_tokens,
                                   tail_key, tail_value, output, score_workspace, stream=None,
                                   logical_blocks=None, probabilities=False):
-    """paged_scaled_dot_product_attention_with_tail_out.  A one-token decode
-    at head_dim 128 / 16-token pages runs the stream decode kernel and uses
-    score_workspace as scratch (content unspecified afterwards);
-    probabilities=True selects the reference's full workspace contract
+    """paged_scaled_dot_product_attention_with_tail_out; score_workspace
+    [q_heads, tail, history + tail] receives the softmax probabilities, as
+    the reference's contract says.  probabilities=True selects the exact
+    scalar kernel for every shape
     (helix_paged_attention_with_tail_probabilities_out)."""
     hq, t, kd = query.shape
     n, hkv, p, vd = value_blocks.shape

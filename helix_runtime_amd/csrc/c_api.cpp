@@ -11,8 +11,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <cstring>
 #include <limits>
 #include <memory>
@@ -536,52 +540,81 @@ void run_reference_attention(const AttentionShape& s, const float* query,
   helix::hip_check(helix::hip::launch_generic(a, stream), (std::string(op) + " launch").c_str());
 }
 
-// The one-token decode through the reference-shaped entry point on the
-// stream kernel: head_dim 128, 16-token pages, a supported query group,
-// 16-byte aligned buffers and a score workspace large enough to hold the
-// partials of at least one wavefront.  The workspace is scratch then.
-// Returns false (nothing launched) when the call does not qualify.
-bool try_stream_decode(const AttentionShape& s, const float* query, const float* key_blocks,
-                       const float* value_blocks, const std::uint32_t* block_table,
-                       const float* tail_key, const float* tail_value, float* output,
-                       float* workspace, std::size_t workspace_elements, hipStream_t stream,
-                       const char* op) {
+// Device scratch of the reference-shaped fast routes, one buffer per
+// (device, stream, purpose): calls on one stream run in order and may share
+// it, calls on different streams get their own.  It grows on demand (the
+// old buffer is freed after the device has drained, which hipFree waits
+// for).  Buffers live until the process ends.
+enum class ScratchUse : int { kDecode = 0, kChunk = 1 };
+void* route_scratch(std::size_t bytes, hipStream_t stream, ScratchUse use) {
+  struct Buffer {
+    void* ptr = nullptr;
+    std::size_t bytes = 0;
+  };
+  static std::mutex mutex;
+  static std::map<std::tuple<int, void*, int>, Buffer> buffers;
+  int device = 0;
+  helix::hip_check(hipGetDevice(&device), "route scratch: hipGetDevice");
+  std::scoped_lock lock(mutex);
+  Buffer& b = buffers[{device, static_cast<void*>(stream), static_cast<int>(use)}];
+  if (b.bytes < bytes) {
+    const std::size_t grown = std::max(bytes, 2 * b.bytes);
+    if (b.ptr != nullptr) {
+      helix::hip_check(hipFree(b.ptr), "route scratch: hipFree");
+      b = Buffer{};
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, grown) != hipSuccess) {
+      (void)hipGetLastError();
+      fail(Status::kResourceExhausted, "route scratch: device allocation failed");
+    }
+    b = Buffer{p, grown};
+  }
+  return b.ptr;
+}
+
+bool aligned16p(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+// The reference-shaped call with one query row on the one-launch decode
+// kernel: head_dim 128, 16-token pages, a supported query group and 16-byte
+// aligned rows.  The score workspace ends up holding the probabilities, as
+// on the reference's own path.  `visible` page tokens, then (tail) the tail
+// row.  Returns false (nothing launched) when the call does not qualify.
+bool try_ref_decode(const AttentionShape& s, const float* query, const float* key_blocks,
+                    const float* value_blocks, const std::uint32_t* block_table,
+                    const float* tail_key, const float* tail_value, float* output,
+                    float* workspace, std::size_t visible, bool tail, hipStream_t stream,
+                    const char* op) {
   namespace hh = helix::hip;
-  if (s.queries != 1 || s.tail != 1 || s.key_dim != hh::kDecodeHeadDim ||
-      s.value_dim != hh::kDecodeHeadDim || s.block_tokens != hh::kDecodeBlockTokens ||
-      s.kv_heads == 0 || s.q_heads % s.kv_heads != 0 ||
-      !hh::decode_group_supported(s.q_heads / s.kv_heads) ||
-      s.physical > std::numeric_limits<std::uint32_t>::max() ||
-      s.history > static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max() / 2)) {
+  if (s.queries != 1 || s.key_dim != hh::kDecodeHeadDim || s.value_dim != hh::kDecodeHeadDim ||
+      s.block_tokens != hh::kDecodeBlockTokens || s.kv_heads == 0 ||
+      s.q_heads % s.kv_heads != 0 || !hh::decode_group_supported(s.q_heads / s.kv_heads) ||
+      s.keys > hh::kRefDecodeMaxKeys) {
     return false;
   }
-  const auto a16 = [](const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; };
-  if (!a16(query) || !a16(key_blocks) || !a16(value_blocks) || !a16(tail_key) ||
-      !a16(tail_value) || !a16(output) || !a16(workspace)) {
+  if (!aligned16p(query) || !aligned16p(output) || (visible > 0 && (!aligned16p(key_blocks) ||
+                                                                   !aligned16p(value_blocks))) ||
+      (tail && (!aligned16p(tail_key) || !aligned16p(tail_value)))) {
     return false;
   }
-  const std::size_t waves =
-      hh::single_decode_waves(s.q_heads, s.kv_heads, workspace_elements * sizeof(float));
-  if (waves == 0) return false;
-  hh::DecodeArgs a{};
+  const hh::RefDecodePlan plan = hh::ref_decode_plan(s.q_heads, s.kv_heads, visible, tail);
+  hh::RefDecodeArgs a{};
   a.query = query;
   a.key_pool = key_blocks;
   a.value_pool = value_blocks;
-  a.tables = block_table;
-  a.lengths = nullptr;
-  a.single_length = static_cast<std::int32_t>(s.history);
-  a.single_waves = waves;
-  a.tail_key = tail_key;
-  a.tail_value = tail_value;
+  a.table = block_table;
+  a.tail_key = tail ? tail_key : nullptr;
+  a.tail_value = tail ? tail_value : nullptr;
   a.out = output;
-  a.workspace = workspace;
-  a.batch = 1;
+  a.probs = workspace;
   a.q_heads = s.q_heads;
   a.kv_heads = s.kv_heads;
-  a.max_blocks = (s.history + s.block_tokens - 1) / s.block_tokens;
   a.physical_blocks = s.physical;
-  a.pages_per_split = 0;
-  helix::hip_check(hh::launch_decode(a, stream), (std::string(op) + " launch").c_str());
+  a.visible = visible;
+  a.keys = s.keys;
+  a.tail = tail;
+  a.scratch = route_scratch(plan.scratch_bytes, stream, ScratchUse::kDecode);
+  helix::hip_check(hh::launch_ref_decode(a, plan, stream), (std::string(op) + " launch").c_str());
   return true;
 }
 
@@ -600,6 +633,15 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
     AttentionShape s{q_heads, queries, key_dim, physical_blocks, kv_heads, block_tokens,
                      value_dim, logical_blocks, kv_tokens, 0, kv_tokens, query_position_offset};
     validate_attention(s, false, op);
+    if (!validate_reference_buffers(s, query, key_blocks, value_blocks, block_table, nullptr,
+                                    nullptr, output, score_workspace, workspace_elements, op)) {
+      return;
+    }
+    if (try_ref_decode(s, query, key_blocks, value_blocks, block_table, nullptr, nullptr, output,
+                       score_workspace, query_position_offset + 1, false, as_stream(stream),
+                       op)) {
+      return;
+    }
     run_reference_attention(s, query, key_blocks, value_blocks, block_table, nullptr, nullptr,
                             output, score_workspace, workspace_elements, as_stream(stream), op);
   });
@@ -628,8 +670,8 @@ void attention_with_tail(const float* query, size_t q_heads, size_t tail_tokens,
                                     tail_value, output, score_workspace, workspace_elements, op)) {
       return;
     }
-    if (try_stream_decode(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
-                          output, score_workspace, workspace_elements, as_stream(stream), op)) {
+    if (try_ref_decode(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
+                       output, score_workspace, history_tokens, true, as_stream(stream), op)) {
       return;
     }
   }

@@ -1934,6 +1934,400 @@ __global__ __launch_bounds__(kThreads) void generic_attention_kernel(GenericArgs
   }
 }
 
+
+// ------------------------------------- reference-shaped one-sequence decode ----
+// paged_scaled_dot_product_attention{,_with_tail}_out with one query row per
+// head (the reference model's per-layer decode call, src/model/
+// cuda_llama.cpp:361-367), in one launch that also leaves the softmax
+// probabilities in the caller's score workspace as the reference does
+// (src/attention/cuda_paged.cu:420-548).
+//
+// Work: the pages of each kv head (its history pages plus, with a tail, one
+// pseudo-page holding the tail row) are cut into chunks of 4 * ppw pages;
+// one workgroup of 4 wavefronts runs one chunk, each wavefront ppw
+// consecutive pages with the stream kernel's lane layout and online
+// softmax, writing every score (log2 domain) to its workspace entry.  The
+// workgroup merges its wavefronts through LDS.  With one workgroup per kv
+// head it finishes in place; otherwise it leaves one partial (m, l, o) per
+// query head in the scratch for ref_decode_merge_kernel.  Finishing means
+// the output rows and the kv head's workspace rows rewritten from scores to
+// probabilities, exp2(x - m) / l with the reference's softmax rules
+// (src/kernels/cpu/reference.cpp:264-316): a NaN score or a row without a
+// finite maximum gives a NaN row, +inf scores share the mass, masked keys
+// get 0.
+struct RefDecodeKernelArgs {
+  const float* query;        // [q_heads, 128]
+  const float* key_pool;     // [physical, kv_heads, 16, 128]
+  const float* value_pool;
+  const std::uint32_t* table;
+  const float* tail_key;     // [kv_heads, 128] or null
+  const float* tail_value;
+  float* out;                // [q_heads, 128]
+  float* probs;              // [q_heads, keys]
+  float4* part_o;            // [kv_heads * chunks, G, 32]
+  float* part_ml;            // [kv_heads * chunks, G, 2]
+  int visible;               // page tokens the query row sees
+  int keys;                  // workspace row length
+  int tail;                  // 1: the tail row is key `visible`
+  int kv_heads;
+  int chunks;                // workgroups per kv head
+  int ppw;                   // pages per wavefront
+  std::uint32_t physical_blocks;
+  float qscale;              // log2(e) / sqrt(128)
+};
+
+template <int G>
+__global__ __launch_bounds__(256) void ref_decode_kernel(RefDecodeKernelArgs a) {
+  constexpr int D = 128;
+  constexpr int P = 16;
+  constexpr int R = G >= 4 ? G / 4 : 1;
+  constexpr int DUPB = G >= 4 ? 0 : (G == 2 ? 1 : 2);
+  constexpr int NV = 8 * G;
+  __shared__ __align__(16) float s_p[4][2][NV];
+  __shared__ float s_alpha[4][G];
+  __shared__ __align__(16) float4 s_o[4][G][32];
+  __shared__ float s_ml[4][G][2];
+  __shared__ float s_fin[G][2];
+
+  const int unit = static_cast<int>(blockIdx.x) / a.chunks;
+  const int chunk = static_cast<int>(blockIdx.x) % a.chunks;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int parity = lane >> 5;
+  const int j = lane & 31;
+  const bool owner = (j & ((1 << DUPB) - 1)) == 0;
+  const int hp = (a.visible + P - 1) / P;
+  const int np = hp + a.tail;
+  const int p0 = (chunk * 4 + w) * a.ppw;
+  const int p1 = min(p0 + a.ppw, np);
+
+  float4 q[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    q[h] = reinterpret_cast<const float4*>(a.query + static_cast<std::size_t>(unit * G + h) * D)[j];
+  }
+  float acc[G][4];
+#pragma unroll
+  for (int h = 0; h < G; ++h) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
+  float m[R], l[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+  }
+  bool bad = false;
+  float* prow = a.probs + static_cast<std::size_t>(unit) * G * a.keys;
+
+  // K/V rows of page p: slot i holds token 2i + parity, dims 4j..4j+3; the
+  // tail pseudo-page holds the tail row in every slot (masked to token 0).
+  auto load = [&](int p, float4 (&k)[8], float4 (&v)[8]) {
+    const bool tail = p >= hp;
+    const bool skip = p >= p1;
+    const void* kb;
+    const void* vb;
+    if (tail) {
+      kb = a.tail_key + static_cast<std::size_t>(unit) * D;
+      vb = a.tail_value + static_cast<std::size_t>(unit) * D;
+    } else {
+      std::uint32_t phys = a.table[p];
+      if (phys >= a.physical_blocks) {
+        bad = true;
+        phys = 0;
+      }
+      const std::size_t off = (static_cast<std::size_t>(phys) * a.kv_heads + unit) * P * D;
+      kb = a.key_pool + off;
+      vb = a.value_pool + off;
+    }
+    const int bytes = skip ? 0 : (tail ? D * 4 : P * D * 4);
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kb), 0, bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vb), 0, bytes, kBufferWord3);
+    const int voff = tail ? j * 16 : lane * 16;
+    const int step = tail ? 0 : 1024;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(kr, voff, i * step, kStreamLoad));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(vr, voff, i * step, kStreamLoad));
+  };
+
+  auto process = [&](int p, const float4 (&k)[8], float4 (&v)[8]) {
+    const bool tail = p >= hp;
+    const int valid = tail ? 1 : min(P, a.visible - p * P);
+    float xs[NV];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        xs[i * G + h] = q[h].x * k[i].x + q[h].y * k[i].y + q[h].z * k[i].z + q[h].w * k[i].w;
+      }
+    }
+    reduce_scores<G>(xs, j);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int vi = (j >> DUPB) * R + r;
+      const int tok = 2 * (vi / G) + parity;
+      const int head = vi % G;
+      const bool ok = tok < valid;
+      const float s = ok ? xs[r] * a.qscale : -INFINITY;
+      if (ok && owner) prow[static_cast<std::size_t>(head) * a.keys + (tail ? a.visible : p * P + tok)] = s;
+      const float mn = fmaxf(m[r], token_max(s));
+      const float alpha = exp2_ratio(m[r], mn);
+      const float pr = ok ? exp2_ratio(s, mn) : 0.0f;
+      l[r] = l[r] * alpha + token_sum(pr);
+      m[r] = mn;
+      if (owner) s_p[w][parity][vi] = pr;
+      if (parity == 0 && vi < G && owner) s_alpha[w][vi] = alpha;
+    }
+    stream_sync<true>();
+    float pp[NV];
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i) {
+      const float4 t4 = reinterpret_cast<const float4*>(s_p[w][parity])[i];
+      pp[4 * i] = t4.x;
+      pp[4 * i + 1] = t4.y;
+      pp[4 * i + 2] = t4.z;
+      pp[4 * i + 3] = t4.w;
+    }
+    float al[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) al[h] = s_alpha[w][h];
+    stream_sync<true>();
+    if (valid < P) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = masked_row(v[i], 2 * i + parity < valid);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      acc[h][0] *= al[h];
+      acc[h][1] *= al[h];
+      acc[h][2] *= al[h];
+      acc[h][3] *= al[h];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float pv = pp[i * G + h];
+        acc[h][0] += pv * v[i].x;
+        acc[h][1] += pv * v[i].y;
+        acc[h][2] += pv * v[i].z;
+        acc[h][3] += pv * v[i].w;
+      }
+    }
+  };
+
+  // Two pages in flight.
+  float4 ka[8], va[8], kb[8], vb[8];
+  for (int p = p0; p < p1; p += 2) {
+    load(p, ka, va);
+    load(p + 1, kb, vb);
+    process(p, ka, va);
+    if (p + 1 < p1) process(p + 1, kb, vb);
+  }
+
+  // This wavefront's partial into LDS (waves without pages leave m = -inf,
+  // l = 0, o = 0), then the workgroup's merge of its four wavefronts.
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[h][c] += half_xor(acc[h][c]);
+  }
+  if (parity == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) s_o[w][h][j] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int vi = (j >> DUPB) * R + r;
+    if (parity == 0 && vi < G && owner) {
+      s_ml[w][vi][0] = m[r];
+      s_ml[w][vi][1] = bad ? NAN : l[r];
+    }
+  }
+  __syncthreads();
+  const int h = tid >> 5;
+  const int d4 = tid & 31;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  float mx = -INFINITY, den = 0.0f;
+  if (h < G) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) mx = fmaxf(mx, s_ml[x][h][0]);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const float wgt = exp2_ratio(s_ml[x][h][0], mx);
+      den += wgt * s_ml[x][h][1];
+      const float4 ox = s_o[x][h][d4];
+      o.x += wgt * ox.x;
+      o.y += wgt * ox.y;
+      o.z += wgt * ox.z;
+      o.w += wgt * ox.w;
+    }
+  }
+  if (a.chunks > 1) {
+    // One partial per head for ref_decode_merge_kernel.
+    const std::size_t slot = static_cast<std::size_t>(unit) * a.chunks + chunk;
+    if (h < G) {
+      a.part_o[(slot * G + h) * 32 + d4] = o;
+      if (d4 == 0) {
+        a.part_ml[(slot * G + h) * 2] = mx;
+        a.part_ml[(slot * G + h) * 2 + 1] = den;
+      }
+    }
+    return;
+  }
+  // Output rows and the final (m, l) of each head.
+  if (h < G) {
+    const bool nan_row = mx == -INFINITY || isnan(den);
+    const float inv = 1.0f / den;
+    const float4 r = nan_row ? make_float4(NAN, NAN, NAN, NAN)
+                             : make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    reinterpret_cast<float4*>(a.out + static_cast<std::size_t>(unit * G + h) * D)[d4] = r;
+    if (d4 == 0) {
+      s_fin[h][0] = mx;
+      s_fin[h][1] = den;
+    }
+  }
+  __syncthreads();
+  // Scores -> probabilities over the kv head's G workspace rows.
+  const int seen = a.visible + a.tail;
+  for (int hh = 0; hh < G; ++hh) {
+    const float fm = s_fin[hh][0];
+    const float fl = s_fin[hh][1];
+    const bool nan_row = fm == -INFINITY || isnan(fl);
+    float* row = prow + static_cast<std::size_t>(hh) * a.keys;
+    for (int k = tid; k < a.keys; k += 256) {
+      float p;
+      if (nan_row) {
+        p = NAN;
+      } else if (k < seen) {
+        p = exp2_ratio(row[k], fm) / fl;
+      } else {
+        p = 0.0f;
+      }
+      row[k] = p;
+    }
+  }
+}
+
+// Finishes a call whose kv heads took several workgroups.  Workgroup
+// (row, s) with row = kv head * G + query head: every workgroup of a row
+// merges the row's (m, l) over the kv head's partials, rewrites its share
+// of the row's workspace entries (kRefNormKeys keys from s * kRefNormKeys)
+// from scores to probabilities, and workgroup s = 0 also merges the output
+// row (eight groups of 32 threads over the partials, combined through LDS).
+// All loads of a step are issued together: the data was written by other
+// XCDs in the previous launch, so every round trip goes to memory.  The
+// split of ref_decode_kernel and this merge into two launches is
+// deliberate: merging in the last workgroup to finish would need a
+// device-scope release per workgroup, which on a multi-XCD part writes back
+// the L2 each time (measured: 63 us per config-3 call in one launch).
+constexpr int kRefNormUnroll = static_cast<int>(kRefNormKeys / 256);
+
+template <int G>
+__global__ __launch_bounds__(256) void ref_decode_merge_kernel(RefDecodeKernelArgs a) {
+  constexpr int D = 128;
+  constexpr int kOPer = 8;  // partials per group loaded in the first round
+  __shared__ float s_red[4];
+  __shared__ __align__(16) float4 s_o[8][32];
+  const int row = blockIdx.x;
+  const int unit = row / G;
+  const int h = row % G;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const bool out_group = blockIdx.y == 0;
+  const std::size_t slot0 = static_cast<std::size_t>(unit) * a.chunks;
+  auto ml = [&](int c, int i) { return a.part_ml[((slot0 + c) * G + h) * 2 + i]; };
+  const int g = tid >> 5;
+  const int d4 = tid & 31;
+  auto part_o = [&](int c) { return a.part_o[((slot0 + c) * G + h) * 32 + d4]; };
+
+  // One round of loads: this share's scores, the first (m, l) pair per
+  // thread and (output workgroup) the first kOPer partial rows per group.
+  const int seen = a.visible + a.tail;
+  float* prow = a.probs + static_cast<std::size_t>(row) * a.keys;
+  const int k0 = static_cast<int>(blockIdx.y) * static_cast<int>(kRefNormKeys) + tid;
+  float x[kRefNormUnroll];
+#pragma unroll
+  for (int u = 0; u < kRefNormUnroll; ++u) {
+    const int k = k0 + u * 256;
+    x[u] = k < seen ? prow[k] : 0.0f;
+  }
+  const float m0 = tid < a.chunks ? ml(tid, 0) : -INFINITY;
+  const float l0 = tid < a.chunks ? ml(tid, 1) : 0.0f;
+  float4 oc[kOPer];
+  float om[kOPer];
+#pragma unroll
+  for (int i = 0; i < kOPer; ++i) {
+    const int c = g + 8 * i;
+    const bool in = out_group && c < a.chunks;
+    om[i] = in ? ml(c, 0) : -INFINITY;
+    oc[i] = in ? part_o(c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  // Final (m, l) of the row: maximum, then the rescaled sum.
+  float mx = m0;
+  for (int c = tid + 256; c < a.chunks; c += 256) mx = fmaxf(mx, ml(c, 0));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) s_red[wv] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  float den = tid < a.chunks ? exp2_ratio(m0, mx) * l0 : 0.0f;
+  for (int c = tid + 256; c < a.chunks; c += 256) den += exp2_ratio(ml(c, 0), mx) * ml(c, 1);
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  if (lane == 0) s_red[wv] = den;
+  __syncthreads();
+  den = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  const bool nan_row = mx == -INFINITY || isnan(den);
+
+  if (out_group) {
+    // Output row: group g takes partials g, g + 8, ...
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < kOPer; ++i) {
+      const float w1 = g + 8 * i < a.chunks ? exp2_ratio(om[i], mx) : 0.0f;
+      o.x += w1 * oc[i].x;
+      o.y += w1 * oc[i].y;
+      o.z += w1 * oc[i].z;
+      o.w += w1 * oc[i].w;
+    }
+    for (int c = g + 8 * kOPer; c < a.chunks; c += 8) {
+      const float w1 = exp2_ratio(ml(c, 0), mx);
+      const float4 v = part_o(c);
+      o.x += w1 * v.x;
+      o.y += w1 * v.y;
+      o.z += w1 * v.z;
+      o.w += w1 * v.w;
+    }
+    s_o[g][d4] = o;
+    __syncthreads();
+    if (tid < 32) {
+      float4 r = s_o[0][tid];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        r.x += s_o[i][tid].x;
+        r.y += s_o[i][tid].y;
+        r.z += s_o[i][tid].z;
+        r.w += s_o[i][tid].w;
+      }
+      const float inv = 1.0f / den;
+      r = nan_row ? make_float4(NAN, NAN, NAN, NAN)
+                  : make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+      reinterpret_cast<float4*>(a.out + static_cast<std::size_t>(row) * D)[tid] = r;
+    }
+  }
+
+  // This workgroup's share of the row: scores -> probabilities.
+#pragma unroll
+  for (int u = 0; u < kRefNormUnroll; ++u) {
+    const int k = k0 + u * 256;
+    if (k < a.keys) prow[k] = nan_row ? NAN : (k < seen ? exp2_ratio(x[u], mx) / den : 0.0f);
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------ launchers ----
@@ -2491,6 +2885,95 @@ std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
     }
   }
   return lo;
+}
+
+namespace {
+
+// CUs of the current device, looked up once per device.
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      n = 256;
+    }
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+}  // namespace
+
+RefDecodePlan ref_decode_plan(std::size_t q_heads, std::size_t kv_heads, std::size_t visible,
+                              bool tail) {
+  RefDecodePlan p{};
+  if (kv_heads == 0 || q_heads % kv_heads != 0) return p;
+  const std::size_t group = q_heads / kv_heads;
+  const std::size_t pages = (visible + kDecodeBlockTokens - 1) / kDecodeBlockTokens + (tail ? 1 : 0);
+  // About eight wavefronts per CU over the whole call, whole pages each.
+  const std::size_t target = static_cast<std::size_t>(device_cus()) * 8;
+  const std::size_t total = kv_heads * pages;
+  p.ppw = total <= target ? 1 : (total + target - 1) / target;
+  p.chunks = (pages + 4 * p.ppw - 1) / (4 * p.ppw);
+  if (p.chunks == 0) p.chunks = 1;
+  const std::size_t slots = p.chunks > 1 ? kv_heads * p.chunks : 0;
+  p.scratch_bytes = align256(slots * group * 2 * sizeof(float)) +
+                    slots * group * kDecodeHeadDim * sizeof(float);
+  return p;
+}
+
+hipError_t launch_ref_decode(const RefDecodeArgs& a, const RefDecodePlan& plan,
+                             hipStream_t stream) {
+  if (a.q_heads == 0) return hipSuccess;
+  const std::size_t group = a.q_heads / a.kv_heads;
+  auto* ws = static_cast<unsigned char*>(a.scratch);
+  const std::size_t slots = a.kv_heads * plan.chunks;
+  RefDecodeKernelArgs k{};
+  k.query = a.query;
+  k.key_pool = a.key_pool;
+  k.value_pool = a.value_pool;
+  k.table = a.table;
+  k.tail_key = a.tail_key;
+  k.tail_value = a.tail_value;
+  k.out = a.out;
+  k.probs = a.probs;
+  k.part_ml = reinterpret_cast<float*>(ws);
+  k.part_o = reinterpret_cast<float4*>(ws + align256(slots * group * 2 * sizeof(float)));
+  k.visible = static_cast<int>(a.visible);
+  k.keys = static_cast<int>(a.keys);
+  k.tail = a.tail ? 1 : 0;
+  k.kv_heads = static_cast<int>(a.kv_heads);
+  k.chunks = static_cast<int>(plan.chunks);
+  k.ppw = static_cast<int>(plan.ppw);
+  k.physical_blocks = static_cast<std::uint32_t>(a.physical_blocks);
+  k.qscale = kLog2e / sqrtf(static_cast<float>(kDecodeHeadDim));
+  const dim3 grid(static_cast<unsigned>(slots));
+  switch (group) {
+    case 1: ref_decode_kernel<1><<<grid, 256, 0, stream>>>(k); break;
+    case 2: ref_decode_kernel<2><<<grid, 256, 0, stream>>>(k); break;
+    case 4: ref_decode_kernel<4><<<grid, 256, 0, stream>>>(k); break;
+    case 8: ref_decode_kernel<8><<<grid, 256, 0, stream>>>(k); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || plan.chunks == 1) return e;
+  if (a.between_event != nullptr) {
+    e = hipEventRecord(a.between_event, stream);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 mgrid(static_cast<unsigned>(a.q_heads),
+                   static_cast<unsigned>((a.keys + kRefNormKeys - 1) / kRefNormKeys));
+  switch (group) {
+    case 1: ref_decode_merge_kernel<1><<<mgrid, 256, 0, stream>>>(k); break;
+    case 2: ref_decode_merge_kernel<2><<<mgrid, 256, 0, stream>>>(k); break;
+    case 4: ref_decode_merge_kernel<4><<<mgrid, 256, 0, stream>>>(k); break;
+    case 8: ref_decode_merge_kernel<8><<<mgrid, 256, 0, stream>>>(k); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_generic(const GenericArgs& a, hipStream_t stream) {

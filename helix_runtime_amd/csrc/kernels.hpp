@@ -200,6 +200,46 @@ std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_head
 std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
                                 std::size_t workspace_bytes);
 
+// ------------------------------------- reference-shaped one-sequence decode ----
+// One query row per head (the reference's per-layer model call) over pages of
+// head_dim 128 and 16 tokens, query groups 1/2/4/8, in one launch that also
+// leaves the softmax probabilities in the score workspace [q_heads, keys]
+// as the reference does: keys [0, visible) from the pages, then with `tail`
+// the tail row as key `visible`; keys past those get probability 0.
+struct RefDecodeArgs {
+  const float* query;        // [q_heads, 128]
+  const float* key_pool;     // [physical_blocks, kv_heads, 16, 128]
+  const float* value_pool;
+  const std::uint32_t* table;  // ceil(visible / 16) entries
+  const float* tail_key;     // [kv_heads, 128] when tail
+  const float* tail_value;
+  float* out;                // [q_heads, 128]
+  float* probs;              // [q_heads, keys]
+  std::size_t q_heads, kv_heads, physical_blocks;
+  std::size_t visible, keys;
+  bool tail;
+  // ref_decode_plan(...).scratch_bytes of device memory for the partials of
+  // calls that take more than one workgroup per kv head (those then run a
+  // second, merging launch).  Calls that share a scratch must run in order
+  // (one stream).
+  void* scratch;
+  // Optional: recorded between the two launches (timing of the first).
+  hipEvent_t between_event = nullptr;
+};
+struct RefDecodePlan {
+  std::size_t chunks = 0;        // workgroups per kv head
+  std::size_t ppw = 0;           // pages per wavefront
+  std::size_t scratch_bytes = 0;
+};
+// Workspace keys one merging workgroup normalises, and the longest row the
+// route takes (the merge grid's second dimension stays within 65535).
+constexpr std::size_t kRefNormKeys = 2048;
+constexpr std::size_t kRefDecodeMaxKeys = 65535 * kRefNormKeys;
+RefDecodePlan ref_decode_plan(std::size_t q_heads, std::size_t kv_heads, std::size_t visible,
+                              bool tail);
+hipError_t launch_ref_decode(const RefDecodeArgs& a, const RefDecodePlan& plan,
+                             hipStream_t stream);
+
 // ------------------------------------------------------------ generic ----
 // Reference-shaped paged attention for any geometry (one query row per
 // workgroup).  Materialises probabilities into workspace [q_heads, queries,

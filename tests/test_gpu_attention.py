@@ -319,7 +319,16 @@ def test_decode_rejects_bad_arguments(device):
                                   dev(lengths), dev(tk), dev(tv), out, small, 1)
 
 
-# ------------------------------- reference-shaped entry, stream-kernel route ----
+# ------------------------------ reference-shaped entry, one-launch decode route ----
+# One query row per head at head_dim 128 and 16-token pages (the reference
+# model's per-layer call, src/model/cuda_llama.cpp:361-367) runs the
+# one-launch decode kernel; the score workspace still ends up holding the
+# softmax probabilities, as the reference's contract says
+# (tests/cuda_attention_test.cpp:441-443).  Outputs within 2e-5 + 1e-4 rel
+# of the oracle, probabilities within the reference's 2e-6.
+PROB_ATOL = 2e-6
+
+
 def single_decode_problem(seed, hkv, g, hist, spare=3):
     rng = np.random.default_rng(seed)
     logical = (hist + 15) // 16
@@ -333,56 +342,99 @@ def single_decode_problem(seed, hkv, g, hist, spare=3):
     return table, kp, vp, q, tk, tv
 
 
-def oracle_single(q, kp, vp, table, hist, tk, tv):
-    tables = np.zeros((1, max(len(table), 1)), np.uint32)
-    tables[0, : len(table)] = table
-    return oracle.batched_decode(q[:, 0][None], kp, vp, tables, np.array([hist], np.int32),
-                                 tk[:, 0][None], tv[:, 0][None])[0]
+def run_single(q, kp, vp, table, hist, tk, tv, stream=None, probabilities=False, ws_fill=7.0):
+    out = torch.full((q.shape[0], 1, 128), 5.0, device="cuda:0")
+    ws = torch.full((q.shape[0], 1, hist + 1), ws_fill, device="cuda:0")
+    tab = dev(table.astype(np.int32)) if len(table) else 0
+    args = (dev(q), dev(kp), dev(vp), tab, hist, dev(tk), dev(tv), out, ws)
+    torch.cuda.synchronize()  # the inputs are ready for a call on another stream
+    hx.paged_attention_with_tail_out(*args, stream=stream, probabilities=probabilities)
+    torch.cuda.synchronize()
+    return host(out), host(ws)
 
 
 @pytest.mark.parametrize("hkv,g", [(8, 4), (32, 1), (4, 2), (2, 8)])
-@pytest.mark.parametrize("hist", [0, 1, 150, 257, 1000, 2770, 8192])
-def test_with_tail_decode_routes_match_oracle(device, hkv, g, hist):
-    """The reference model's per-layer call (one token, head_dim 128,
-    16-token pages): from about 150 history tokens on the score workspace is
-    large enough for the stream kernel's partials and the call runs it;
-    below, the exact kernel runs.  Either way the output matches the oracle
-    within 2e-5 + 1e-4 rel, and the probability-contract variant still
-    fills the workspace."""
+@pytest.mark.parametrize("hist", [0, 1, 15, 16, 150, 257, 1000, 2770, 8192])
+def test_with_tail_decode_route_matches_oracle(device, hkv, g, hist):
+    """Output and probabilities against the oracle for every query group and
+    history lengths around page edges; a second call on the same buffers is
+    bit-identical (the kernel's per-kv-head tickets reset themselves), and
+    the exact probability variant agrees."""
     table, kp, vp, q, tk, tv = single_decode_problem(hist + 7 * g, hkv, g, hist)
-    ref = oracle_single(q, kp, vp, table, hist, tk, tv)
-    out = torch.empty(hkv * g, 1, 128, device=device)
-    ws = torch.full((hkv * g, 1, hist + 1), 7.0, device=device)
-    tab = dev(table.astype(np.int32)) if len(table) else 0
-    args = (dev(q), dev(kp), dev(vp), tab, hist, dev(tk), dev(tv), out, ws)
-    hx.paged_attention_with_tail_out(*args)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    out, ws = run_single(q, kp, vp, table, hist, tk, tv)
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
+    out2, ws2 = run_single(q, kp, vp, table, hist, tk, tv, ws_fill=-3.0)
+    np.testing.assert_array_equal(out2, out)
+    np.testing.assert_array_equal(ws2, ws)
+    if hist <= 1000:
+        out3, ws3 = run_single(q, kp, vp, table, hist, tk, tv, probabilities=True)
+        np.testing.assert_allclose(out3, exp_out, atol=2e-5 + 128e-6, rtol=0)
+        np.testing.assert_allclose(ws3, exp_ws, atol=PROB_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("kv,offset", [(1, 0), (40, 0), (40, 17), (1000, 999), (1000, 500),
+                                       (3001, 1234)])
+def test_history_decode_route_matches_oracle(device, kv, offset):
+    """paged_scaled_dot_product_attention_out with one query row at position
+    `offset` of kv_tokens keys: keys past the position get probability 0."""
+    table, kp, vp, q, _, _ = single_decode_problem(kv + offset, 8, 4, kv)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, kv, query_position_offset=offset)
+    out = torch.full((32, 1, 128), 5.0, device=device)
+    ws = torch.full((32, 1, kv), 7.0, device=device)
+    hx.paged_attention_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), kv, offset,
+                           out, ws)
     torch.cuda.synchronize()
-    np.testing.assert_allclose(host(out)[:, 0], ref, atol=ATOL, rtol=RTOL)
-    first = host(out).copy()
-    hx.paged_attention_with_tail_out(*args)  # deterministic on a reused workspace
-    torch.cuda.synchronize()
-    np.testing.assert_array_equal(host(out), first)
-    if g == 1:
-        hx.paged_attention_with_tail_out(*args, probabilities=True)
-        torch.cuda.synchronize()
-        exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
-        np.testing.assert_allclose(host(out), exp_out, atol=2e-5 + 128e-6, rtol=0)
-        np.testing.assert_allclose(host(ws), exp_ws, atol=2e-6, rtol=0)
+    np.testing.assert_allclose(host(out), exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(host(ws), exp_ws, atol=PROB_ATOL, rtol=0)
+
+
+def test_decode_route_special_values(device):
+    """The reference softmax rules on the one-launch route
+    (src/kernels/cpu/reference.cpp:264-316): +inf scores share the mass, a
+    NaN score makes its row NaN, other rows are untouched."""
+    hist = 700
+    table, kp, vp, q, tk, tv = single_decode_problem(41, 8, 4, hist)
+    kp = kp.copy()
+    q[:, 0, :] = np.abs(q[:, 0, :]) + 0.1
+    for tok in (3, 650):  # kv head 0: two +inf keys
+        kp[table[tok // 16], 0, tok % 16, :] = np.inf
+    kp[table[321 // 16], 2, 321 % 16, 9] = np.nan  # kv head 2: one NaN key element
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    out, ws = run_single(q, kp, vp, table, hist, tk, tv)
+    assert np.isnan(out[8:12]).all() and np.isnan(ws[8:12]).all()
+    assert (ws[0:4, 0, 3] == 0.5).all() and (ws[0:4, 0, 650] == 0.5).all()
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
 
 
 def test_with_tail_decode_route_bad_page_is_nan(device):
-    """A page ID past the pool yields NaN on the stream route too, and is
-    never dereferenced (cuda_paged.cu:58-61)."""
+    """A page ID past the pool yields NaN output and probabilities, and is
+    never dereferenced (cuda_paged.cu:58-61); other kv heads are unaffected
+    only through the output shape (the reference poisons the whole call's
+    rows that read the page: every kv head reads it)."""
     hist = 1000
     table, kp, vp, q, tk, tv = single_decode_problem(5, 8, 4, hist)
     table = table.copy()
     table[17] = kp.shape[0] + 5
-    out = torch.empty(32, 1, 128, device=device)
-    ws = torch.empty(32, 1, hist + 1, device=device)
-    hx.paged_attention_with_tail_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), hist,
-                                     dev(tk), dev(tv), out, ws)
-    torch.cuda.synchronize()
-    assert np.isnan(host(out)).all()
+    out, ws = run_single(q, kp, vp, table, hist, tk, tv)
+    assert np.isnan(out).all() and np.isnan(ws).all()
+
+
+def test_decode_route_calls_on_two_streams_and_changing_sizes(device):
+    """Alternating history lengths on one stream, then the same calls on a
+    second stream: each call's scratch (partials and tickets) is its
+    stream's own and left clean for the next call."""
+    s2 = torch.cuda.Stream()
+    cases = [single_decode_problem(60 + i, 8, 4, h) + (h,) for i, h in
+             enumerate([5000, 40, 8192, 700, 0, 3333])]
+    for stream in (None, s2):
+        for table, kp, vp, q, tk, tv, hist in cases:
+            exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+            out, ws = run_single(q, kp, vp, table, hist, tk, tv, stream=stream)
+            np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+            np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
 
 
 def test_with_tail_decode_route_config3_batch_as_calls(device):
@@ -393,10 +445,7 @@ def test_with_tail_decode_route_config3_batch_as_calls(device):
     for i in range(8):
         hist = int(np.exp(rng.uniform(math.log(512), math.log(8192))))
         table, kp, vp, q, tk, tv = single_decode_problem(300 + i, 8, 4, hist)
-        ref = oracle_single(q, kp, vp, table, hist, tk, tv)
-        out = torch.empty(32, 1, 128, device=device)
-        ws = torch.empty(32, 1, hist + 1, device=device)
-        hx.paged_attention_with_tail_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)),
-                                         hist, dev(tk), dev(tv), out, ws)
-        torch.cuda.synchronize()
-        np.testing.assert_allclose(host(out)[:, 0], ref, atol=ATOL, rtol=RTOL)
+        exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+        out, ws = run_single(q, kp, vp, table, hist, tk, tv)
+        np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
