@@ -618,6 +618,91 @@ bool try_ref_decode(const AttentionShape& s, const float* query, const float* ke
   return true;
 }
 
+// Whether a reference-shaped call with several query rows (a prefill
+// chunk) fits the exact matrix-core prefill kernel: head_dim 128, 16-token
+// pages, a supported query group, 16-byte aligned rows and index ranges the
+// kernel's 32-bit arithmetic holds.
+bool ref_prefill_fits(const AttentionShape& s, const float* query, const float* output,
+                      const float* key_blocks, const float* value_blocks, std::size_t history,
+                      std::size_t prob_keys) {
+  namespace hh = helix::hip;
+  constexpr auto kIntMax = static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max());
+  return s.queries >= 2 && s.key_dim == hh::kDecodeHeadDim &&
+         s.value_dim == hh::kDecodeHeadDim && s.block_tokens == hh::kDecodeBlockTokens &&
+         s.kv_heads != 0 && s.q_heads % s.kv_heads == 0 &&
+         hh::prefill_group_supported(s.q_heads / s.kv_heads) && prob_keys <= kIntMax / 2 &&
+         s.queries * s.kv_heads <= kIntMax && aligned16p(query) && aligned16p(output) &&
+         (history == 0 || (aligned16p(key_blocks) && aligned16p(value_blocks)));
+}
+
+// Such a call on that kernel, which also leaves the probabilities in the
+// workspace: query row q sees the `history` page tokens and chunk rows
+// 0..q; workspace rows are `prob_keys` long.
+void run_ref_prefill(const AttentionShape& s, const float* query, const float* key_blocks,
+                     const float* value_blocks, const std::uint32_t* block_table,
+                     const float* chunk_key, const float* chunk_value, float* output,
+                     float* workspace, std::size_t history, std::size_t prob_keys,
+                     hipStream_t stream, const char* op) {
+  namespace hh = helix::hip;
+  hh::PrefillArgs a{};
+  a.query = query;
+  a.key_pool = key_blocks;
+  a.value_pool = value_blocks;
+  a.tables = block_table;
+  a.lengths = nullptr;
+  a.single_length = static_cast<std::int32_t>(history);
+  a.chunk_key = chunk_key;
+  a.chunk_value = chunk_value;
+  a.out = output;
+  a.batch = 1;
+  a.q_heads = s.q_heads;
+  a.kv_heads = s.kv_heads;
+  a.tokens = s.queries;
+  a.max_blocks = (history + hh::kDecodeBlockTokens - 1) / hh::kDecodeBlockTokens;
+  a.physical_blocks = s.physical;
+  a.probs = workspace;
+  a.prob_keys = prob_keys;
+  helix::hip_check(hh::launch_prefill(a, stream), (std::string(op) + " launch").c_str());
+}
+
+// _with_tail_out with several tail rows: the tail is the chunk.
+bool try_ref_prefill(const AttentionShape& s, const float* query, const float* key_blocks,
+                     const float* value_blocks, const std::uint32_t* block_table,
+                     const float* tail_key, const float* tail_value, float* output,
+                     float* workspace, hipStream_t stream, const char* op) {
+  if (!ref_prefill_fits(s, query, output, key_blocks, value_blocks, s.history, s.keys) ||
+      !aligned16p(tail_key) || !aligned16p(tail_value)) {
+    return false;
+  }
+  run_ref_prefill(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value, output,
+                  workspace, s.history, s.keys, stream, op);
+  return true;
+}
+
+// _out with several query rows: page rows [offset, offset + queries) are
+// gathered into this stream's scratch as the chunk (history = offset).
+bool try_ref_history_prefill(const AttentionShape& s, const float* query,
+                             const float* key_blocks, const float* value_blocks,
+                             const std::uint32_t* block_table, float* output, float* workspace,
+                             hipStream_t stream, const char* op) {
+  namespace hh = helix::hip;
+  if (!ref_prefill_fits(s, query, output, key_blocks, value_blocks, s.offset, s.keys) ||
+      !aligned16p(key_blocks) || !aligned16p(value_blocks)) {
+    return false;
+  }
+  const std::size_t rows = mul(mul(s.kv_heads, s.queries), hh::kDecodeHeadDim);
+  auto* chunk = static_cast<float*>(
+      route_scratch(mul(rows, 2 * sizeof(float)), stream, ScratchUse::kChunk));
+  const hh::PageGeometry g{s.physical, s.kv_heads, s.block_tokens, s.key_dim};
+  helix::hip_check(hh::launch_gather(key_blocks, value_blocks, g, block_table, s.queries, chunk,
+                                     chunk + rows, s.queries, stream, hh::PageFormat(),
+                                     s.offset),
+                   (std::string(op) + " gather").c_str());
+  run_ref_prefill(s, query, key_blocks, value_blocks, block_table, chunk, chunk + rows, output,
+                  workspace, s.offset, s.keys, stream, op);
+  return true;
+}
+
 }  // namespace
 
 int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries, size_t key_dim,
@@ -639,7 +724,9 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
     }
     if (try_ref_decode(s, query, key_blocks, value_blocks, block_table, nullptr, nullptr, output,
                        score_workspace, query_position_offset + 1, false, as_stream(stream),
-                       op)) {
+                       op) ||
+        try_ref_history_prefill(s, query, key_blocks, value_blocks, block_table, output,
+                                score_workspace, as_stream(stream), op)) {
       return;
     }
     run_reference_attention(s, query, key_blocks, value_blocks, block_table, nullptr, nullptr,
@@ -671,7 +758,9 @@ void attention_with_tail(const float* query, size_t q_heads, size_t tail_tokens,
       return;
     }
     if (try_ref_decode(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
-                       output, score_workspace, history_tokens, true, as_stream(stream), op)) {
+                       output, score_workspace, history_tokens, true, as_stream(stream), op) ||
+        try_ref_prefill(s, query, key_blocks, value_blocks, block_table, tail_key, tail_value,
+                        output, score_workspace, as_stream(stream), op)) {
       return;
     }
   }

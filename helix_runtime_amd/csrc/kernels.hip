@@ -260,13 +260,14 @@ __global__ void rope_kernel(RopeSegment s0, RopeSegment s1, unsigned rows, unsig
 }
 
 // Reference: PagedKvCache copy_layer / copy_layer_prefix_out
-// (src/kv_cache/paged.cpp:242-280, 895-950).
+// (src/kv_cache/paged.cpp:242-280, 895-950).  Tokens [first, first + length)
+// of the sequence land at rows [0, length) of the outputs.
 template <typename S, int W>
 __global__ void gather_kernel(const S* __restrict__ key_pool, const S* __restrict__ value_pool,
                               std::size_t heads, std::size_t block_tokens, std::size_t dim,
                               const std::uint32_t* __restrict__ blocks, std::size_t length,
                               float* keys_out, float* values_out, std::size_t dest_tokens,
-                              float2 scale) {
+                              float2 scale, std::size_t first) {
   const std::size_t dv = dim / W;
   const std::size_t total = heads * length * dv;
   const S* pool = blockIdx.y == 0 ? key_pool : value_pool;
@@ -278,9 +279,10 @@ __global__ void gather_kernel(const S* __restrict__ key_pool, const S* __restric
     const std::size_t ht = e / dv;
     const std::size_t t = ht % length;
     const std::size_t h = ht / length;
-    const std::size_t phys = blocks[t / block_tokens];
+    const std::size_t src = first + t;
+    const std::size_t phys = blocks[src / block_tokens];
     Elems<S, W>::get(out + (h * dest_tokens + t) * dim + c * W,
-                     pool + ((phys * heads + h) * block_tokens + t % block_tokens) * dim + c * W,
+                     pool + ((phys * heads + h) * block_tokens + src % block_tokens) * dim + c * W,
                      sc);
   }
 }
@@ -466,7 +468,6 @@ struct DecodeKernelArgs {
   const std::int64_t* append_slots;
   float* append_key_pool;
   float* append_value_pool;
-  int single_length;  // history of the one sequence when lengths is not used
   // fp8 pages: scales of the key and value codes (the key scale is also
   // folded into qscale).
   float k_scale;
@@ -1015,7 +1016,7 @@ __device__ __forceinline__ void stream_sync() {
 
 // The body of one stream wavefront: `wave` is its index among
 // a.stream_waves, `lane` its lane, `sh` its LDS.
-template <int G, bool APPEND, int PF, bool SHARED_BLOCK, bool SINGLE = false, int S = kStreamStage>
+template <int G, bool APPEND, int PF, bool SHARED_BLOCK, int S = kStreamStage>
 __device__ __forceinline__ void decode_stream_body(
     DecodeKernelArgs a, const std::uint32_t* __restrict__ tables,
     const std::int32_t* __restrict__ lengths, float* __restrict__ out,
@@ -1067,12 +1068,7 @@ __device__ __forceinline__ void decode_stream_body(
 #pragma unroll
   for (int c = 0; c < kScanChunks; ++c) {
     const int bb = c * 64 + lane;
-    if constexpr (SINGLE) {
-      // One sequence whose length is a kernel argument.
-      histc[c] = bb < a.batch ? clamp_length(a.single_length, a.max_blocks) : -1;
-    } else {
-      histc[c] = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
-    }
+    histc[c] = bb < a.batch ? clamp_length(a.lengths[bb], a.max_blocks) : -1;
   }
   long long lane_pages = 0;
 #pragma unroll
@@ -1081,7 +1077,7 @@ __device__ __forceinline__ void decode_stream_body(
     lane_pages += npc[c];
   }
   long long per_head = wave_sum(lane_pages);
-  if (!SINGLE && a.batch > kScanChunks * 64) {
+  if (a.batch > kScanChunks * 64) {
     per_head += stream_pages_between(a, kScanChunks * 64, a.batch, lane);
   }
   per_head = uniform64(per_head);
@@ -1164,7 +1160,7 @@ __device__ __forceinline__ void decode_stream_body(
       if (cur.g < g1) {
         cur.b = __builtin_amdgcn_readfirstlane(cur.b);
         cur.hist = __builtin_amdgcn_readfirstlane(
-            clamp_length(SINGLE ? a.single_length : a.lengths[cur.b], a.max_blocks));
+            clamp_length(a.lengths[cur.b], a.max_blocks));
         cur.np = unit_pages(cur.hist, a.first_page);
       }
     }
@@ -1630,7 +1626,7 @@ __device__ __forceinline__ void decode_stream_body(
   flush();
 }
 
-template <int G, bool APPEND, int PF, bool SINGLE = false>
+template <int G, bool APPEND, int PF>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     G > 4 ? 1 : (stream_lds_query<PF, G>() ? kFp8StreamWaves : 2))))
 void decode_stream_kernel(
@@ -1651,7 +1647,7 @@ void decode_stream_kernel(
   __shared__ __align__(16) float4 s_app_v[S][32];
   __shared__ long long s_app_dst[S];
   __shared__ __align__(16) float4 s_qslot[QLDS ? 3 : 1][G][32];
-  decode_stream_body<G, APPEND, PF, false, SINGLE, S>(
+  decode_stream_body<G, APPEND, PF, false, S>(
       a, tables, lengths, out, part_o, part_ml, segments, append_slots, blockIdx.x, threadIdx.x,
       StreamLds<G, S>{s_p, s_head, s_res_o, s_res_ml, s_res_dst, s_seg, s_seg_unit, s_app_k,
                       s_app_v, s_app_dst, QLDS ? s_qslot : nullptr});
@@ -2447,7 +2443,7 @@ hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t row
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
                          float* values_out, std::size_t dest_tokens, hipStream_t stream,
-                         PageFormat type) {
+                         PageFormat type, std::size_t first_token) {
   if (length == 0) return hipSuccess;
   const bool vec = g.head_dim % 4 == 0 && aligned16(keys_out) && aligned16(values_out);
   const std::size_t work = g.kv_heads * length * (vec ? g.head_dim / 4 : g.head_dim);
@@ -2456,7 +2452,7 @@ hipError_t launch_gather(const void* key_pool, const void* value_pool, const Pag
     using S = decltype(s);
     gather_kernel<S, decltype(w)::value><<<grid, kThreads, 0, stream>>>(
         as_pages<S>(key_pool), as_pages<S>(value_pool), g.kv_heads, g.block_tokens, g.head_dim,
-        blocks, length, keys_out, values_out, dest_tokens, scales(type));
+        blocks, length, keys_out, values_out, dest_tokens, scales(type), first_token);
   });
 }
 
@@ -2565,15 +2561,9 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 
 namespace {
 
-// Wavefronts the stream kernel launches: every resident slot of the device
-// (fp32 and bf16 pages: two per SIMD up to four query heads per kv head, one
-// for eight; fp8 pages: four per SIMD up to four query heads, as the
-// kernels' register and LDS use allows), at most kMaxStreamWaves.
-// beside_prefix: one per SIMD whatever the group, so the concurrent cascade
-// prefix pass finds registers on every SIMD.
-std::size_t stream_waves(std::size_t group, bool beside_prefix,
-                         PageType type = PageType::kF32) {
-  // CU count per device, looked up once; host threads may launch at once.
+// CUs of the current device, looked up once per device (host threads may
+// launch at once).
+int device_cus() {
   static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -2585,6 +2575,19 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix,
     }
     cus[dev].store(n, std::memory_order_relaxed);
   }
+  return n;
+}
+
+
+// Wavefronts the stream kernel launches: every resident slot of the device
+// (fp32 and bf16 pages: two per SIMD up to four query heads per kv head, one
+// for eight; fp8 pages: four per SIMD up to four query heads, as the
+// kernels' register and LDS use allows), at most kMaxStreamWaves.
+// beside_prefix: one per SIMD whatever the group, so the concurrent cascade
+// prefix pass finds registers on every SIMD.
+std::size_t stream_waves(std::size_t group, bool beside_prefix,
+                         PageType type = PageType::kF32) {
+  const int n = device_cus();
   const std::size_t per_simd =
       group >= 8 || beside_prefix ? 1 : (stream_lds_query_type(type) ? kFp8StreamWaves : 2);
   const std::size_t w = static_cast<std::size_t>(n) * 4 * per_simd;
@@ -2595,9 +2598,9 @@ std::size_t stream_waves(std::size_t group, bool beside_prefix,
 
 namespace {
 
-template <int G, bool APPEND, int PF, bool SINGLE = false>
+template <int G, bool APPEND, int PF>
 void launch_stream_variant(const dim3& grid, hipStream_t stream, const DecodeKernelArgs& k) {
-  decode_stream_kernel<G, APPEND, PF, SINGLE><<<grid, 64, 0, stream>>>(
+  decode_stream_kernel<G, APPEND, PF><<<grid, 64, 0, stream>>>(
       k, k.tables, k.lengths, k.out, k.part_o, k.part_ml, k.segments,
       APPEND ? k.append_slots : nullptr);
 }
@@ -2676,43 +2679,7 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   k.v_scale = a.page_type.v_scale;
   // fp8 keys widen to bare code values: their scale joins the score scale.
   if (a.page_type.type == PageType::kFP8) k.qscale *= a.page_type.k_scale;
-  if (a.lengths == nullptr) {
-    // One sequence, history length passed by value, the caller's workspace
-    // laid out for single_waves wavefronts.
-    if (a.batch != 1 || !streamed || a.single_waves == 0 || a.shared_pages != 0 ||
-        a.append_slots != nullptr || a.page_type.type != PageType::kF32) {
-      return hipErrorInvalidValue;
-    }
-    const WorkspaceLayout lay = stream_layout(1, a.q_heads, a.kv_heads, a.single_waves, 0);
-    k.part_o = reinterpret_cast<float*>(ws + lay.part_o);
-    k.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
-    k.segments = reinterpret_cast<int*>(ws + lay.segments);
-    k.single_length = a.single_length;
-    k.stream_waves = static_cast<int>(a.single_waves);
-    const dim3 grid(static_cast<unsigned>(a.single_waves));
-    switch (group) {
-      case 1: launch_stream_variant<1, false, 0, true>(grid, stream, k); break;
-      case 2: launch_stream_variant<2, false, 0, true>(grid, stream, k); break;
-      case 4: launch_stream_variant<4, false, 0, true>(grid, stream, k); break;
-      case 8: launch_stream_variant<8, false, 0, true>(grid, stream, k); break;
-      default: return hipErrorInvalidValue;
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (a.between_event != nullptr) {
-      e = hipEventRecord(a.between_event, stream);
-      if (e != hipSuccess) return e;
-    }
-    const dim3 mgrid(static_cast<unsigned>(a.kv_heads));
-    switch (group) {
-      case 1: decode_stream_merge_kernel<1><<<mgrid, 1 * 32, 0, stream>>>(k); break;
-      case 2: decode_stream_merge_kernel<2><<<mgrid, 2 * 32, 0, stream>>>(k); break;
-      case 4: decode_stream_merge_kernel<4><<<mgrid, 4 * 32, 0, stream>>>(k); break;
-      case 8: decode_stream_merge_kernel<8><<<mgrid, 8 * 32, 0, stream>>>(k); break;
-      default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-  }
+  if (a.lengths == nullptr) return hipErrorInvalidValue;
   if (streamed) {
     // Cascade in one launch for groups up to kCascadeFusedMaxGroup (the
     // stream LDS of four wavefronts then fits beside a prefix workgroup's,
@@ -2868,44 +2835,6 @@ std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_head
   return stream_layout(batch, q_heads, kv_heads, stream_waves(q_heads / kv_heads, false), 0).total;
 }
 
-std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
-                                std::size_t workspace_bytes) {
-  if (kv_heads == 0 || q_heads % kv_heads != 0) return 0;
-  const std::size_t group = q_heads / kv_heads;
-  std::size_t w = stream_waves(group, false);
-  // The layout grows with the wave count: take the largest count that fits.
-  if (stream_layout(1, q_heads, kv_heads, w, 0).total <= workspace_bytes) return w;
-  std::size_t lo = 0, hi = w;
-  while (lo < hi) {
-    const std::size_t mid = (lo + hi + 1) / 2;
-    if (stream_layout(1, q_heads, kv_heads, mid, 0).total <= workspace_bytes) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
-    }
-  }
-  return lo;
-}
-
-namespace {
-
-// CUs of the current device, looked up once per device.
-int device_cus() {
-  static std::atomic<int> cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int n = cus[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0) {
-      n = 256;
-    }
-    cus[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
-}  // namespace
 
 RefDecodePlan ref_decode_plan(std::size_t q_heads, std::size_t kv_heads, std::size_t visible,
                               bool tail) {

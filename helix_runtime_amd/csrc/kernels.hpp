@@ -88,11 +88,12 @@ hipError_t launch_rope(const RopeTensor& a, const RopeTensor& b, std::size_t row
                        std::size_t head_dim, const float* cosine, const float* sine,
                        std::size_t cache_rows, const std::int32_t* positions, hipStream_t stream);
 
-// Gather one layer of one sequence into fp32 [kv_heads, dest_tokens, dim].
+// Gather one layer of one sequence into fp32 [kv_heads, dest_tokens, dim]:
+// tokens [first_token, first_token + length) to rows [0, length).
 hipError_t launch_gather(const void* key_pool, const void* value_pool, const PageGeometry& g,
                          const std::uint32_t* blocks, std::size_t length, float* keys_out,
                          float* values_out, std::size_t dest_tokens, hipStream_t stream,
-                         PageFormat type = PageFormat());
+                         PageFormat type = PageFormat(), std::size_t first_token = 0);
 
 // Copy the first `tokens` token rows of block `from` into block `to` for
 // every layer and head (copy-on-write of a partial shared page).
@@ -160,12 +161,6 @@ struct DecodeArgs {
   const std::int64_t* append_slots = nullptr;
   float* append_key_pool = nullptr;
   float* append_value_pool = nullptr;
-  // One sequence whose history length is a host value (the reference-shaped
-  // entry point): lengths == nullptr, batch == 1, stream mode, no cascade.
-  // The stream kernel then runs `single_waves` wavefronts with the partials
-  // laid out for that count (single_decode_layout) in `workspace`.
-  std::int32_t single_length = 0;
-  std::size_t single_waves = 0;
   // Stream mode without a cascade: partials laid out for the launch's own
   // wavefront count (compact_decode_workspace_bytes) instead of the
   // worst-case layout of decode_workspace_bytes.
@@ -194,11 +189,6 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
 // Workspace of a stream-mode decode with compact_layout (no cascade).
 std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_heads,
                                            std::size_t kv_heads);
-// Stream wavefronts a one-sequence decode can run with a caller workspace of
-// `workspace_bytes` (the partial slots of that many wavefronts must fit),
-// capped at the device's resident count; 0 when none fit.
-std::size_t single_decode_waves(std::size_t q_heads, std::size_t kv_heads,
-                                std::size_t workspace_bytes);
 
 // ------------------------------------- reference-shaped one-sequence decode ----
 // One query row per head (the reference's per-layer model call) over pages of
@@ -287,6 +277,13 @@ struct PrefillArgs {
   // special value (a NaN score, a non-finite value row that some row
   // masks); the words are written by the launch itself.
   std::uint32_t* redo = nullptr;
+  // One sequence whose history is a host value: lengths == nullptr.
+  std::int32_t single_length = 0;
+  // fp32 pages, exact kernel: also write the softmax probabilities of every
+  // query row to probs [q_heads, tokens, prob_keys] (batch 1), 0 for keys
+  // the row does not see -- the reference's score workspace contract.
+  float* probs = nullptr;
+  std::size_t prob_keys = 0;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of

@@ -21,6 +21,17 @@ void prefill_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ table
   prefill_body<G, CASCADE, PF, RT>(a, tables, order, blockIdx.x, sh);
 }
 
+// The exact kernel that also leaves the softmax probabilities (the
+// reference-shaped chunk call, fp32 pages).
+template <int G>
+__global__ __launch_bounds__(512 / kTilesPerWave, 6 - 2 * kTilesPerWave)
+void prefill_probs_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__ tables,
+                          const std::uint32_t* __restrict__ order) {
+  __shared__ PrefillShared sh;
+  prefill_body<G, false, 0, kTilesPerWave, false, PrefillShared, true>(a, tables, order,
+                                                                       blockIdx.x, sh);
+}
+
 // The exact kernel over the blocks the matrix-core launch flagged (every
 // other block returns at once).
 template <int G, int PF, int RT>
@@ -149,7 +160,22 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.batch = static_cast<int>(a.batch);
   k.k_scale = a.page_type.k_scale;
   k.v_scale = a.page_type.v_scale;
+  k.single_length = a.single_length;
+  k.probs = a.probs;
+  k.prob_keys = static_cast<int>(a.prob_keys);
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
+  if (a.probs != nullptr) {
+    if (a.page_type.type != PageType::kF32 || a.redo != nullptr) return hipErrorInvalidValue;
+    constexpr unsigned threads = 512 / kTilesPerWave;
+    switch (group) {
+      case 1: prefill_probs_kernel<1><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
+      case 2: prefill_probs_kernel<2><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
+      case 4: prefill_probs_kernel<4><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
+      case 8: prefill_probs_kernel<8><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (a.redo != nullptr && a.page_type.type == PageType::kF32) {
     switch (group) {
       case 1: launch_fast<1>(grid, stream, k, a.tables, a.order, a.redo); break;

@@ -98,6 +98,14 @@ struct PrefillKernelArgs {
   // fp8 pages: scales of the key and value codes.
   float k_scale;
   float v_scale;
+  // History of a one-sequence launch whose length is a host value
+  // (lengths == nullptr).
+  int single_length;
+  // Probabilities (the PROBS kernels): row (head * tokens + position) of
+  // probs, prob_keys entries long, receives the softmax probabilities of
+  // that query row over keys [0, prob_keys); keys the row does not see get 0.
+  float* probs;
+  int prob_keys;
 };
 
 // exp2(a - b), with a == b (also +inf == +inf, -inf == -inf) giving 1 and
@@ -197,13 +205,22 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 // probability, or the exact result is NaN anyway) is flagged in
 // redo[block] for the exact kernel.  Without the exact path the kernel
 // fits one 16-row tile per wavefront at four wavefronts per SIMD.
-template <int G, bool CASCADE, int PF, int RT, bool FAST = false, class Shared>
+// PROBS (the reference-shaped chunk call): every score the rows see is
+// written (log2 domain) to its probability entry as it is computed, and
+// once the rows' final maxima and sums are known each lane rewrites the
+// entries it wrote into probabilities and fills the keys its rows do not
+// see (0, or NaN on a NaN row), following the reference's softmax rules
+// (src/kernels/cpu/reference.cpp:264-316).  Every entry is read back only
+// by the lane that wrote it.
+template <int G, bool CASCADE, int PF, int RT, bool FAST = false, class Shared,
+          bool PROBS = false>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
                                              const std::uint32_t* __restrict__ tables,
                                              const std::uint32_t* __restrict__ order,
                                              std::uint32_t block, Shared& sh,
                                              std::uint32_t* __restrict__ redo = nullptr) {
   static_assert(!FAST || !CASCADE, "the fast prefill is the standalone one");
+  static_assert(!PROBS || (!FAST && !CASCADE), "probabilities come from the exact kernel");
   constexpr int PW = kRows / G;  // chunk positions per workgroup
   constexpr bool BF16 = PF == 1;
   constexpr bool FP8 = PF == 2;
@@ -252,7 +269,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   const int T = a.tokens;
   const int pos0 = pb * PW;
 
-  int hist = CASCADE ? a.cascade_keys : a.lengths[b];
+  int hist = CASCADE ? a.cascade_keys : (a.lengths != nullptr ? a.lengths[b] : a.single_length);
   bool bad = hist < 0 || hist > a.max_blocks * P;
   if (bad) hist = 0;
   const int key_begin = CASCADE ? chunk * a.cascade_chunk_pages * P : 0;
@@ -268,6 +285,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   int qpos[RT];
   bool qvalid[RT];
   std::size_t qrow[RT];
+  int r_head[RT];  // query head within the kv head's group (PROBS)
   float4 q[RT][8];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
@@ -280,6 +298,7 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       qrow[t] = (static_cast<std::size_t>(qvalid[t] ? seq : 0) * a.q_heads + kvh * G + row % G) * D;
     } else {
       const int head = kvh * G + r / PW;
+      r_head[t] = r / PW;
       qpos[t] = pos0 + r % PW;
       qvalid[t] = qpos[t] < T;
       qrow[t] = ((static_cast<std::size_t>(b) * a.q_heads + head) * T + qpos[t]) * D;
@@ -565,6 +584,17 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
           vis[i] = FULL || (key < key_end && (key < hist || key - hist <= qpos[t]));
           x[i] = vis[i] ? st[t][i] : -INFINITY;
         }
+        if constexpr (PROBS) {
+          if (qvalid[t]) {
+            float* pr = a.probs + (static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t]) *
+                                      static_cast<std::size_t>(a.prob_keys);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = n * kKeys + 4 * grp + i;
+              if (key < key_end) pr[key] = x[i];
+            }
+          }
+        }
         const float mx = row_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
         const float mn = fmaxf(m[t], mx);
         const float alpha = exp2_ratio(m[t], mn);
@@ -690,6 +720,23 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
       }
     }
     return;
+  }
+  if constexpr (PROBS) {
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      if (qpos[t] >= T) continue;
+      const bool nan_row = any_bad || m[t] == -INFINITY || isnan(l[t]);
+      float* pr = a.probs + (static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t]) *
+                                static_cast<std::size_t>(a.prob_keys);
+      for (int n = nfirst; n < nblocks; ++n) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = n * kKeys + 4 * grp + i;
+          if (key < key_end) pr[key] = nan_row ? NAN : exp2_ratio(pr[key], m[t]) / l[t];
+        }
+      }
+      for (int key = key_end + grp; key < a.prob_keys; key += 4) pr[key] = nan_row ? NAN : 0.0f;
+    }
   }
 #pragma unroll
   for (int t = 0; t < RT; ++t) {

@@ -449,3 +449,96 @@ def test_with_tail_decode_route_config3_batch_as_calls(device):
         out, ws = run_single(q, kp, vp, table, hist, tk, tv)
         np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
+
+
+# ------------------------------ reference-shaped entry, matrix-core chunk route ----
+# Several query rows at head_dim 128 and 16-token pages (the reference's
+# chunked-prefill call through the same entry points) run the exact fp32
+# matrix-core prefill kernel, which also leaves the probabilities.
+def chunk_problem(seed, hkv, g, hist, T, spare=3):
+    rng = np.random.default_rng(seed)
+    logical = (hist + 15) // 16
+    phys = logical + spare
+    table = rng.permutation(phys)[:logical].astype(np.uint32)
+    kp = rng.standard_normal((phys, hkv, 16, 128), dtype=np.float32)
+    vp = rng.standard_normal((phys, hkv, 16, 128), dtype=np.float32)
+    q = rng.standard_normal((hkv * g, T, 128), dtype=np.float32)
+    tk = rng.standard_normal((hkv, T, 128), dtype=np.float32)
+    tv = rng.standard_normal((hkv, T, 128), dtype=np.float32)
+    return table, kp, vp, q, tk, tv
+
+
+def run_chunk(q, kp, vp, table, hist, tk, tv, probabilities=False):
+    hq, T, _ = q.shape
+    out = torch.full((hq, T, 128), 5.0, device="cuda:0")
+    ws = torch.full((hq, T, hist + T), 7.0, device="cuda:0")
+    tab = dev(table.astype(np.int32)) if len(table) else 0
+    hx.paged_attention_with_tail_out(dev(q), dev(kp), dev(vp), tab, hist, dev(tk), dev(tv), out,
+                                     ws, probabilities=probabilities)
+    torch.cuda.synchronize()
+    return host(out), host(ws)
+
+
+@pytest.mark.parametrize("T,hist", [(2, 0), (2, 1000), (2, 4096), (37, 0), (37, 1000),
+                                    (37, 4096), (512, 0), (512, 1000), (512, 4096)])
+def test_with_tail_chunk_route_matches_oracle(device, T, hist):
+    """Config-5 geometry (32 query / 8 kv heads) chunks of 2, 37 and 512 rows
+    over histories of 0, 1000 and 4096 tokens: outputs and the probability
+    workspace against the oracle."""
+    table, kp, vp, q, tk, tv = chunk_problem(T * 7 + hist, 8, 4, hist, T)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    out, ws = run_chunk(q, kp, vp, table, hist, tk, tv)
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("hkv,g", [(32, 1), (4, 2), (2, 8)])
+def test_with_tail_chunk_route_every_group(device, hkv, g):
+    table, kp, vp, q, tk, tv = chunk_problem(90 + g, hkv, g, 333, 70)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, 333, tk, tv)
+    out, ws = run_chunk(q, kp, vp, table, 333, tk, tv)
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
+    out2, ws2 = run_chunk(q, kp, vp, table, 333, tk, tv, probabilities=True)
+    np.testing.assert_allclose(out2, exp_out, atol=2e-5 + 128e-6, rtol=0)
+    np.testing.assert_allclose(ws2, ws, atol=PROB_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("kv,offset,nq", [(40, 0, 40), (300, 100, 37), (1000, 488, 512),
+                                          (2000, 16, 2), (700, 650, 50)])
+def test_history_chunk_route_matches_oracle(device, kv, offset, nq):
+    """paged_scaled_dot_product_attention_out with several query rows at
+    positions offset .. offset + nq - 1 of kv_tokens keys: the rows' own
+    keys come from the pages, keys past a row's position get 0."""
+    table, kp, vp, q, _, _ = chunk_problem(kv + offset + nq, 8, 4, kv, nq)
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, kv, query_position_offset=offset)
+    out = torch.full((32, nq, 128), 5.0, device=device)
+    ws = torch.full((32, nq, kv), 7.0, device=device)
+    hx.paged_attention_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), kv, offset,
+                           out, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(host(out), exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(host(ws), exp_ws, atol=PROB_ATOL, rtol=0)
+
+
+def test_chunk_route_special_values(device):
+    """+inf and NaN keys in the history, a non-finite value row in the chunk
+    that earlier rows mask, and a bad page ID in a second call."""
+    hist, T = 300, 40
+    table, kp, vp, q, tk, tv = chunk_problem(17, 8, 4, hist, T)
+    kp = kp.copy()
+    q[:4] = np.abs(q[:4]) + 0.1
+    for tok in (7, 250):  # kv head 0: two +inf keys every row sees
+        kp[table[tok // 16], 0, tok % 16, :] = np.inf
+    kp[table[100 // 16], 3, 100 % 16, 2] = np.nan  # kv head 3: NaN rows
+    tv[5, 20, 7] = np.inf                           # kv head 5: rows 0-19 must not see it
+    exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+    out, ws = run_chunk(q, kp, vp, table, hist, tk, tv)
+    assert np.isnan(out[12:16]).all() and np.isnan(ws[12:16]).all()
+    assert np.isfinite(out[20:24, :20]).all()
+    np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0)
+    table = table.copy()
+    table[5] = kp.shape[0] + 9
+    out, ws = run_chunk(q, kp, vp, table, hist, tk, tv)
+    assert np.isnan(out).all() and np.isnan(ws).all()
