@@ -457,6 +457,114 @@ def run_reference_entry(args):
     cache.close()
 
 
+def run_reference_chunk(args):
+    """The reference-shaped chunk call at config-5 shape: the reference runs
+    chunked prefill through the same entry point as decode
+    (attention::cuda::paged_scaled_dot_product_attention_with_tail_out with a
+    T-token tail, include/helix/attention/cuda_paged.hpp:49-53), one sequence
+    per call, so a layer of config 5 is 16 calls, each with that sequence's
+    block table, its [32, 512, 128] query, [8, 512, 128] chunk and a
+    [32, 512, history + 512] score workspace that receives the
+    probabilities.  Here those calls run the exact fp32 matrix-core prefill
+    kernel (prefill_probs_kernel).  The exact scalar route
+    (helix_paged_attention_with_tail_probabilities_out, the generic kernel)
+    is timed on two of the calls beside it."""
+    rng = np.random.default_rng(args.seed + 50)
+    hists = rng.integers(0, 4097, size=CHUNK_BATCH)
+    T = CHUNK_TOKENS
+    n_phys = int(((hists + P - 1) // P).sum() + 16)
+    cache = hx.PagedKvCache(1, HKV, D, P, n_phys)
+    tok = torch.zeros(1, HKV, D, device="cuda:0")
+    dummies = []
+    for _ in range(n_phys):
+        s = cache.create_sequence()
+        cache.append(s, tok, tok)
+        dummies.append(s)
+    for i in rng.permutation(len(dummies)):
+        cache.release_sequence(dummies[int(i)])
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(args.seed)
+    seqs = []
+    for b in range(CHUNK_BATCH):
+        s = cache.create_sequence()
+        n = int(hists[b])
+        if n:
+            cache.append_layer_major(s, [torch.randn(HKV, n, D, device="cuda:0", generator=gen)],
+                                     [torch.randn(HKV, n, D, device="cuda:0", generator=gen)])
+        seqs.append(s)
+    kptr, vptr = cache.layer_pool_pointers(0)
+
+    class _Pool(_DevicePointer):
+        shape = (cache.physical_blocks, HKV, P, D)
+
+    kpool, vpool = _Pool(kptr), _Pool(vptr)
+    tables = [torch.tensor(cache.block_table(s) or [0], dtype=torch.int32, device="cuda:0")
+              for s in seqs]
+    q = torch.randn(CHUNK_BATCH, HQ, T, D, device="cuda:0", generator=gen)
+    ck = torch.randn(CHUNK_BATCH, HKV, T, D, device="cuda:0", generator=gen)
+    cv = torch.randn(CHUNK_BATCH, HKV, T, D, device="cuda:0", generator=gen)
+    out = torch.empty(CHUNK_BATCH, HQ, T, D, device="cuda:0")
+    ws = [torch.empty(HQ, T, int(n) + T, device="cuda:0") for n in hists]
+    stream = torch.cuda.current_stream()
+
+    def call(b, probabilities=False):
+        hx.paged_attention_with_tail_out(q[b], kpool, vpool, tables[b], int(hists[b]), ck[b],
+                                         cv[b], out[b], ws[b], stream,
+                                         probabilities=probabilities)
+
+    def layer(e0, e1, which=range(CHUNK_BATCH), probabilities=False):
+        torch.cuda._sleep(20_000_000)
+        e0.record(stream)
+        for b in which:
+            call(b, probabilities)
+        e1.record(stream)
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(args.warmup):
+        layer(e0, e1)
+    torch.cuda.synchronize()
+    layer_ms = []
+    for _ in range(args.steps):
+        layer(e0, e1)
+        torch.cuda.synchronize()
+        layer_ms.append(e0.elapsed_time(e1))
+    ms = float(np.mean(layer_ms))
+    flops = prefill_flops(hists)
+    tflops = flops / (ms * 1e-3) / 1e12
+    exact = [int(np.argmin(hists)), int(np.argsort(hists)[CHUNK_BATCH // 2])]
+    layer(e0, e1, exact, True)
+    torch.cuda.synchronize()
+    exact_ms = e0.elapsed_time(e1)
+    exact_tflops = prefill_flops(hists[exact]) / (exact_ms * 1e-3) / 1e12
+    prob_bytes = float(sum(HQ * T * (int(n) + T) * 4 for n in hists))
+    line = {
+        "metric": "reference-shaped chunk call (one call per sequence) TFLOP/s (fp32 MFMA, "
+                  "probabilities written), 8B-GQA 16 x 512-token chunks",
+        "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic N(0,1) K/V/Q, seeded; pages shuffled across the pool",
+        "config": {"workload": "config5 chunks attended through "
+                               "paged_scaled_dot_product_attention_with_tail_out: 16 calls per "
+                               "layer, 32q/8kv heads, head_dim 128, page 16, 512-token tails",
+                   "batch": CHUNK_BATCH, "chunk_tokens": T,
+                   "mean_history": float(hists.mean())},
+        "layer_avg_us": round(ms * 1e3, 2),
+        "call_avg_us": round(ms * 1e3 / CHUNK_BATCH, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None},
+        "probability_bytes_per_layer": prob_bytes,
+        "exact_route_calls": exact,
+        "exact_route_us": round(exact_ms * 1e3, 2),
+        "exact_route_tflops": round(exact_tflops, 4),
+        "exact_route_note": "generic kernel (helix_paged_attention_with_tail_probabilities_out) "
+                            "on the shortest and the median history",
+    }
+    print(json.dumps(line), flush=True)
+    cache.close()
+
+
 def run_tiny(args):
     """Config 1: the tiny reference-shaped decode (1 sequence, 4/4 heads,
     head_dim 16, 16-token pages, a 64-token history in 4 pages drawn by a
@@ -918,6 +1026,9 @@ def main():
     ap.add_argument("--model-step", action="store_true",
                     help="a whole Llama-3-8B-shaped decode step (torch dense ops, library KV "
                          "path): the integrated flow against the reference's per-layer order")
+    ap.add_argument("--chunk", action="store_true",
+                    help="with --reference-entry: the config-5 chunk call through the "
+                         "reference-shaped entry point")
     ap.add_argument("--reference-entry", action="store_true",
                     help="time the reference-shaped per-sequence decode entry point at config-3 "
                          "shape (64 calls per layer) instead of the batched step")
@@ -946,6 +1057,9 @@ def main():
         return
     if args.model_step:
         run_model_step(args)
+        return
+    if args.reference_entry and args.chunk:
+        run_reference_chunk(args)
         return
     if args.reference_entry:
         run_reference_entry(args)

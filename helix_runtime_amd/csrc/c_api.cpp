@@ -545,7 +545,7 @@ void run_reference_attention(const AttentionShape& s, const float* query,
 // it, calls on different streams get their own.  It grows on demand (the
 // old buffer is freed after the device has drained, which hipFree waits
 // for).  Buffers live until the process ends.
-enum class ScratchUse : int { kDecode = 0, kChunk = 1 };
+enum class ScratchUse : int { kDecode = 0, kChunk = 1, kRowStats = 2 };
 void* route_scratch(std::size_t bytes, hipStream_t stream, ScratchUse use) {
   struct Buffer {
     void* ptr = nullptr;
@@ -662,6 +662,8 @@ void run_ref_prefill(const AttentionShape& s, const float* query, const float* k
   a.physical_blocks = s.physical;
   a.probs = workspace;
   a.prob_keys = prob_keys;
+  a.prob_ml = static_cast<float*>(route_scratch(mul(mul(s.q_heads, s.queries), 2 * sizeof(float)),
+                                                stream, ScratchUse::kRowStats));
   helix::hip_check(hh::launch_prefill(a, stream), (std::string(op) + " launch").c_str());
 }
 

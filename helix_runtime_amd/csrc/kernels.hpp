@@ -279,11 +279,15 @@ struct PrefillArgs {
   std::uint32_t* redo = nullptr;
   // One sequence whose history is a host value: lengths == nullptr.
   std::int32_t single_length = 0;
-  // fp32 pages, exact kernel: also write the softmax probabilities of every
-  // query row to probs [q_heads, tokens, prob_keys] (batch 1), 0 for keys
-  // the row does not see -- the reference's score workspace contract.
+  // fp32 pages, exact kernel, one sequence: also write the softmax
+  // probabilities of every query row to probs [q_heads, tokens, prob_keys],
+  // 0 for keys the row does not see -- the reference's score workspace
+  // contract (a second launch turns the written scores into probabilities).
   float* probs = nullptr;
   std::size_t prob_keys = 0;
+  // With probs (one sequence, lengths == nullptr): scratch of q_heads *
+  // tokens * 2 floats for each row's final maximum and sum.
+  float* prob_ml = nullptr;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of

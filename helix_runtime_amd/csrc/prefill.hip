@@ -32,6 +32,37 @@ void prefill_probs_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__
                                                                        blockIdx.x, sh);
 }
 
+// Scores -> probabilities of the reference-shaped chunk call: workgroup
+// (row, s) rewrites keys [s * 2048, s * 2048 + 2048) of workspace row `row`
+// (q head * tokens + position): keys the row sees, [0, history + position
+// + 1), become exp2(x - m) / l, the rest 0; a row without a finite maximum
+// or with a NaN sum is NaN throughout (src/kernels/cpu/reference.cpp:
+// 264-316).  Eight loads per thread are in flight at once.
+constexpr int kNormUnroll = 8;
+__global__ __launch_bounds__(256) void prob_normalize_kernel(float* __restrict__ probs,
+                                                             const float* __restrict__ ml,
+                                                             int tokens, int history, int keys) {
+  const std::size_t row = blockIdx.x;
+  const int pos = static_cast<int>(row % static_cast<std::size_t>(tokens));
+  const int seen = history + pos + 1;
+  const float m = ml[row * 2];
+  const float l = ml[row * 2 + 1];
+  const bool nan_row = m == -INFINITY || isnan(l);
+  float* pr = probs + row * static_cast<std::size_t>(keys);
+  const int k0 = static_cast<int>(blockIdx.y) * 256 * kNormUnroll + threadIdx.x;
+  float x[kNormUnroll];
+#pragma unroll
+  for (int u = 0; u < kNormUnroll; ++u) {
+    const int k = k0 + u * 256;
+    x[u] = k < seen ? pr[k] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kNormUnroll; ++u) {
+    const int k = k0 + u * 256;
+    if (k < keys) pr[k] = nan_row ? NAN : (k < seen ? exp2_ratio(x[u], m) / l : 0.0f);
+  }
+}
+
 // The exact kernel over the blocks the matrix-core launch flagged (every
 // other block returns at once).
 template <int G, int PF, int RT>
@@ -163,9 +194,13 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.single_length = a.single_length;
   k.probs = a.probs;
   k.prob_keys = static_cast<int>(a.prob_keys);
+  k.prob_ml = a.prob_ml;
   const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   if (a.probs != nullptr) {
-    if (a.page_type.type != PageType::kF32 || a.redo != nullptr) return hipErrorInvalidValue;
+    if (a.page_type.type != PageType::kF32 || a.redo != nullptr || a.batch != 1 ||
+        a.lengths != nullptr || a.prob_ml == nullptr) {
+      return hipErrorInvalidValue;
+    }
     constexpr unsigned threads = 512 / kTilesPerWave;
     switch (group) {
       case 1: prefill_probs_kernel<1><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
@@ -174,6 +209,15 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
       case 8: prefill_probs_kernel<8><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
       default: return hipErrorInvalidValue;
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 ngrid(static_cast<unsigned>(a.q_heads * a.tokens),
+                     static_cast<unsigned>((a.prob_keys + 256 * kNormUnroll - 1) /
+                                           (256 * kNormUnroll)));
+    prob_normalize_kernel<<<ngrid, 256, 0, stream>>>(a.probs, a.prob_ml,
+                                                     static_cast<int>(a.tokens),
+                                                     a.single_length,
+                                                     static_cast<int>(a.prob_keys));
     return hipGetLastError();
   }
   if (a.redo != nullptr && a.page_type.type == PageType::kF32) {

@@ -49,6 +49,7 @@
 namespace helix::hip::prefill_detail {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v4f_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int D = 128;
 constexpr int P = 16;
@@ -106,6 +107,7 @@ struct PrefillKernelArgs {
   // that query row over keys [0, prob_keys); keys the row does not see get 0.
   float* probs;
   int prob_keys;
+  float* prob_ml;  // [rows, 2]: each row's final maximum and sum
 };
 
 // exp2(a - b), with a == b (also +inf == +inf, -inf == -inf) giving 1 and
@@ -205,13 +207,11 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 // probability, or the exact result is NaN anyway) is flagged in
 // redo[block] for the exact kernel.  Without the exact path the kernel
 // fits one 16-row tile per wavefront at four wavefronts per SIMD.
-// PROBS (the reference-shaped chunk call): every score the rows see is
-// written (log2 domain) to its probability entry as it is computed, and
-// once the rows' final maxima and sums are known each lane rewrites the
-// entries it wrote into probabilities and fills the keys its rows do not
-// see (0, or NaN on a NaN row), following the reference's softmax rules
-// (src/kernels/cpu/reference.cpp:264-316).  Every entry is read back only
-// by the lane that wrote it.
+// PROBS (the reference-shaped chunk call): every score of the rows' keys
+// [0, key_end) is written (log2 domain, -inf where masked) to its
+// probability entry as it is computed, and each row's final maximum and sum
+// (sum NaN for a row of a work item that met a bad page) go to prob_ml;
+// prob_normalize_kernel then turns the scores into probabilities.
 template <int G, bool CASCADE, int PF, int RT, bool FAST = false, class Shared,
           bool PROBS = false>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
@@ -588,10 +588,16 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
           if (qvalid[t]) {
             float* pr = a.probs + (static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t]) *
                                       static_cast<std::size_t>(a.prob_keys);
+            const int key = n * kKeys + 4 * grp;
+            if (key + 4 <= key_end) {
+              // Rows are prob_keys floats long: the four keys are 4-byte
+              // aligned only; one dwordx4 store either way.
+              *reinterpret_cast<v4f_a4*>(pr + key) = v4f_a4{x[0], x[1], x[2], x[3]};
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = n * kKeys + 4 * grp + i;
-              if (key < key_end) pr[key] = x[i];
+              for (int i = 0; i < 4; ++i) {
+                if (key + i < key_end) pr[key + i] = x[i];
+              }
             }
           }
         }
@@ -724,18 +730,10 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   if constexpr (PROBS) {
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      if (qpos[t] >= T) continue;
-      const bool nan_row = any_bad || m[t] == -INFINITY || isnan(l[t]);
-      float* pr = a.probs + (static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t]) *
-                                static_cast<std::size_t>(a.prob_keys);
-      for (int n = nfirst; n < nblocks; ++n) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = n * kKeys + 4 * grp + i;
-          if (key < key_end) pr[key] = nan_row ? NAN : exp2_ratio(pr[key], m[t]) / l[t];
-        }
-      }
-      for (int key = key_end + grp; key < a.prob_keys; key += 4) pr[key] = nan_row ? NAN : 0.0f;
+      if (qpos[t] >= T || grp != 0) continue;
+      const std::size_t row = static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t];
+      a.prob_ml[row * 2] = m[t];
+      a.prob_ml[row * 2 + 1] = any_bad ? NAN : l[t];
     }
   }
 #pragma unroll
