@@ -243,7 +243,10 @@ int helix_paged_tail_score_workspace_bytes(size_t q_heads, size_t tail_tokens, s
                                            size_t physical_blocks, size_t block_tokens,
                                            size_t logical_blocks, size_t history_tokens,
                                            size_t* out);
-/* paged_scaled_dot_product_attention_out (cuda_paged.cu:420-481). */
+/* paged_scaled_dot_product_attention_out (cuda_paged.cu:420-481).  Routes as
+ * helix_paged_attention_with_tail_out: one query row on the one-launch
+ * decode kernel, several on the matrix-core prefill kernel (the rows' own
+ * page tokens gathered into the stream's scratch as the chunk). */
 int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries, size_t key_dim,
                               const float* key_blocks, const float* value_blocks,
                               size_t physical_blocks, size_t kv_heads, size_t block_tokens,
@@ -256,15 +259,15 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
  * tail_key [kv_heads, tail_tokens, key_dim], tail_value [kv_heads,
  * tail_tokens, value_dim]; query row q sees the history and tail rows 0..q.
  * The reference model's per-layer decode call (src/model/cuda_llama.cpp:
- * 365-367).  A one-token decode (tail_tokens 1) with key_dim = value_dim =
- * 128, 16-token pages, q_heads / kv_heads in {1, 2, 4, 8} and 16-byte aligned
- * buffers runs on the persistent stream decode kernel when score_workspace
- * can hold that kernel's partial results for at least one wavefront (from a
- * history of about 150 tokens on; more history, more wavefronts).  The
- * workspace is scratch then and its content after the call is unspecified.
- * Every other call runs the exact reference-shaped kernel, which leaves the
- * probabilities in the workspace.  Callers that read the probabilities
- * use helix_paged_attention_with_tail_probabilities_out. */
+ * 365-367).  The workspace receives the probabilities on every route, as in
+ * the reference.  With key_dim = value_dim = 128, 16-token pages, q_heads /
+ * kv_heads in {1, 2, 4, 8} and 16-byte aligned rows, a one-token call runs
+ * the one-launch decode kernel (plus a merging launch when a kv head spans
+ * several workgroups) and a call with several tail rows (a prefill chunk)
+ * runs the exact fp32 matrix-core prefill kernel plus a normalisation
+ * launch; both use a device scratch the library keeps per (device, stream),
+ * allocated or grown on first use.  Every other call runs the exact scalar
+ * kernel. */
 int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size_t tail_tokens,
                                         size_t key_dim, const float* key_blocks,
                                         const float* value_blocks, size_t physical_blocks,
@@ -277,7 +280,8 @@ int helix_paged_attention_with_tail_out(const float* query, size_t q_heads, size
 /* The same call with the reference's full workspace contract
  * (cuda_paged.cu:483-548, checked by tests/cuda_attention_test.cpp:443):
  * score_workspace [q_heads, tail_tokens, history + tail] receives the
- * attention probabilities whatever the shape. */
+ * attention probabilities; always the exact scalar kernel (the reference's
+ * loop order, no device scratch), whatever the shape. */
 int helix_paged_attention_with_tail_probabilities_out(
     const float* query, size_t q_heads, size_t tail_tokens, size_t key_dim,
     const float* key_blocks, const float* value_blocks, size_t physical_blocks, size_t kv_heads,

@@ -1248,10 +1248,9 @@ inline void with_tail_out(TailEntry entry, const Tensor& query, const Tensor& ke
 
 /// include/helix/attention/cuda_paged.hpp:49-60: T tail queries at
 /// positions history.. attend over the history pages and, causally, the
-/// uncommitted tail rows.  A one-token decode at head_dim 128 with 16-token
-/// pages runs the stream decode kernel and uses the workspace as scratch
-/// (its content afterwards is unspecified); other shapes leave the
-/// probabilities in it.
+/// uncommitted tail rows; the workspace receives the probabilities.  At
+/// head_dim 128 with 16-token pages a one-token decode runs the one-launch
+/// decode kernel and a chunk the matrix-core prefill kernel.
 inline void paged_scaled_dot_product_attention_with_tail_out(
     const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,
     const PagedBlockTable& block_table, std::size_t history_tokens, const Tensor& tail_key,
@@ -1261,8 +1260,9 @@ inline void paged_scaled_dot_product_attention_with_tail_out(
                         score_workspace, stream);
 }
 
-/// The same call with the reference's workspace contract: the workspace
-/// [heads, tail, history + tail] receives the probabilities for every shape.
+/// The same call on the exact scalar kernel for every shape (the
+/// reference's loop order, no device scratch); the workspace [heads, tail,
+/// history + tail] receives the probabilities.
 inline void paged_scaled_dot_product_attention_with_tail_probabilities_out(
     const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,
     const PagedBlockTable& block_table, std::size_t history_tokens, const Tensor& tail_key,
