@@ -542,22 +542,29 @@ def decode_workspace(batch, q_heads, kv_heads, max_blocks, pages_per_split=0, de
     return ws
 
 
+_PAGE_DTYPES = {"f32": 0, "bf16": 1, "fp8": 2}
+
+
 def paged_decode_attention(query, key_pool, value_pool, tables, lengths, tail_key, tail_value,
-                           output, workspace, pages_per_split=0, stream=None, pool_shape=None):
+                           output, workspace, pages_per_split=0, stream=None, pool_shape=None,
+                           page_dtype="f32", k_scale=1.0, v_scale=1.0):
     """Batched decode: query [B, Hq, 128]; pools [N, Hkv, 16, 128] tensors (or raw
-    device addresses with pool_shape); tables [B, max_blocks] int32/uint32;
+    device addresses with pool_shape) of page_dtype "f32", "bf16" or "fp8"
+    (E4M3 codes with scales k_scale / v_scale, pools as uint8 / int16 / any
+    tensor whose bytes are the pages); tables [B, max_blocks] int32/uint32;
     lengths [B] int32; tail [B, Hkv, 128]; output [B, Hq, 128]."""
     b, hq, _ = query.shape
     if pool_shape is None:
         pool_shape = tuple(key_pool.shape)
         key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
     n, hkv, p, d = pool_shape
-    check(_lib().helix_paged_decode_attention(
+    dtype = _PAGE_DTYPES.get(page_dtype, page_dtype)
+    check(_lib().helix_paged_decode_attention_typed(
         _ptr(query), b, hq, hkv, d, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool), n,
         p, _ptr(tables),
         tables.shape[1], _ptr(lengths), _ptr(tail_key), _ptr(tail_value), _ptr(output),
         _ptr(workspace), workspace.numel() * workspace.element_size(), pages_per_split,
-        _stream(stream)))
+        dtype, k_scale, v_scale, _stream(stream)))
 
 
 def append_slots(keys, values, key_pool, value_pool, slots, stream=None):
@@ -569,20 +576,23 @@ def append_slots(keys, values, key_pool, value_pool, slots, stream=None):
 
 
 def paged_prefill_attention(query, key_pool, value_pool, tables, lengths, chunk_key,
-                            chunk_value, output, stream=None, pool_shape=None):
+                            chunk_value, output, stream=None, pool_shape=None,
+                            page_dtype="f32", k_scale=1.0, v_scale=1.0):
     """Batched chunked prefill (MFMA): query [B, Hq, T, 128]; pools [N, Hkv, 16,
-    128] tensors (or raw device addresses with pool_shape); tables [B,
+    128] tensors (or raw device addresses with pool_shape) of page_dtype
+    "f32", "bf16" or "fp8" (scales k_scale / v_scale); tables [B,
     max_blocks] int32/uint32; lengths [B] int32 history tokens; chunk_key /
-    chunk_value [B, Hkv, T, 128]; output [B, Hq, T, 128]."""
+    chunk_value [B, Hkv, T, 128] fp32; output [B, Hq, T, 128]."""
     b, hq, t, _ = query.shape
     if pool_shape is None:
         pool_shape = tuple(key_pool.shape)
         key_pool, value_pool = key_pool.data_ptr(), value_pool.data_ptr()
     n, hkv, p, d = pool_shape
-    check(_lib().helix_paged_prefill_attention(
+    dtype = _PAGE_DTYPES.get(page_dtype, page_dtype)
+    check(_lib().helix_paged_prefill_attention_typed(
         _ptr(query), b, hq, hkv, t, d, ctypes.c_void_p(key_pool), ctypes.c_void_p(value_pool),
         n, p, _ptr(tables), tables.shape[1], _ptr(lengths), _ptr(chunk_key), _ptr(chunk_value),
-        _ptr(output), _stream(stream)))
+        _ptr(output), dtype, k_scale, v_scale, _stream(stream)))
 
 
 def append_chunk(keys, values, key_pool, value_pool, slots, stream=None):

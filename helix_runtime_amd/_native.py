@@ -148,6 +148,12 @@ SIGNATURES = {
     "helix_paged_decode_attention": (
         c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size, vp, vp,
                 vp, vp, vp, c_size, c_size, vp]),
+    "helix_paged_decode_attention_typed": (
+        c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size, vp, vp,
+                vp, vp, vp, c_size, c_size, c_int, c_float, c_float, vp]),
+    "helix_paged_prefill_attention_typed": (
+        c_int, [vp, c_size, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size,
+                vp, vp, vp, vp, c_int, c_float, c_float, vp]),
     "helix_paged_append_slots": (
         c_int, [vp, vp, vp, vp, c_size, c_size, c_size, c_size, vp, c_size, vp]),
     "helix_paged_prefill_attention": (

@@ -922,6 +922,25 @@ void* scratch_address(const char* op) {
   return p;
 }
 
+// The page format of a typed entry point's pools: HELIX_PAGE_F32 (the
+// reference's), HELIX_PAGE_BF16, or HELIX_PAGE_FP8_E4M3 with the pools'
+// finite, positive key and value scales (ignored for the other types).
+helix::hip::PageFormat page_format(int page_dtype, float key_scale, float value_scale,
+                                   const char* op) {
+  check(page_dtype == HELIX_PAGE_F32 || page_dtype == HELIX_PAGE_BF16 ||
+            page_dtype == HELIX_PAGE_FP8_E4M3,
+        Status::kInvalidArgument,
+        std::string(op) + ": page dtype must be HELIX_PAGE_F32, HELIX_PAGE_BF16 or "
+                          "HELIX_PAGE_FP8_E4M3");
+  if (page_dtype != HELIX_PAGE_FP8_E4M3) {
+    return helix::hip::PageFormat(static_cast<helix::hip::PageType>(page_dtype));
+  }
+  check(std::isfinite(key_scale) && key_scale > 0.0f && std::isfinite(value_scale) &&
+            value_scale > 0.0f,
+        Status::kInvalidArgument, std::string(op) + ": fp8 page scales must be finite and positive");
+  return helix::hip::PageFormat(helix::hip::PageType::kFP8, key_scale, value_scale);
+}
+
 helix::hip::DecodeArgs decode_args(const float* query, size_t batch, size_t q_heads,
                                    size_t kv_heads, const float* key_blocks,
                                    const float* value_blocks, size_t physical_blocks,
@@ -961,12 +980,32 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
                                  helix_stream stream) {
+  return helix_paged_decode_attention_typed(
+      query, batch, q_heads, kv_heads, head_dim, key_blocks, value_blocks, physical_blocks,
+      block_tokens, tables, max_blocks, lengths, tail_key, tail_value, output, workspace,
+      workspace_bytes, pages_per_split, HELIX_PAGE_F32, 1.0f, 1.0f, stream);
+}
+
+int helix_paged_decode_attention_typed(const float* query, size_t batch, size_t q_heads,
+                                       size_t kv_heads, size_t head_dim, const void* key_blocks,
+                                       const void* value_blocks, size_t physical_blocks,
+                                       size_t block_tokens, const uint32_t* tables,
+                                       size_t max_blocks, const int32_t* lengths,
+                                       const float* tail_key, const float* tail_value,
+                                       float* output, void* workspace, size_t workspace_bytes,
+                                       size_t pages_per_split, int page_dtype, float key_scale,
+                                       float value_scale, helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_decode_attention";
+    const helix::hip::PageFormat fmt = page_format(page_dtype, key_scale, value_scale, op);
+    check(fmt.type == helix::hip::PageType::kF32 || pages_per_split == 0, Status::kUnsupported,
+          std::string(op) + ": bf16 and fp8 pages run the stream kernel only (pages_per_split 0)");
     const std::size_t split = resolve_split(pages_per_split);
-    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, key_blocks,
-                           value_blocks, physical_blocks, block_tokens, tables, max_blocks,
-                           lengths, tail_key, tail_value, output, split)) {
+    const auto* kb = static_cast<const float*>(key_blocks);
+    const auto* vb = static_cast<const float*>(value_blocks);
+    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, kb, vb,
+                           physical_blocks, block_tokens, tables, max_blocks, lengths, tail_key,
+                           tail_value, output, split)) {
       return;
     }
     check(workspace != nullptr && aligned16(workspace), Status::kInvalidArgument,
@@ -977,9 +1016,10 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
     const std::size_t ob = batch * q_heads * helix::hip::kDecodeHeadDim * sizeof(float);
     check(!overlap(output, ob, workspace, workspace_bytes), Status::kInvalidArgument,
           std::string(op) + ": output must not alias query or workspace");
-    const helix::hip::DecodeArgs a =
-        decode_args(query, batch, q_heads, kv_heads, key_blocks, value_blocks, physical_blocks,
-                    tables, max_blocks, lengths, tail_key, tail_value, output, workspace, split);
+    helix::hip::DecodeArgs a =
+        decode_args(query, batch, q_heads, kv_heads, kb, vb, physical_blocks, tables,
+                    max_blocks, lengths, tail_key, tail_value, output, workspace, split);
+    a.page_type = fmt;
     helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), op);
   });
 }
@@ -1089,8 +1129,24 @@ int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_hea
                                   const uint32_t* tables, size_t max_blocks,
                                   const int32_t* lengths, const float* chunk_key,
                                   const float* chunk_value, float* output, helix_stream stream) {
+  return helix_paged_prefill_attention_typed(query, batch, q_heads, kv_heads, tokens, head_dim,
+                                             key_blocks, value_blocks, physical_blocks,
+                                             block_tokens, tables, max_blocks, lengths, chunk_key,
+                                             chunk_value, output, HELIX_PAGE_F32, 1.0f, 1.0f,
+                                             stream);
+}
+
+int helix_paged_prefill_attention_typed(const float* query, size_t batch, size_t q_heads,
+                                        size_t kv_heads, size_t tokens, size_t head_dim,
+                                        const void* key_blocks, const void* value_blocks,
+                                        size_t physical_blocks, size_t block_tokens,
+                                        const uint32_t* tables, size_t max_blocks,
+                                        const int32_t* lengths, const float* chunk_key,
+                                        const float* chunk_value, float* output, int page_dtype,
+                                        float key_scale, float value_scale, helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_prefill_attention";
+    const helix::hip::PageFormat fmt = page_format(page_dtype, key_scale, value_scale, op);
     require_kernel_geometry(head_dim, block_tokens, op);
     check(kv_heads != 0 && q_heads % kv_heads == 0 &&
               helix::hip::prefill_group_supported(q_heads / kv_heads),
@@ -1118,8 +1174,8 @@ int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_hea
           Status::kInvalidArgument, std::string(op) + ": output must not alias query or chunk");
     helix::hip::PrefillArgs a{};
     a.query = query;
-    a.key_pool = key_blocks;
-    a.value_pool = value_blocks;
+    a.key_pool = static_cast<const float*>(key_blocks);
+    a.value_pool = static_cast<const float*>(value_blocks);
     a.tables = tables;
     a.lengths = lengths;
     a.chunk_key = chunk_key;
@@ -1131,6 +1187,7 @@ int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_hea
     a.tokens = tokens;
     a.max_blocks = max_blocks;
     a.physical_blocks = physical_blocks;
+    a.page_type = fmt;
     helix::hip_check(helix::hip::launch_prefill(a, as_stream(stream)), op);
   });
 }

@@ -319,6 +319,26 @@ int helix_paged_decode_attention(const float* query, size_t batch, size_t q_head
                                  const float* tail_value, float* output, void* workspace,
                                  size_t workspace_bytes, size_t pages_per_split,
                                  helix_stream stream);
+/* helix_paged_decode_attention over bf16 or fp8 E4M3 pools (extension: the
+ * reference's pools are fp32 only, docs/KV_CACHE.md:531), for callers that
+ * keep reduced-precision pools without a helix_decode_batch.  page_dtype is
+ * a helix_page_dtype; key_blocks / value_blocks hold elements of that type
+ * (the layout of helix_paged_cache_create_typed / _create_fp8 pools, whose
+ * key_scale / value_scale an fp8 call passes: finite and positive; ignored
+ * for the other types).  query, tails and output stay fp32.  bf16 and fp8
+ * pools take the stream kernel only (pages_per_split 0; otherwise
+ * HELIX_UNSUPPORTED); an unknown page_dtype or a bad fp8 scale is
+ * HELIX_INVALID_ARGUMENT before any launch.  HELIX_PAGE_F32 is exactly
+ * helix_paged_decode_attention. */
+int helix_paged_decode_attention_typed(const float* query, size_t batch, size_t q_heads,
+                                       size_t kv_heads, size_t head_dim, const void* key_blocks,
+                                       const void* value_blocks, size_t physical_blocks,
+                                       size_t block_tokens, const uint32_t* tables,
+                                       size_t max_blocks, const int32_t* lengths,
+                                       const float* tail_key, const float* tail_value,
+                                       float* output, void* workspace, size_t workspace_bytes,
+                                       size_t pages_per_split, int page_dtype, float key_scale,
+                                       float value_scale, helix_stream stream);
 /* helix_paged_decode_attention in stream mode without a workspace argument
  * and without any allocation.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
@@ -378,6 +398,20 @@ int helix_paged_prefill_attention(const float* query, size_t batch, size_t q_hea
                                   const uint32_t* tables, size_t max_blocks,
                                   const int32_t* lengths, const float* chunk_key,
                                   const float* chunk_value, float* output, helix_stream stream);
+/* helix_paged_prefill_attention over bf16 or fp8 E4M3 pools (extension, as
+ * helix_paged_decode_attention_typed): history keys and values are widened
+ * from the pages, and the fp32 chunk rows rounded onto the pool's grid (the
+ * values their pages hold once appended), so the result is the fp32
+ * attention of the values the pages hold.  Runs the exact kernel (fp32
+ * matrix cores).  HELIX_PAGE_F32 is exactly helix_paged_prefill_attention. */
+int helix_paged_prefill_attention_typed(const float* query, size_t batch, size_t q_heads,
+                                        size_t kv_heads, size_t tokens, size_t head_dim,
+                                        const void* key_blocks, const void* value_blocks,
+                                        size_t physical_blocks, size_t block_tokens,
+                                        const uint32_t* tables, size_t max_blocks,
+                                        const int32_t* lengths, const float* chunk_key,
+                                        const float* chunk_value, float* output, int page_dtype,
+                                        float key_scale, float value_scale, helix_stream stream);
 /* Chunk append (PagedKvCache::append_layer_major, paged.cpp:721-871, for one
  * layer of `batch` sequences): rows [batch, kv_heads, tokens, head_dim] go
  * to slots[b * tokens + t] = block * block_tokens + offset (negative:

@@ -124,3 +124,32 @@ def test_python_cache_rejects_bad_page_formats_before_any_allocation():
         with pytest.raises(hx.HelixError) as e:
             hx.PagedKvCache(**geometry, **kw)
         assert e.value.status == hx.INVALID_ARGUMENT, kw
+
+
+def test_typed_entry_points_reject_bad_formats_before_launch():
+    """The typed stateless decode and prefill refuse an unknown page dtype
+    and a non-finite or non-positive fp8 scale with HELIX_INVALID_ARGUMENT,
+    and bf16 / fp8 pools with an explicit split size with
+    HELIX_UNSUPPORTED, before any pointer is read (NULL pointers, no GPU)."""
+    lib = hx.load()
+
+    def decode(dtype, ks=1.0, vs=1.0, split=0):
+        return lib.helix_paged_decode_attention_typed(
+            None, 4, 32, 8, 128, None, None, 100, 16, None, 8, None, None, None, None, None,
+            1 << 20, split, dtype, ks, vs, None)
+
+    def prefill(dtype, ks=1.0, vs=1.0):
+        return lib.helix_paged_prefill_attention_typed(
+            None, 4, 32, 8, 64, 128, None, None, 100, 16, None, 8, None, None, None, None,
+            dtype, ks, vs, None)
+
+    for call in (decode, prefill):
+        assert call(3) == hx.INVALID_ARGUMENT
+        assert b"page dtype" in lib.helix_last_error()
+        assert call(-1) == hx.INVALID_ARGUMENT
+        for ks, vs in ((0.0, 1.0), (1.0, -2.0), (float("nan"), 1.0), (1.0, float("inf"))):
+            assert call(2, ks, vs) == hx.INVALID_ARGUMENT
+            assert b"fp8 page scales" in lib.helix_last_error()
+    assert decode(1, split=4) == hx.UNSUPPORTED
+    assert decode(2, 0.5, 0.5, split=1) == hx.UNSUPPORTED
+    assert b"stream kernel only" in lib.helix_last_error()
