@@ -66,7 +66,13 @@ __device__ __forceinline__ int bmma_key_slot(int kr) {
 }
 
 // x = hi + mid + lo exactly (truncating splits of a finite fp32); a
-// non-finite x is hi alone.  Results are bf16 bit patterns.
+// non-finite x is hi alone.  Results are bf16 bit patterns.  Range: lo's
+// exponent is 16 or more below x's, so for |x| < 2^-109 lo can be a bf16
+// subnormal, which the matrix cores may flush; mid likewise for |x| <
+// 2^-117.  Then the terms sum to x within |x| * 2^-7 (an absolute error
+// below 2^-116), far under any tolerance of the products they enter (the
+// scaled query and the probabilities of a row whose sum is at least 1);
+// such items are not flagged for the exact redo.
 __device__ __forceinline__ void split3(float x, short& hi, short& mid, short& lo) {
   const unsigned u = __float_as_uint(x);
   hi = static_cast<short>(u >> 16);

@@ -348,7 +348,9 @@ int helix_paged_decode_attention_typed(const float* query, size_t batch, size_t 
  * (about 6000 (sequence, kv head) units at query groups of 4) returns
  * HELIX_OUT_OF_RANGE.  Every call on one GPU shares that array, so calls
  * that overlap on one GPU (on different streams, or from several threads
- * without ordering) race; calls ordered on one stream do not.  Nothing in
+ * without ordering) race; calls ordered on one stream do not.  To use it
+ * from two streams, order the calls: hipEventRecord(e, s1) after the call on
+ * s1, hipStreamWaitEvent(s2, e, 0) before the call on s2.  Nothing in
  * the array needs to start at zero: each call writes every partial it
  * reads.  Same arguments and results as helix_paged_decode_attention with
  * pages_per_split 0. */

@@ -74,6 +74,28 @@ def test_noalloc_matches_workspace_entry_twice_shrinking(device):
         np.testing.assert_allclose(got.cpu().numpy(), ref, atol=2e-5, rtol=1e-4)
 
 
+def test_noalloc_calls_queued_on_one_stream_do_not_race(device):
+    """Two calls of different sizes queued back to back on one stream, with
+    no host synchronisation between them, share the library's array
+    correctly: calls ordered on one stream are the supported way to reuse
+    it (calls that overlap on one GPU race, as the header states)."""
+    cases = [problem(11, 30, 8, 4, 2500), problem(12, 7, 8, 4, 400)]
+    outs, wants = [], []
+    for q, kp, vp, tables, lengths, tk, tv in cases:
+        args = [dev(x) for x in (q, kp, vp, tables.view(np.int32), lengths, tk, tv)]
+        want = torch.empty(q.shape, device=device)
+        ws = hx.decode_workspace(q.shape[0], q.shape[1], kp.shape[1], tables.shape[1])
+        hx.paged_decode_attention(*args, want, ws)
+        outs.append((args, torch.full(q.shape, 7.0, device=device)))
+        wants.append(want)
+    torch.cuda.synchronize()
+    for args, got in outs:  # queued, no synchronisation in between
+        assert noalloc(*args, got) == 0, hx.load().helix_last_error()
+    torch.cuda.synchronize()
+    for (_, got), want in zip(outs, wants):
+        np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+
+
 def test_noalloc_rejects_batches_beyond_its_scratch(device):
     """More (sequence, kv head) units than the 16 MiB scratch holds are
     refused before any launch."""
