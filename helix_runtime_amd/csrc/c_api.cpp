@@ -662,8 +662,15 @@ void run_ref_prefill(const AttentionShape& s, const float* query, const float* k
   a.physical_blocks = s.physical;
   a.probs = workspace;
   a.prob_keys = prob_keys;
-  a.prob_ml = static_cast<float*>(route_scratch(mul(mul(s.q_heads, s.queries), 2 * sizeof(float)),
-                                                stream, ScratchUse::kRowStats));
+  a.prob_splits = hh::prefill_prob_splits(s.q_heads, s.kv_heads, s.queries, history + s.queries,
+                                          hh::device_cus());
+  const std::size_t slots = mul(mul(s.q_heads, s.queries), a.prob_splits);
+  const std::size_t ml_floats = (slots * 2 + 63) / 64 * 64;  // keeps prob_o 256-byte aligned
+  auto* stats = static_cast<float*>(route_scratch(
+      mul(ml_floats + mul(slots, hh::kDecodeHeadDim), sizeof(float)), stream,
+      ScratchUse::kRowStats));
+  a.prob_ml = stats;
+  a.prob_o = stats + ml_floats;
   helix::hip_check(hh::launch_prefill(a, stream), (std::string(op) + " launch").c_str());
 }
 

@@ -2561,22 +2561,6 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 
 namespace {
 
-// CUs of the current device, looked up once per device (host threads may
-// launch at once).
-int device_cus() {
-  static std::atomic<int> cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int n = cus[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0) {
-      n = 256;
-    }
-    cus[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
 
 
 // Wavefronts the stream kernel launches: every resident slot of the device
@@ -2910,6 +2894,23 @@ hipError_t launch_generic(const GenericArgs& a, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(a.queries), static_cast<unsigned>(a.q_heads));
   generic_attention_kernel<<<grid, kThreads, 0, stream>>>(a);
   return hipGetLastError();
+}
+
+// CUs of the current device, looked up once per device (host threads may
+// launch at once).
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      n = 256;
+    }
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace helix::hip

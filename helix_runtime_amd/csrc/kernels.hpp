@@ -285,9 +285,14 @@ struct PrefillArgs {
   // contract (a second launch turns the written scores into probabilities).
   float* probs = nullptr;
   std::size_t prob_keys = 0;
-  // With probs (one sequence, lengths == nullptr): scratch of q_heads *
-  // tokens * 2 floats for each row's final maximum and sum.
+  // With probs (one sequence, lengths == nullptr): the key blocks of each
+  // work item are split into prob_splits ranges (prefill_prob_splits), and
+  // scratch of q_heads * tokens * prob_splits * 2 floats (prob_ml) and
+  // * 128 floats (prob_o) holds each range's row maximum, sum and
+  // unnormalised output.
+  std::size_t prob_splits = 1;
   float* prob_ml = nullptr;
+  float* prob_o = nullptr;
 };
 
 // Shared-prefix attention for a decode batch (cascade): every query row of
@@ -319,5 +324,10 @@ bool prefill_group_supported(std::size_t group);
 // Chunk positions one prefill work item covers for a query group size.
 std::size_t prefill_position_block(std::size_t group);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
+// Key ranges per work item of a one-sequence probability prefill (1..8).
+std::size_t prefill_prob_splits(std::size_t q_heads, std::size_t kv_heads, std::size_t tokens,
+                                std::size_t keys, int cus);
+// CUs of the current device, looked up once per device.
+int device_cus();
 
 }  // namespace helix::hip

@@ -32,22 +32,25 @@ void prefill_probs_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__
                                                                        blockIdx.x, sh);
 }
 
-// Scores -> probabilities of the reference-shaped chunk call: workgroup
-// (row, s) rewrites keys [s * 2048, s * 2048 + 2048) of workspace row `row`
-// (q head * tokens + position): keys the row sees, [0, history + position
-// + 1), become exp2(x - m) / l, the rest 0; a row without a finite maximum
-// or with a NaN sum is NaN throughout (src/kernels/cpu/reference.cpp:
-// 264-316).  Eight loads per thread are in flight at once.
+// Finishes the reference-shaped chunk call.  Workgroup (row, s), row =
+// q head * tokens + position: merges the row's key-range partials into its
+// maximum and sum, rewrites keys [s * 2048, s * 2048 + 2048) of the row's
+// workspace entries from scores to probabilities (keys the row sees,
+// [0, history + position + 1), become exp2(x - m) / l, the rest 0; a row
+// without a finite maximum or with a NaN sum is NaN throughout,
+// src/kernels/cpu/reference.cpp:264-316), and workgroup s = 0 writes the
+// output row.  All of a thread's loads are issued at once.
 constexpr int kNormUnroll = 8;
+constexpr int kMaxProbSplits = 8;
 __global__ __launch_bounds__(256) void prob_normalize_kernel(float* __restrict__ probs,
                                                              const float* __restrict__ ml,
-                                                             int tokens, int history, int keys) {
+                                                             const float* __restrict__ po,
+                                                             float* __restrict__ out,
+                                                             int splits, int tokens, int history,
+                                                             int keys) {
   const std::size_t row = blockIdx.x;
   const int pos = static_cast<int>(row % static_cast<std::size_t>(tokens));
   const int seen = history + pos + 1;
-  const float m = ml[row * 2];
-  const float l = ml[row * 2 + 1];
-  const bool nan_row = m == -INFINITY || isnan(l);
   float* pr = probs + row * static_cast<std::size_t>(keys);
   const int k0 = static_cast<int>(blockIdx.y) * 256 * kNormUnroll + threadIdx.x;
   float x[kNormUnroll];
@@ -55,6 +58,38 @@ __global__ __launch_bounds__(256) void prob_normalize_kernel(float* __restrict__
   for (int u = 0; u < kNormUnroll; ++u) {
     const int k = k0 + u * 256;
     x[u] = k < seen ? pr[k] : 0.0f;
+  }
+  float ms[kMaxProbSplits], ls[kMaxProbSplits];
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxProbSplits; ++s) {
+    ms[s] = s < splits ? ml[(row * splits + s) * 2] : -INFINITY;
+    ls[s] = s < splits ? ml[(row * splits + s) * 2 + 1] : 0.0f;
+    m = fmaxf(m, ms[s]);
+  }
+  float l = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxProbSplits; ++s) {
+    if (s < splits) l += exp2_ratio(ms[s], m) * ls[s];
+  }
+  const bool nan_row = m == -INFINITY || isnan(l);
+  if (blockIdx.y == 0 && threadIdx.x < D / 4) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < kMaxProbSplits; ++s) {
+      if (s < splits) {
+        const float w = exp2_ratio(ms[s], m);
+        const float4 v = reinterpret_cast<const float4*>(po + (row * splits + s) * D)[threadIdx.x];
+        o.x += w * v.x;
+        o.y += w * v.y;
+        o.z += w * v.z;
+        o.w += w * v.w;
+      }
+    }
+    const float inv = 1.0f / l;
+    reinterpret_cast<float4*>(out + row * D)[threadIdx.x] =
+        nan_row ? make_float4(NAN, NAN, NAN, NAN)
+                : make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
   }
 #pragma unroll
   for (int u = 0; u < kNormUnroll; ++u) {
@@ -143,6 +178,20 @@ void launch_variant(const dim3& grid, hipStream_t stream, const PrefillKernelArg
 
 std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
 
+std::size_t prefill_prob_splits(std::size_t q_heads, std::size_t kv_heads, std::size_t tokens,
+                                std::size_t keys, int cus) {
+  // About two workgroups per CU (the exact kernel's occupancy), with at
+  // least four 16-key blocks per range on average.
+  const std::size_t pw = kRows / (q_heads / kv_heads);
+  const std::size_t items = kv_heads * ((tokens + pw - 1) / pw);
+  const std::size_t target = 2 * static_cast<std::size_t>(cus > 0 ? cus : 256);
+  std::size_t s = (target + items - 1) / items;
+  const std::size_t by_keys = (keys + 63) / 64;
+  if (s > by_keys) s = by_keys;
+  if (s > static_cast<std::size_t>(kMaxProbSplits)) s = kMaxProbSplits;
+  return s == 0 ? 1 : s;
+}
+
 // Key pages per cascade work item: enough chunks that the launch has about
 // one workgroup per CU, at most kMaxCascadeChunks chunks.  Every extra chunk
 // re-loads the query tile, writes one more partial per row and adds merge
@@ -195,12 +244,16 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   k.probs = a.probs;
   k.prob_keys = static_cast<int>(a.prob_keys);
   k.prob_ml = a.prob_ml;
-  const dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
+  dim3 grid(static_cast<unsigned>(k.pos_blocks * a.kv_heads * a.batch));
   if (a.probs != nullptr) {
     if (a.page_type.type != PageType::kF32 || a.redo != nullptr || a.batch != 1 ||
-        a.lengths != nullptr || a.prob_ml == nullptr) {
+        a.lengths != nullptr || a.prob_ml == nullptr || a.prob_o == nullptr ||
+        a.prob_splits < 1 || a.prob_splits > static_cast<std::size_t>(kMaxProbSplits)) {
       return hipErrorInvalidValue;
     }
+    k.prob_splits = static_cast<int>(a.prob_splits);
+    k.prob_o = a.prob_o;
+    grid.x *= static_cast<unsigned>(a.prob_splits);
     constexpr unsigned threads = 512 / kTilesPerWave;
     switch (group) {
       case 1: prefill_probs_kernel<1><<<grid, threads, 0, stream>>>(k, a.tables, a.order); break;
@@ -214,10 +267,9 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
     const dim3 ngrid(static_cast<unsigned>(a.q_heads * a.tokens),
                      static_cast<unsigned>((a.prob_keys + 256 * kNormUnroll - 1) /
                                            (256 * kNormUnroll)));
-    prob_normalize_kernel<<<ngrid, 256, 0, stream>>>(a.probs, a.prob_ml,
-                                                     static_cast<int>(a.tokens),
-                                                     a.single_length,
-                                                     static_cast<int>(a.prob_keys));
+    prob_normalize_kernel<<<ngrid, 256, 0, stream>>>(
+        a.probs, a.prob_ml, a.prob_o, a.out, static_cast<int>(a.prob_splits),
+        static_cast<int>(a.tokens), a.single_length, static_cast<int>(a.prob_keys));
     return hipGetLastError();
   }
   if (a.redo != nullptr && a.page_type.type == PageType::kF32) {

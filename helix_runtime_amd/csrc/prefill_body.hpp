@@ -107,7 +107,13 @@ struct PrefillKernelArgs {
   // that query row over keys [0, prob_keys); keys the row does not see get 0.
   float* probs;
   int prob_keys;
-  float* prob_ml;  // [rows, 2]: each row's final maximum and sum
+  // PROBS: each work item's key blocks are split into prob_splits ranges,
+  // one per work item; every (row, split) leaves its maximum and sum in
+  // prob_ml [rows, prob_splits, 2] and its unnormalised output in prob_o
+  // [rows, prob_splits, 128] for prob_normalize_kernel to merge.
+  int prob_splits;
+  float* prob_ml;
+  float* prob_o;
 };
 
 // exp2(a - b), with a == b (also +inf == +inf, -inf == -inf) giving 1 and
@@ -207,11 +213,14 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
 // probability, or the exact result is NaN anyway) is flagged in
 // redo[block] for the exact kernel.  Without the exact path the kernel
 // fits one 16-row tile per wavefront at four wavefronts per SIMD.
-// PROBS (the reference-shaped chunk call): every score of the rows' keys
-// [0, key_end) is written (log2 domain, -inf where masked) to its
-// probability entry as it is computed, and each row's final maximum and sum
-// (sum NaN for a row of a work item that met a bad page) go to prob_ml;
-// prob_normalize_kernel then turns the scores into probabilities.
+// PROBS (the reference-shaped chunk call, one sequence): the key blocks of
+// each (kv head, position block) are split into prob_splits ranges, one
+// work item each, so a single sequence still fills the GPU.  Every score of
+// the range is written (log2 domain, -inf where masked) to its probability
+// entry as it is computed, and each row leaves the range's maximum, sum
+// (NaN for a work item that met a bad page) and unnormalised output;
+// prob_normalize_kernel merges the ranges into the output row and turns the
+// scores into probabilities.
 template <int G, bool CASCADE, int PF, int RT, bool FAST = false, class Shared,
           bool PROBS = false>
 __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
@@ -240,6 +249,11 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   // longest-first order; by default later position blocks (more keys) of a
   // (sequence, kv head) go first.
   std::uint32_t item = block;
+  int split = 0;
+  if constexpr (PROBS) {
+    split = static_cast<int>(block % static_cast<std::uint32_t>(a.prob_splits));
+    item = block / static_cast<std::uint32_t>(a.prob_splits);
+  }
   int pb, kvh, b, chunk;
   if constexpr (CASCADE) {
     // Cascade items, kv head major: (kvh * chunks + chunk) * pos_blocks +
@@ -272,9 +286,17 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   int hist = CASCADE ? a.cascade_keys : (a.lengths != nullptr ? a.lengths[b] : a.single_length);
   bool bad = hist < 0 || hist > a.max_blocks * P;
   if (bad) hist = 0;
-  const int key_begin = CASCADE ? chunk * a.cascade_chunk_pages * P : 0;
-  const int key_end =
+  int key_begin = CASCADE ? chunk * a.cascade_chunk_pages * P : 0;
+  int key_end =
       CASCADE ? min(hist, (chunk + 1) * a.cascade_chunk_pages * P) : hist + min(T, pos0 + PW);
+  if constexpr (PROBS) {
+    // This item's share of the key blocks (possibly none).
+    const int nb = (key_end + kKeys - 1) / kKeys;
+    const int b0 = static_cast<int>(static_cast<long long>(nb) * split / a.prob_splits);
+    const int b1 = static_cast<int>(static_cast<long long>(nb) * (split + 1) / a.prob_splits);
+    key_begin = b0 * kKeys;
+    key_end = min(key_end, b1 * kKeys);
+  }
   // Read-only and indexed by workgroup-uniform values: scalar loads.
   const std::uint32_t* __restrict__ table = tables + static_cast<std::size_t>(b) * a.max_blocks;
   const std::size_t chunk_row0 = (static_cast<std::size_t>(b) * a.kv_heads + kvh) * T;
@@ -730,11 +752,23 @@ __device__ __forceinline__ void prefill_body(PrefillKernelArgs a,
   if constexpr (PROBS) {
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      if (qpos[t] >= T || grp != 0) continue;
-      const std::size_t row = static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t];
-      a.prob_ml[row * 2] = m[t];
-      a.prob_ml[row * 2 + 1] = any_bad ? NAN : l[t];
+      if (qpos[t] >= T) continue;
+      const std::size_t slot =
+          (static_cast<std::size_t>(kvh * G + r_head[t]) * T + qpos[t]) * a.prob_splits + split;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          *reinterpret_cast<float4*>(a.prob_o + slot * D + 64 * h + 16 * grp + 4 * ii) =
+              make_float4(o[t][h][0][ii], o[t][h][1][ii], o[t][h][2][ii], o[t][h][3][ii]);
+        }
+      }
+      if (grp == 0) {
+        a.prob_ml[slot * 2] = m[t];
+        a.prob_ml[slot * 2 + 1] = any_bad ? NAN : l[t];
+      }
     }
+    return;
   }
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
