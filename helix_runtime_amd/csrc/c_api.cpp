@@ -543,8 +543,9 @@ void run_reference_attention(const AttentionShape& s, const float* query,
 // Device scratch of the reference-shaped fast routes, one buffer per
 // (device, stream, purpose): calls on one stream run in order and may share
 // it, calls on different streams get their own.  It grows on demand (the
-// old buffer is freed after the device has drained, which hipFree waits
-// for).  Buffers live until the process ends.
+// old buffer is freed once the stream has drained).  Buffers live until the
+// process ends.  Host threads that issue calls on one stream must order
+// those calls themselves, as they must for the stream's work anyway.
 enum class ScratchUse : int { kDecode = 0, kChunk = 1, kRowStats = 2 };
 void* route_scratch(std::size_t bytes, hipStream_t stream, ScratchUse use) {
   struct Buffer {
@@ -560,6 +561,8 @@ void* route_scratch(std::size_t bytes, hipStream_t stream, ScratchUse use) {
   if (b.bytes < bytes) {
     const std::size_t grown = std::max(bytes, 2 * b.bytes);
     if (b.ptr != nullptr) {
+      // Earlier calls on this stream may still read the old buffer.
+      helix::hip_check(hipStreamSynchronize(stream), "route scratch: hipStreamSynchronize");
       helix::hip_check(hipFree(b.ptr), "route scratch: hipFree");
       b = Buffer{};
     }
