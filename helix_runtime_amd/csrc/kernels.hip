@@ -2826,8 +2826,10 @@ RefDecodePlan ref_decode_plan(std::size_t q_heads, std::size_t kv_heads, std::si
   if (kv_heads == 0 || q_heads % kv_heads != 0) return p;
   const std::size_t group = q_heads / kv_heads;
   const std::size_t pages = (visible + kDecodeBlockTokens - 1) / kDecodeBlockTokens + (tail ? 1 : 0);
-  // About eight wavefronts per CU over the whole call, whole pages each.
-  const std::size_t target = static_cast<std::size_t>(device_cus()) * 8;
+  // About four wavefronts per CU over the whole call, whole pages each
+  // (config-3 calls: 12.4 us against 12.8 at three or six per CU, 13.2 at
+  // eight and 13.8 at two).
+  const std::size_t target = static_cast<std::size_t>(device_cus()) * 4;
   const std::size_t total = kv_heads * pages;
   p.ppw = total <= target ? 1 : (total + target - 1) / target;
   p.chunks = (pages + 4 * p.ppw - 1) / (4 * p.ppw);
