@@ -181,7 +181,9 @@ std::size_t prefill_position_block(std::size_t group) { return kRows / group; }
 std::size_t prefill_prob_splits(std::size_t q_heads, std::size_t kv_heads, std::size_t tokens,
                                 std::size_t keys, int cus) {
   // About two workgroups per CU (the exact kernel's occupancy), with at
-  // least four 16-key blocks per range on average.
+  // least four 16-key blocks per range on average.  Config-5 calls (128
+  // items per sequence): 4 ranges 338 us per call, 3 ranges 379, 6 ranges
+  // 383, 8 ranges 366.
   const std::size_t pw = kRows / (q_heads / kv_heads);
   const std::size_t items = kv_heads * ((tokens + pw - 1) / pw);
   const std::size_t target = 2 * static_cast<std::size_t>(cus > 0 ? cus : 256);
