@@ -633,7 +633,8 @@ bool ref_prefill_fits(const AttentionShape& s, const float* query, const float* 
   return s.queries >= 2 && s.key_dim == hh::kDecodeHeadDim &&
          s.value_dim == hh::kDecodeHeadDim && s.block_tokens == hh::kDecodeBlockTokens &&
          s.kv_heads != 0 && s.q_heads % s.kv_heads == 0 &&
-         hh::prefill_group_supported(s.q_heads / s.kv_heads) && prob_keys <= kIntMax / 2 &&
+         hh::prefill_group_supported(s.q_heads / s.kv_heads) &&
+         prob_keys <= hh::kRefDecodeMaxKeys &&
          s.queries * s.kv_heads <= kIntMax && aligned16p(query) && aligned16p(output) &&
          (history == 0 || (aligned16p(key_blocks) && aligned16p(value_blocks)));
 }

@@ -221,8 +221,9 @@ struct RefDecodePlan {
   std::size_t ppw = 0;           // pages per wavefront
   std::size_t scratch_bytes = 0;
 };
-// Workspace keys one merging workgroup normalises, and the longest row the
-// route takes (the merge grid's second dimension stays within 65535).
+// Workspace keys one merging or normalising workgroup rewrites, and the
+// longest workspace row the fast reference-shaped routes take (their
+// grids' second dimension stays within 65535).
 constexpr std::size_t kRefNormKeys = 2048;
 constexpr std::size_t kRefDecodeMaxKeys = 65535 * kRefNormKeys;
 RefDecodePlan ref_decode_plan(std::size_t q_heads, std::size_t kv_heads, std::size_t visible,

@@ -40,7 +40,7 @@ void prefill_probs_kernel(PrefillKernelArgs a, const std::uint32_t* __restrict__
 // without a finite maximum or with a NaN sum is NaN throughout,
 // src/kernels/cpu/reference.cpp:264-316), and workgroup s = 0 writes the
 // output row.  All of a thread's loads are issued at once.
-constexpr int kNormUnroll = 8;
+constexpr int kNormUnroll = static_cast<int>(kRefNormKeys / 256);
 constexpr int kMaxProbSplits = 8;
 __global__ __launch_bounds__(256) void prob_normalize_kernel(float* __restrict__ probs,
                                                              const float* __restrict__ ml,
