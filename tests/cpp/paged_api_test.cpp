@@ -7,7 +7,7 @@
 // API.  Everything else is this repository's own checking: seeded random
 // operation programs against the CPU oracle's pool, a table of invalid
 // calls that must fail before any launch, the read lease, seeded attention
-// sweeps against the oracle, the stream-kernel route of the decode entry
+// sweeps against the oracle, the one-launch route of the decode entry
 // point, and the extensions (copy-on-write fork, bulk append, bf16 pages,
 // the prefix cache, DecodeBatch decode and chunk steps).
 //
