@@ -372,7 +372,7 @@ def run_reference_entry(args):
     src/model/cuda_llama.cpp:365-367), so a layer of the batch-64 step is 64
     calls, each with that sequence's device block table, its [32, 1, 128]
     query, [8, 1, 128] tail and a [32, 1, history + 1] score workspace.
-    Here those calls take the one-launch decode route (ref_decode_kernel,
+    Here those calls take the single-sequence decode route (ref_decode_kernel,
     plus its merge launch when a kv head takes several workgroups), which
     also leaves the probabilities in the workspace as the reference does.
     Each layer's 64 calls are queued behind a short device-side sleep so the

@@ -578,7 +578,7 @@ void* route_scratch(std::size_t bytes, hipStream_t stream, ScratchUse use) {
 
 bool aligned16p(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
-// The reference-shaped call with one query row on the one-launch decode
+// The reference-shaped call with one query row on the single-sequence decode
 // kernel: head_dim 128, 16-token pages, a supported query group and 16-byte
 // aligned rows.  The score workspace ends up holding the probabilities, as
 // on the reference's own path.  `visible` page tokens, then (tail) the tail

@@ -244,7 +244,7 @@ int helix_paged_tail_score_workspace_bytes(size_t q_heads, size_t tail_tokens, s
                                            size_t logical_blocks, size_t history_tokens,
                                            size_t* out);
 /* paged_scaled_dot_product_attention_out (cuda_paged.cu:420-481).  Routes as
- * helix_paged_attention_with_tail_out: one query row on the one-launch
+ * helix_paged_attention_with_tail_out: one query row on the single-sequence
  * decode kernel, several on the matrix-core prefill kernel (the rows' own
  * page tokens gathered into the stream's scratch as the chunk). */
 int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries, size_t key_dim,
@@ -262,7 +262,7 @@ int helix_paged_attention_out(const float* query, size_t q_heads, size_t queries
  * 365-367).  The workspace receives the probabilities on every route, as in
  * the reference.  With key_dim = value_dim = 128, 16-token pages, q_heads /
  * kv_heads in {1, 2, 4, 8} and 16-byte aligned rows, a one-token call runs
- * the one-launch decode kernel (plus a merging launch when a kv head spans
+ * the single-sequence decode kernel (plus a merging launch when a kv head spans
  * several workgroups) and a call with several tail rows (a prefill chunk)
  * runs the exact fp32 matrix-core prefill kernel plus a normalisation
  * launch; both use a device scratch the library keeps per (device, stream),

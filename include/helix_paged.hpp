@@ -1249,7 +1249,7 @@ inline void with_tail_out(TailEntry entry, const Tensor& query, const Tensor& ke
 /// include/helix/attention/cuda_paged.hpp:49-60: T tail queries at
 /// positions history.. attend over the history pages and, causally, the
 /// uncommitted tail rows; the workspace receives the probabilities.  At
-/// head_dim 128 with 16-token pages a one-token decode runs the one-launch
+/// head_dim 128 with 16-token pages a one-token decode runs the single-sequence
 /// decode kernel and a chunk the matrix-core prefill kernel.
 inline void paged_scaled_dot_product_attention_with_tail_out(
     const Tensor& query, const Tensor& key_blocks, const Tensor& value_blocks,

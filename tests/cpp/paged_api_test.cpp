@@ -7,7 +7,7 @@
 // API.  Everything else is this repository's own checking: seeded random
 // operation programs against the CPU oracle's pool, a table of invalid
 // calls that must fail before any launch, the read lease, seeded attention
-// sweeps against the oracle, the one-launch route of the decode entry
+// sweeps against the oracle, the single-sequence decode route of the decode entry
 // point, and the extensions (copy-on-write fork, bulk append, bf16 pages,
 // the prefix cache, DecodeBatch decode and chunk steps).
 //
@@ -1095,11 +1095,11 @@ TEST_F(HipAttentionTest, MaskedNonFiniteTailRowsDoNotLeak) {
 }
 
 // The model's per-layer call at head_dim 128 and 16-token pages runs the
-// one-launch decode kernel; its output matches the oracle within the
+// single-sequence decode kernel; its output matches the oracle within the
 // north-star tolerance and its score workspace holds the same probabilities
 // as the exact scalar route's (the reference's workspace contract, within
 // the reference test's 2e-6), for MHA and GQA.
-TEST_F(HipAttentionTest, DecodeCallsTakeTheOneLaunchRoute) {
+TEST_F(HipAttentionTest, DecodeCallsTakeTheSingleSequenceRoute) {
   Stream stream;
   for (const auto& [hkv, group, history] :
        std::vector<std::array<std::size_t, 3>>{{8, 4, 1500}, {4, 1, 700}, {2, 8, 3000}}) {

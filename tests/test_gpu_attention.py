@@ -319,10 +319,10 @@ def test_decode_rejects_bad_arguments(device):
                                   dev(lengths), dev(tk), dev(tv), out, small, 1)
 
 
-# ------------------------------ reference-shaped entry, one-launch decode route ----
+# ------------------------------ reference-shaped entry, single-sequence decode route ----
 # One query row per head at head_dim 128 and 16-token pages (the reference
 # model's per-layer call, src/model/cuda_llama.cpp:361-367) runs the
-# one-launch decode kernel; the score workspace still ends up holding the
+# single-sequence decode kernel; the score workspace still ends up holding the
 # softmax probabilities, as the reference's contract says
 # (tests/cuda_attention_test.cpp:441-443).  Outputs within 2e-5 + 1e-4 rel
 # of the oracle, probabilities within the reference's 2e-6.
@@ -391,7 +391,7 @@ def test_history_decode_route_matches_oracle(device, kv, offset):
 
 
 def test_decode_route_special_values(device):
-    """The reference softmax rules on the one-launch route
+    """The reference softmax rules on the single-sequence decode route
     (src/kernels/cpu/reference.cpp:264-316): +inf scores share the mass, a
     NaN score makes its row NaN, other rows are untouched."""
     hist = 700

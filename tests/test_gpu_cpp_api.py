@@ -1,7 +1,7 @@
 """The C++ API suite (tests/cpp/paged_api_test.cpp) on the GPU: the golden
 fixtures of tests/golden/ replayed through include/helix_paged.hpp, random
 operation programs against the oracle pool, invalid-call tables, the read
-lease, seeded attention sweeps, the one-launch route of the decode entry point
+lease, seeded attention sweeps, the single-sequence decode route of the decode entry point
 and the extensions.  One process runs every case; the binary prints each
 case's name before it runs."""
 
