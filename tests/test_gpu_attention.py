@@ -542,3 +542,38 @@ def test_chunk_route_special_values(device):
     table[5] = kp.shape[0] + 9
     out, ws = run_chunk(q, kp, vp, table, hist, tk, tv)
     assert np.isnan(out).all() and np.isnan(ws).all()
+
+
+def test_reference_routes_seeded_random_calls(device):
+    """Seeded random calls of both reference-shaped entry points at head_dim
+    128 and 16-token pages: query groups 1/2/4/8, one or several query rows,
+    histories from 0 (tail form) or offsets anywhere in the keys (history
+    form), so every route (single-sequence decode with and without a merge,
+    matrix-core chunk with its key ranges, the gathered-chunk history form)
+    meets ragged edges; outputs and probabilities against the oracle."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        g = int(rng.choice([1, 2, 4, 8]))
+        hkv = int(rng.choice([1, 2, 4, 8])) if g < 8 else int(rng.choice([1, 2, 4]))
+        T = int(rng.choice([1, 1, 2, 3, 17, 64, 130]))
+        tail_form = case % 2 == 0
+        hist = int(rng.integers(0, 1500))
+        print(f"case {case}: g={g} hkv={hkv} T={T} hist={hist} tail={tail_form}", flush=True)
+        if tail_form:
+            table, kp, vp, q, tk, tv = chunk_problem(7000 + case, hkv, g, hist, T)
+            exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+            out, ws = run_chunk(q, kp, vp, table, hist, tk, tv)
+        else:
+            kv = hist + T + int(rng.integers(0, 40))
+            offset = int(rng.integers(0, kv - T + 1))
+            table, kp, vp, q, _, _ = chunk_problem(7000 + case, hkv, g, kv, T)
+            exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, kv,
+                                                     query_position_offset=offset)
+            o = torch.full((hkv * g, T, 128), 5.0, device=device)
+            w = torch.full((hkv * g, T, kv), 7.0, device=device)
+            hx.paged_attention_out(dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), kv,
+                                   offset, o, w)
+            torch.cuda.synchronize()
+            out, ws = host(o), host(w)
+        np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL, err_msg=f"case {case}")
+        np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0, err_msg=f"case {case}")
