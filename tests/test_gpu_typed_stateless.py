@@ -19,7 +19,7 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-5, 1e-4
-D, P, H, HQ = 128, 16, 8, 32
+D, P, H = 128, 16, 8
 KS, VS = 0.037, 0.011
 
 
@@ -63,11 +63,13 @@ def build(dtype, hists, seed):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-def test_typed_stateless_decode_matches_oracle(device, dtype):
+@pytest.mark.parametrize("hq", [8, 16, 32, 64])
+def test_typed_stateless_decode_matches_oracle(device, dtype, hq):
     hists = [0, 5, 16, 300, 1000, 2100]
-    cache, pool, tables, N, rng = build(dtype, hists, 71)
+    cache, pool, tables, N, rng = build(dtype, hists, 71 + hq)
     rk, rv = rounders(dtype)
     B = len(hists)
+    HQ = hq
     q = rng.standard_normal((B, HQ, D), dtype=np.float32)
     tk = rng.standard_normal((B, H, D), dtype=np.float32)
     tv = rng.standard_normal((B, H, D), dtype=np.float32)
@@ -91,11 +93,13 @@ def test_typed_stateless_decode_matches_oracle(device, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-def test_typed_stateless_prefill_matches_oracle(device, dtype):
+@pytest.mark.parametrize("hq", [8, 16, 32, 64])
+def test_typed_stateless_prefill_matches_oracle(device, dtype, hq):
     hists = [0, 7, 64, 333, 1200]
-    cache, pool, tables, N, rng = build(dtype, hists, 72)
+    cache, pool, tables, N, rng = build(dtype, hists, 72 + hq)
     rk, rv = rounders(dtype)
     B, T = len(hists), 40
+    HQ = hq
     q = rng.standard_normal((B, HQ, T, D), dtype=np.float32)
     ck = rng.standard_normal((B, H, T, D), dtype=np.float32)
     cv = rng.standard_normal((B, H, T, D), dtype=np.float32)
