@@ -142,7 +142,7 @@ SIGNATURES = {
                 c_size, vp, vp, vp, vp, c_size, vp]),
     "helix_paged_decode_attention_noalloc": (
         c_int, [vp, c_size, c_size, c_size, c_size, vp, vp, c_size, c_size, vp, c_size, vp, vp,
-                vp, vp, vp]),
+                vp, vp, c_int, c_float, c_float, vp]),
     "helix_paged_decode_workspace_bytes": (c_int, [c_size] * 5 + [P(c_size)]),
     "helix_paged_decode_workspace_init": (c_int, [vp, c_size, vp]),
     "helix_paged_decode_attention": (

@@ -1036,29 +1036,33 @@ int helix_paged_decode_attention_typed(const float* query, size_t batch, size_t 
 }
 
 int helix_paged_decode_attention_noalloc(const float* query, size_t batch, size_t q_heads,
-                                         size_t kv_heads, size_t head_dim,
-                                         const float* key_blocks, const float* value_blocks,
-                                         size_t physical_blocks, size_t block_tokens,
-                                         const uint32_t* tables, size_t max_blocks,
-                                         const int32_t* lengths, const float* tail_key,
-                                         const float* tail_value, float* output,
-                                         helix_stream stream) {
+                                         size_t kv_heads, size_t head_dim, const void* key_blocks,
+                                         const void* value_blocks, size_t physical_blocks,
+                                         size_t block_tokens, const uint32_t* tables,
+                                         size_t max_blocks, const int32_t* lengths,
+                                         const float* tail_key, const float* tail_value,
+                                         float* output, int page_dtype, float key_scale,
+                                         float value_scale, helix_stream stream) {
   return guarded([&] {
     constexpr const char* op = "paged_decode_attention_noalloc";
-    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, key_blocks,
-                           value_blocks, physical_blocks, block_tokens, tables, max_blocks,
-                           lengths, tail_key, tail_value, output, 0)) {
+    const helix::hip::PageFormat fmt = page_format(page_dtype, key_scale, value_scale, op);
+    const auto* kb = static_cast<const float*>(key_blocks);
+    const auto* vb = static_cast<const float*>(value_blocks);
+    if (!check_decode_call(op, query, batch, q_heads, kv_heads, head_dim, kb, vb,
+                           physical_blocks, block_tokens, tables, max_blocks, lengths, tail_key,
+                           tail_value, output, 0)) {
       return;
     }
-    check(helix::hip::compact_decode_workspace_bytes(batch, q_heads, kv_heads) <=
+    check(helix::hip::compact_decode_workspace_bytes(batch, q_heads, kv_heads, fmt.type) <=
               kNoAllocScratchBytes,
           Status::kOutOfRange, op,
           "batch * kv_heads too large for the 16 MiB scratch (use "
           "helix_paged_decode_attention with a workspace)");
     void* ws = scratch_address(op);
     helix::hip::DecodeArgs a =
-        decode_args(query, batch, q_heads, kv_heads, key_blocks, value_blocks, physical_blocks,
-                    tables, max_blocks, lengths, tail_key, tail_value, output, ws, 0);
+        decode_args(query, batch, q_heads, kv_heads, kb, vb, physical_blocks, tables,
+                    max_blocks, lengths, tail_key, tail_value, output, ws, 0);
+    a.page_type = fmt;
     a.compact_layout = true;
     helix::hip_check(helix::hip::launch_decode(a, as_stream(stream)), op);
   });

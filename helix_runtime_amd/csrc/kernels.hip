@@ -2673,10 +2673,9 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     const bool overlap = !fused && a.shared_pages > 0 && a.side_stream != nullptr &&
                          a.fork_event != nullptr && a.join_event != nullptr;
     const std::size_t waves = stream_waves(group, overlap || fused, a.page_type.type);
-    // The compact layout is sized for the fp32 kernel's wavefront count.
-    if (a.compact_layout && (a.shared_pages != 0 || a.page_type.type != PageType::kF32)) {
-      return hipErrorInvalidValue;
-    }
+    // The compact layout is sized for this launch's wavefront count (which
+    // compact_decode_workspace_bytes gives for the same page type).
+    if (a.compact_layout && a.shared_pages != 0) return hipErrorInvalidValue;
     const WorkspaceLayout lay =
         a.compact_layout ? stream_layout(a.batch, a.q_heads, a.kv_heads, waves, 0)
                          : stream_layout_for(a.batch, a.q_heads, a.kv_heads);
@@ -2814,9 +2813,10 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
 }
 
 std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_heads,
-                                           std::size_t kv_heads) {
+                                           std::size_t kv_heads, PageType type) {
   if (kv_heads == 0 || q_heads % kv_heads != 0) return 0;
-  return stream_layout(batch, q_heads, kv_heads, stream_waves(q_heads / kv_heads, false), 0).total;
+  return stream_layout(batch, q_heads, kv_heads, stream_waves(q_heads / kv_heads, false, type), 0)
+      .total;
 }
 
 

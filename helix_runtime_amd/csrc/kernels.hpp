@@ -186,9 +186,11 @@ std::size_t decode_items(const std::int32_t* lengths, std::size_t batch, std::si
 hipError_t launch_decode_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream);
 bool decode_group_supported(std::size_t group);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
-// Workspace of a stream-mode decode with compact_layout (no cascade).
+// Workspace of a stream-mode decode with compact_layout (no cascade) over
+// pages of `type`.
 std::size_t compact_decode_workspace_bytes(std::size_t batch, std::size_t q_heads,
-                                           std::size_t kv_heads);
+                                           std::size_t kv_heads,
+                                           PageType type = PageType::kF32);
 
 // ------------------------------------- reference-shaped one-sequence decode ----
 // One query row per head (the reference's per-layer model call) over pages of

@@ -352,16 +352,17 @@ int helix_paged_decode_attention_typed(const float* query, size_t batch, size_t 
  * from two streams, order the calls: hipEventRecord(e, s1) after the call on
  * s1, hipStreamWaitEvent(s2, e, 0) before the call on s2.  Nothing in
  * the array needs to start at zero: each call writes every partial it
- * reads.  Same arguments and results as helix_paged_decode_attention with
- * pages_per_split 0. */
+ * reads.  Same arguments and results as helix_paged_decode_attention_typed
+ * with pages_per_split 0 (page_dtype, key_scale and value_scale as there;
+ * bf16 and fp8 pools take the same array). */
 int helix_paged_decode_attention_noalloc(const float* query, size_t batch, size_t q_heads,
-                                         size_t kv_heads, size_t head_dim,
-                                         const float* key_blocks, const float* value_blocks,
-                                         size_t physical_blocks, size_t block_tokens,
-                                         const uint32_t* tables, size_t max_blocks,
-                                         const int32_t* lengths, const float* tail_key,
-                                         const float* tail_value, float* output,
-                                         helix_stream stream);
+                                         size_t kv_heads, size_t head_dim, const void* key_blocks,
+                                         const void* value_blocks, size_t physical_blocks,
+                                         size_t block_tokens, const uint32_t* tables,
+                                         size_t max_blocks, const int32_t* lengths,
+                                         const float* tail_key, const float* tail_value,
+                                         float* output, int page_dtype, float key_scale,
+                                         float value_scale, helix_stream stream);
 /* kernels::rope / cpu::rope_out (src/kernels/cpu/reference.cpp:490-533):
  * rotates the adjacent pairs (2i, 2i+1) of every head vector, out[2i] =
  * x[2i]*cos - x[2i+1]*sin, out[2i+1] = x[2i]*sin + x[2i+1]*cos, each product

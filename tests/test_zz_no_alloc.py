@@ -1,8 +1,9 @@
 """helix_paged_decode_attention_noalloc (the entry point that allocates
 nothing; its partials live in a library-owned device array) against
-helix_paged_decode_attention with a caller workspace: identical outputs,
-bit for bit, on two calls in a row, the second with a smaller input, and
-both within the north-star tolerance of the oracle."""
+helix_paged_decode_attention(_typed) with a caller workspace: identical
+outputs, bit for bit, on two calls in a row, the second with a smaller
+input, on fp32, bf16 and fp8 pools, and within the north-star tolerance of
+the oracle."""
 
 import ctypes
 
@@ -43,13 +44,14 @@ def problem(seed, batch, hkv, g, max_len):
     return q, kp, vp, tables, lengths, tk, tv
 
 
-def noalloc(q, kp, vp, tables, lengths, tk, tv, out):
+def noalloc(q, kp, vp, tables, lengths, tk, tv, out, pool_shape=None, dtype=0, ks=1.0, vs=1.0):
     b, hq, _ = q.shape
-    n, hkv, p, d = kp.shape
-    p_ = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    n, hkv, p, d = kp.shape if pool_shape is None else pool_shape
+    p_ = lambda t: ctypes.c_void_p(t if isinstance(t, int) else t.data_ptr())  # noqa: E731
     return hx.load().helix_paged_decode_attention_noalloc(
         p_(q), b, hq, hkv, d, p_(kp), p_(vp), n, p, p_(tables), tables.shape[1], p_(lengths),
-        p_(tk), p_(tv), p_(out), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        p_(tk), p_(tv), p_(out), dtype, ks, vs,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
 
 
 def test_noalloc_matches_workspace_entry_twice_shrinking(device):
@@ -96,6 +98,46 @@ def test_noalloc_calls_queued_on_one_stream_do_not_race(device):
         np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_noalloc_typed_pools_match_the_typed_workspace_entry(device, dtype):
+    """bf16 and fp8 pools (a typed cache's layer pools) through the entry
+    point, two calls in a row, the second smaller: bit-identical to
+    helix_paged_decode_attention_typed with a workspace."""
+    ks, vs = (0.037, 0.011) if dtype == "fp8" else (1.0, 1.0)
+    code = {"bf16": 1, "fp8": 2}[dtype]
+    kw = dict(k_scale=ks, v_scale=vs) if dtype == "fp8" else {}
+    for seed, batch, max_len in ((21, 20, 2500), (22, 6, 600)):
+        print(f"noalloc typed case {dtype} seed={seed} batch={batch}", flush=True)
+        rng = np.random.default_rng(seed)
+        H, HQ = 8, 32
+        hists = [int(x) for x in rng.integers(0, max_len + 1, size=batch)]
+        N = sum((h + P - 1) // P for h in hists) + 8
+        cache = hx.PagedKvCache(1, H, D, P, N, page_dtype=dtype, **kw)
+        tables = np.zeros((batch, max(1, max((h + P - 1) // P for h in hists))), np.uint32)
+        for b, h in enumerate(hists):
+            s = cache.create_sequence()
+            if h:
+                cache.append_layer_major(s, [dev(rng.standard_normal((H, h, D), dtype=np.float32))],
+                                         [dev(rng.standard_normal((H, h, D), dtype=np.float32))])
+            tab = cache.block_table(s)
+            tables[b, :len(tab)] = tab
+        kptr, vptr = cache.layer_pool_pointers(0)
+        q = dev(rng.standard_normal((batch, HQ, D), dtype=np.float32))
+        tk = dev(rng.standard_normal((batch, H, D), dtype=np.float32))
+        tv = dev(rng.standard_normal((batch, H, D), dtype=np.float32))
+        dtab, dlen = dev(tables.view(np.int32)), dev(np.array(hists, np.int32))
+        want = torch.empty(batch, HQ, D, device=device)
+        ws = hx.decode_workspace(batch, HQ, H, tables.shape[1])
+        hx.paged_decode_attention(q, kptr, vptr, dtab, dlen, tk, tv, want, ws,
+                                  pool_shape=(N, H, P, D), page_dtype=dtype, **kw)
+        got = torch.full((batch, HQ, D), 7.0, device=device)
+        assert noalloc(q, kptr, vptr, dtab, dlen, tk, tv, got, pool_shape=(N, H, P, D),
+                       dtype=code, ks=ks, vs=vs) == 0, hx.load().helix_last_error()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
+        cache.close()
+
+
 def test_noalloc_rejects_batches_beyond_its_scratch(device):
     """More (sequence, kv head) units than the 16 MiB scratch holds are
     refused before any launch."""
@@ -105,6 +147,7 @@ def test_noalloc_rejects_batches_beyond_its_scratch(device):
     p_ = ctypes.c_void_p(x.data_ptr())
     rc = hx.load().helix_paged_decode_attention_noalloc(
         ctypes.c_void_p(q.data_ptr()), 4096, 32, 8, D, p_, p_, 100, P, p_, 4, p_, p_, p_,
-        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        ctypes.c_void_p(out.data_ptr()), 0, 1.0, 1.0,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == hx.OUT_OF_RANGE
     assert b"16 MiB scratch" in hx.load().helix_last_error()
