@@ -577,3 +577,54 @@ def test_reference_routes_seeded_random_calls(device):
             out, ws = host(o), host(w)
         np.testing.assert_allclose(out, exp_out, atol=ATOL, rtol=RTOL, err_msg=f"case {case}")
         np.testing.assert_allclose(ws, exp_ws, atol=PROB_ATOL, rtol=0, err_msg=f"case {case}")
+
+
+def test_reference_routes_from_four_host_threads_on_their_own_streams(device):
+    """Four host threads, each issuing decode and chunk calls of changing
+    sizes on its own stream: every stream gets its own route scratch
+    (grown as its calls grow), so the calls never share partials and all
+    results match the oracle."""
+    import threading
+
+    cases = []
+    for i in range(8):
+        T = [1, 40, 1, 3][i % 4]
+        hist = [900, 300, 4000, 17][i % 4] + 13 * i
+        table, kp, vp, q, tk, tv = chunk_problem(8800 + i, 8, 4, hist, T)
+        exp_out, exp_ws = oracle.paged_attention(q, kp, vp, table, hist, tk, tv)
+        args = (dev(q), dev(kp), dev(vp), dev(table.astype(np.int32)), hist, dev(tk), dev(tv))
+        cases.append((args, hist, T, exp_out, exp_ws))
+    torch.cuda.synchronize()
+    results = {}
+    errors = []
+
+    def worker(w):
+        try:
+            stream = torch.cuda.Stream()
+            outs = []
+            with torch.cuda.stream(stream):
+                for rep in range(3):
+                    for i in range(w, len(cases) + w):
+                        args, hist, T, _, _ = cases[i % len(cases)]
+                        o = torch.empty(32, T, 128, device="cuda:0")
+                        s = torch.empty(32, T, hist + T, device="cuda:0")
+                        hx.paged_attention_with_tail_out(*args, o, s, stream=stream)
+                        outs.append((i % len(cases), o, s))
+            stream.synchronize()
+            results[w] = outs
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(w,)) for w in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert errors == []
+    for w, outs in results.items():
+        for i, o, s in outs:
+            _, _, _, exp_out, exp_ws = cases[i]
+            np.testing.assert_allclose(host(o), exp_out, atol=ATOL, rtol=RTOL,
+                                       err_msg=f"thread {w} case {i}")
+            np.testing.assert_allclose(host(s), exp_ws, atol=PROB_ATOL, rtol=0,
+                                       err_msg=f"thread {w} case {i}")
